@@ -1,0 +1,154 @@
+/* sana_dit.h -- C ABI of the MI355X (gfx950) Sana-0.6B DiT forward.
+ *
+ * This is the drop-in boundary under the reference's C++ transformer API
+ * (src/transformer.h:81-155).  Plain pointers and sizes only; no C++ or torch
+ * types.  Host pointers are fp32 in the reference's layouts; *_device entry
+ * points take device pointers and a hipStream_t passed as void*.
+ *
+ * Errors: every entry point returns SANA_OK (0) or a negative code; the
+ * message of the last failure on the calling thread is sana_dit_last_error().
+ * The C++ wrapper maps SANA_ERR_INVALID_ARGUMENT and SANA_ERR_SHAPE to
+ * std::invalid_argument and the others to std::runtime_error, as the
+ * reference throws them (src/transformer.cpp:500-514, :553-555, :574-579,
+ * :613-624; src/weights_io.cpp:138-150, :336-354).
+ *
+ * Threading: a context is used by one host thread at a time; it owns a HIP
+ * stream, the device weights, a workspace and cached HIP graphs.  All device
+ * memory is allocated by create / weight upload / the first call at a new
+ * shape, never inside a captured graph.
+ */
+#ifndef SANA_DIT_H
+#define SANA_DIT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SANA_OK 0
+#define SANA_ERR_INVALID_ARGUMENT (-1)
+#define SANA_ERR_SHAPE (-2)
+#define SANA_ERR_IO (-3)
+#define SANA_ERR_FORMAT (-4)
+#define SANA_ERR_HIP (-5)
+#define SANA_ERR_OUT_OF_MEMORY (-6)
+#define SANA_ERR_STATE (-7)
+
+typedef struct sana_dit sana_dit;
+
+typedef struct {
+    int64_t layers;          /* transformer blocks (28) */
+    int64_t hidden;          /* C (1152) */
+    int64_t ffn;             /* expanded Mix-FFN channels E (5760 = 2 x 2880) */
+    int64_t caption_dim;     /* caption feature width (2304) */
+    int64_t latent_channels; /* Cl (32) */
+    int64_t self_heads;      /* linear-attention heads (36 in sana_infer, src/infer_main.cpp:366) */
+    int64_t cross_heads;     /* cross-attention heads (16, src/infer_main.cpp:367) */
+    int device;              /* HIP device ordinal */
+} sana_dit_config;
+
+const char * sana_dit_last_error(void);
+
+/* Replaces the model set-up of load_denoiser_weights (src/transformer.cpp:453-488). */
+int sana_dit_create(const sana_dit_config * cfg, sana_dit ** out);
+void sana_dit_destroy(sana_dit * ctx);
+
+/* Upload one top-level tensor by its GGUF name (src/transformer.cpp:473-484,
+ * :171-190): patch_embed.proj.*, time_embed.*, caption_projection.*,
+ * caption_norm.weight, scale_shift_table, proj_out.*.  `shape` is the
+ * PyTorch-order shape (GGUF ne reversed, src/weights_io.cpp:125-132).
+ * transposed = 1 means a linear weight arrives as [in, out], the layout
+ * load_linear_weight_tensor produces (src/weights_io.cpp:367-377). */
+int sana_dit_set_weight(sana_dit * ctx, const char * name, const float * data, const int64_t * shape, int ndim,
+                        int transposed);
+/* Upload one tensor of block `block` by its suffix after the block prefix
+ * (load_block_weights, src/transformer.cpp:214-308), e.g. "attn1.to_q.weight". */
+int sana_dit_set_block_weight(sana_dit * ctx, int64_t block, const char * suffix, const float * data,
+                              const int64_t * shape, int ndim, int transposed);
+/* Optional LayerNorm affine of a block (which = 0: attn norm, 1: mlp norm).
+ * The reference loader injects gamma = 1, beta = 0 (src/transformer.cpp:364-398),
+ * which is also the default here; NULL restores the default. */
+int sana_dit_set_block_norm(sana_dit * ctx, int64_t block, int which, const float * gamma, const float * beta);
+/* Checks that every tensor has been uploaded (validate_denoiser_weights,
+ * src/transformer.cpp:807-884 checks the shapes; set_* already did). */
+int sana_dit_check_weights(sana_dit * ctx);
+/* Loads the three GGUF files of download_weights.sh (model, caption, denoiser),
+ * F32 tensors only (src/weights_io.cpp:134-164, :325-365). */
+int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * caption_path,
+                       const char * denoiser_path);
+
+/* Conditioning for the following forwards.  projected = 0: data is the raw
+ * caption [B, L, caption_dim] and the caption projection
+ * (project_caption_context, src/transformer_ops.cpp:64-76) runs on the GPU;
+ * projected = 1: data is the context [B, L, hidden].  bias is the additive
+ * key mask [B, 1, L] (or NULL).  The cross-attention keys/values of all
+ * blocks are computed here once, since they depend only on the context. */
+int sana_dit_set_context(sana_dit * ctx, const float * data, int64_t B, int64_t L, int64_t dim, int projected,
+                         const float * bias);
+/* Copy the projected context [B, L, hidden] (fp32 before the fp16 operand cast). */
+int sana_dit_get_context(sana_dit * ctx, float * out);
+
+/* The forward of run_full_denoising_step_with_cfg (src/transformer.cpp:627-681):
+ * latent [Bl, Cl, H, W] (repeated x2 for CFG), timestep t for every batch row,
+ * the context set above (batch 2*Bl) -> noise_pred [2*Bl, Cl, H, W].  H == W. */
+int sana_dit_forward(sana_dit * ctx, const float * latent, int64_t Bl, int64_t H, int64_t W, float t,
+                     float * noise_pred);
+/* Same with device pointers, asynchronous on `stream` (NULL = the context's stream). */
+int sana_dit_forward_device(sana_dit * ctx, const float * d_latent, int64_t Bl, int64_t H, int64_t W, float t,
+                            float * d_noise_pred, void * stream);
+/* One whole step from raw inputs on the device: caption projection of
+ * d_caption [2*Bl, L, caption_dim], cross K/V of all blocks, and the forward.
+ * d_bias [2*Bl, L] or NULL.  Asynchronous on `stream`. */
+int sana_dit_step_device(sana_dit * ctx, const float * d_caption, int64_t L, const float * d_bias,
+                         const float * d_latent, int64_t Bl, int64_t H, int64_t W, float t, float * d_noise_pred,
+                         void * stream);
+/* block_forward (src/transformer.cpp:726-778) of one block on the context set
+ * above: x [B, N, C], t_mod [B, 6C] -> the three stage outputs [B, N, C]. */
+int sana_dit_block_forward(sana_dit * ctx, int64_t block, const float * x, const float * t_mod, int64_t B,
+                           int64_t N, float * after_self, float * after_cross, float * after_ff);
+/* Time MLP of the forward (src/transformer.cpp:638-656): B timesteps ->
+ * embedded [B, C] (pre-SiLU) and t_mod [B, 6C]. */
+int sana_dit_time_embed(sana_dit * ctx, const float * t, int64_t B, float * embedded, float * t_mod);
+/* Average duration (ms) over `iters` eager launches of one GEMM of block 0 at
+ * the token count of the last forward: which = 0 QKV, 1 attn out, 2 cross q,
+ * 3 cross out, 4 FFN inverted, 5 FFN point.  Also returns its FLOPs. */
+int sana_dit_time_gemm(sana_dit * ctx, int which, int iters, float * avg_ms, double * flops);
+
+/* GGUF index inspection (no GPU needed): number of tensors, and the name,
+ * PyTorch-order shape (up to 4 dims), ggml type and absolute payload offset of
+ * tensor i -- the fields load_gguf_weight_index records (src/weights_io.cpp:152-158). */
+int sana_gguf_num_tensors(const char * path, int64_t * n);
+int sana_gguf_tensor_info(const char * path, int64_t i, char * name, size_t name_cap, int64_t * shape, int * ndim,
+                          int * type, uint64_t * offset);
+
+/* ---- kernel-level launchers on device pointers (unit tests, op-level API) ---- */
+/* out = act(A . W^T + bias): A fp16 [M, lda], W fp16 [N, ldw], K % 64 == 0. */
+int sana_hip_gemm(const void * A, int64_t lda, const void * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                  const float * bias, int act, void * out16, int64_t ldo16, float * out32, int64_t ldo32,
+                  void * stream);
+/* x[m, n] += gate(m, n) * (A . W^T + bias)[m, n]; gate = gate_a[(m / rows_per_batch) * gate_stride + n]
+ * + gate_t[n] (gate_a NULL: gate 1); optional fp16 copy of the new x. */
+int sana_hip_gemm_residual(const void * A, int64_t lda, const void * W, int64_t ldw, int64_t M, int64_t N,
+                           int64_t K, const float * bias, const float * gate_a, const float * gate_t,
+                           int64_t gate_stride, int64_t rows_per_batch, float * x, int64_t ldx, void * out16,
+                           int64_t ldo16, void * stream);
+int sana_hip_ln_modulate(const float * x, int64_t ldx, void * out16, int64_t ldo, int64_t M, int64_t C,
+                         int64_t rows_per_batch, float eps, const float * gamma, const float * beta,
+                         const float * mod_a, const float * mod_t, int64_t mod_stride, int64_t shift_off,
+                         int64_t scale_off, void * stream);
+int sana_hip_linear_attention(const void * q, const void * k, const void * v, int64_t ld, void * out, int64_t ldo,
+                              int64_t B, int64_t N, int64_t H, int64_t D, float * workspace, void * stream);
+size_t sana_hip_linear_attention_workspace(int64_t B, int64_t N, int64_t H, int64_t D);
+int sana_hip_cross_attention(const void * q, int64_t ldq, const void * k, int64_t ldk, const void * vt,
+                             int64_t ldvt, const float * bias, void * out, int64_t ldo, int64_t B, int64_t N,
+                             int64_t L, int64_t H, int64_t D, void * stream);
+int sana_hip_dwconv_glu(const void * x, int64_t ldx, const float * w_tapmajor, const float * bias, void * out,
+                        int64_t ldo, int64_t B, int64_t H, int64_t W, int64_t F, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SANA_DIT_H */

@@ -1,0 +1,986 @@
+// Device model and C ABI of the Sana DiT forward on one MI355X.
+//
+// HBM layout (all device-resident after upload):
+//   weights   fp16 [out, in] rows padded to a multiple of 64 in K (zeros), the
+//             MFMA "TN" operand; attn1 q|k|v fused into one [3C, C] matrix;
+//             attn2 k / v of all blocks stacked into [layers*C, C] each so the
+//             step-invariant cross K/V of the whole model is two large GEMMs;
+//             biases, adaLN tables, depthwise taps (tap-major [9][E]) and the
+//             small time/patch/proj_out weights in fp32.
+//   residual  fp32 [B*N, C] (token-major, the reference's [B, N, C]); every
+//             GEMM A operand is an fp16 token-major copy with padded row stride.
+//   context   fp16 [B*L, C]; cross K fp16 [B*L, layers*C]; cross V^T fp16
+//             [layers][B][C][Lp] (keys contiguous for the P.V MFMA operand).
+// No layout transposes remain: tokens_to_grid/grid_to_tokens/split_heads/
+// merge_heads of the reference are address arithmetic here, and the CFG
+// batch repeat is two batch rows reading the same latent.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "../../include/sana_dit.h"
+#include "kernels.h"
+
+using sana::half_t;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int set_err(int code, const char * fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+struct SanaError {
+    int code;
+    std::string msg;
+};
+
+[[noreturn]] void throw_err(int code, const std::string & m) { throw SanaError{code, m}; }
+
+void hip_check(hipError_t e, const char * what) {
+    if (e != hipSuccess) {
+        throw_err(e == hipErrorOutOfMemory ? SANA_ERR_OUT_OF_MEMORY : SANA_ERR_HIP,
+                  std::string(what) + ": " + hipGetErrorString(e));
+    }
+}
+
+void launch_check(hipError_t e, const char * what) {
+    if (e == hipErrorInvalidValue) throw_err(SANA_ERR_SHAPE, std::string(what) + ": shape not supported by kernel");
+    hip_check(e, what);
+}
+
+int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Device allocation owned by the context.
+struct DevMem {
+    void * p = nullptr;
+    size_t bytes = 0;
+    DevMem() = default;
+    DevMem(const DevMem &) = delete;
+    DevMem & operator=(const DevMem &) = delete;
+    ~DevMem() {
+        if (p) (void)hipFree(p);
+    }
+    void ensure(size_t n, bool zero = true) {
+        if (n <= bytes && p) return;
+        if (p) hip_check(hipFree(p), "hipFree");
+        p = nullptr;
+        bytes = 0;
+        hip_check(hipMalloc(&p, n ? n : 16), "hipMalloc");
+        bytes = n;
+        if (zero) hip_check(hipMemset(p, 0, n), "hipMemset");
+    }
+    template <class T>
+    T * as() const {
+        return static_cast<T *>(p);
+    }
+};
+
+struct BlockDev {
+    DevMem sst, w_qkv, w_out, b_out, w_cq, b_cq, w_co, b_co, w_inv, b_inv, w_dw, b_dw, w_pt;
+    DevMem ln1_g, ln1_b, ln2_g, ln2_b;
+    bool has_ln1 = false, has_ln2 = false;
+};
+
+__global__ void fill_kernel(float * p, int n, float v) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+struct GraphEntry {
+    hipGraphExec_t exec = nullptr;
+};
+
+}  // namespace
+
+namespace sana {
+void set_last_error(const std::string & m) { g_last_error = m; }
+}  // namespace sana
+
+struct sana_dit {
+    sana_dit_config cfg{};
+    int64_t C = 0, E = 0, F = 0, Ccap = 0, Cl = 0, L_ = 0, Hs = 0, Hc = 0, Ds = 0, Dc = 0;
+    int64_t Cp = 0, Fp = 0, Ccap_p = 0;  // K-padded row strides of GEMM operands
+    hipStream_t stream = nullptr;
+    std::vector<std::unique_ptr<BlockDev>> blocks;
+    DevMem w_k_all, b_k_all, w_v_all, b_v_all;
+    DevMem w_cap1, b_cap1, w_cap2, b_cap2, cap_norm;
+    DevMem w_patch_t, b_patch, w_t1, b_t1, w_t2, b_t2, w_tp, b_tp, sst_final, w_proj, b_proj, freq;
+    std::map<std::string, int> have;  // uploaded tensor names
+    // context
+    int64_t ctx_B = 0, ctx_L = 0, ctx_Lp = 0;
+    bool ctx_ready = false, ctx_bias = false;
+    DevMem cap32, cap16, caph16, capf32, ctx32, ctx16, kc, vt, bias;
+    // forward workspace
+    int64_t ws_M = 0, ws_B = 0;
+    DevMem x32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, d_t, tp, e1, emb, tmod, lat_in, np_out;
+    // graphs keyed by (kind, Bl, H, W, L, pointers)
+    std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, const void *, const void *, const void *, const void *>,
+             GraphEntry>
+        graphs;
+    int64_t last_M = 0, last_B = 0, last_N = 0;
+
+    ~sana_dit() {
+        for (auto & kv : graphs)
+            if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+void drop_graphs(sana_dit * c) {
+    for (auto & kv : c->graphs)
+        if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+    c->graphs.clear();
+}
+
+// Host fp32 -> device fp16 [rows, ld] with zero padding; src is [rows, cols]
+// (or [cols, rows] when transposed).
+void upload_f16(DevMem & dst, const float * src, int64_t rows, int64_t cols, int64_t ld, bool transposed,
+                int64_t row_offset = 0, int64_t total_rows = -1) {
+    if (total_rows < 0) total_rows = rows;
+    std::vector<half_t> h((size_t)rows * ld, (half_t)0.0f);
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+            h[(size_t)r * ld + c] = (half_t)(transposed ? src[c * rows + r] : src[r * cols + c]);
+    if (!dst.p) dst.ensure((size_t)total_rows * ld * sizeof(half_t));
+    hip_check(hipMemcpy(dst.as<half_t>() + (size_t)row_offset * ld, h.data(), h.size() * sizeof(half_t),
+                        hipMemcpyHostToDevice),
+              "upload");
+}
+
+void upload_f32(DevMem & dst, const float * src, size_t n, size_t offset = 0, size_t total = 0) {
+    if (!dst.p) dst.ensure((total ? total : n) * sizeof(float));
+    hip_check(hipMemcpy(dst.as<float>() + offset, src, n * sizeof(float), hipMemcpyHostToDevice), "upload");
+}
+
+void upload_f32_transposed(DevMem & dst, const float * src, int64_t rows, int64_t cols, bool src_transposed) {
+    // dst = [rows, cols] row-major where src is [rows, cols] (or [cols, rows] if src_transposed)
+    std::vector<float> h((size_t)rows * cols);
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) h[(size_t)r * cols + c] = src_transposed ? src[c * rows + r] : src[r * cols + c];
+    upload_f32(dst, h.data(), h.size());
+}
+
+void expect_shape(const char * name, const int64_t * shape, int ndim, std::vector<int64_t> want) {
+    bool ok = ndim == (int)want.size();
+    for (int i = 0; ok && i < ndim; ++i) ok = shape[i] == want[i];
+    if (!ok) {
+        std::string got, exp;
+        for (int i = 0; i < ndim; ++i) got += (i ? "," : "") + std::to_string(shape[i]);
+        for (size_t i = 0; i < want.size(); ++i) exp += (i ? "," : "") + std::to_string(want[i]);
+        throw_err(SANA_ERR_SHAPE, std::string(name) + ": shape [" + got + "] expected [" + exp + "]");
+    }
+}
+
+// ---------------------------------------------------------------- forward pieces
+void gemm_store(sana_dit * c, const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N,
+                int64_t K, const float * bias, int act, half_t * o16, int64_t ldo16, float * o32, int64_t ldo32,
+                hipStream_t s) {
+    sana::GemmParams p;
+    p.A = A;
+    p.lda = lda;
+    p.W = W;
+    p.ldw = ldw;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.bias = bias;
+    p.mode = sana::kGemmStore;
+    p.act = act;
+    p.out16 = o16;
+    p.ldo16 = ldo16;
+    p.out32 = o32;
+    p.ldo32 = ldo32;
+    (void)c;
+    launch_check(sana::gemm(p, s), "gemm");
+}
+
+void gemm_resid(const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                const float * bias, const float * gate_a, const float * gate_t, int64_t gate_stride, int64_t rpb,
+                float * x, int64_t ldx, half_t * o16, int64_t ldo16, hipStream_t s) {
+    sana::GemmParams p;
+    p.A = A;
+    p.lda = lda;
+    p.W = W;
+    p.ldw = ldw;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.bias = bias;
+    p.mode = sana::kGemmResidual;
+    p.gate_a = gate_a;
+    p.gate_t = gate_t;
+    p.gate_stride = gate_stride;
+    p.rows_per_batch = (int)rpb;
+    p.out32 = x;
+    p.ldo32 = ldx;
+    p.out16 = o16;
+    p.ldo16 = ldo16;
+    launch_check(sana::gemm(p, s), "gemm_residual");
+}
+
+void ensure_context_buffers(sana_dit * c, int64_t B, int64_t L) {
+    const int64_t Lp = round_up(L, 32);
+    if (B * L > c->ctx_B * c->ctx_L || Lp > c->ctx_Lp || B != c->ctx_B) {
+        drop_graphs(c);
+        c->cap32.ensure((size_t)B * L * c->Ccap * 4);
+        c->cap16.ensure((size_t)B * L * c->Ccap_p * 2);
+        c->caph16.ensure((size_t)B * L * c->Cp * 2);
+        c->capf32.ensure((size_t)B * L * c->C * 4);
+        c->ctx32.ensure((size_t)B * L * c->C * 4);
+        c->ctx16.ensure((size_t)B * L * c->Cp * 2);
+        c->kc.ensure((size_t)B * L * c->L_ * c->C * 2);
+        c->vt.ensure((size_t)c->L_ * B * c->C * Lp * 2);  // zero: key padding must read as 0
+        c->bias.ensure((size_t)B * L * 4);
+        c->ctx_Lp = Lp;
+    }
+    c->ctx_B = B;
+    c->ctx_L = L;
+}
+
+// Caption projection (optional) + cross K/V of all blocks, enqueued on s.
+void enqueue_context(sana_dit * c, const float * caption, bool projected, int64_t B, int64_t L, hipStream_t s) {
+    const int64_t R = B * L, C = c->C;
+    if (!projected) {
+        launch_check(sana::to_f16_padded(caption, (int)R, (int)c->Ccap, c->cap16.as<half_t>(), c->Ccap_p, s), "to_f16");
+        gemm_store(c, c->cap16.as<half_t>(), c->Ccap_p, c->w_cap1.as<half_t>(), c->Ccap_p, R, C, c->Ccap_p,
+                   c->b_cap1.as<float>(), sana::kActGelu, c->caph16.as<half_t>(), c->Cp, nullptr, 0, s);
+        gemm_store(c, c->caph16.as<half_t>(), c->Cp, c->w_cap2.as<half_t>(), c->Cp, R, C, c->Cp, c->b_cap2.as<float>(),
+                   sana::kActNone, nullptr, 0, c->capf32.as<float>(), C, s);
+        launch_check(sana::rms_norm_f16(c->capf32.as<float>(), C, c->cap_norm.as<float>(), c->ctx16.as<half_t>(),
+                                        c->Cp, c->ctx32.as<float>(), (int)R, (int)C, 1e-5f, s),
+                     "rms_norm");
+    } else {
+        launch_check(sana::to_f16_padded(caption, (int)R, (int)C, c->ctx16.as<half_t>(), c->Cp, s), "to_f16");
+    }
+    // K of all blocks: [B*L, layers*C]
+    gemm_store(c, c->ctx16.as<half_t>(), c->Cp, c->w_k_all.as<half_t>(), c->Cp, R, c->L_ * C, c->Cp,
+               c->b_k_all.as<float>(), sana::kActNone, c->kc.as<half_t>(), c->L_ * C, nullptr, 0, s);
+    // V^T of all blocks: rows (blk, channel), columns (b, key)
+    sana::GemmParams p;
+    p.A = c->w_v_all.as<half_t>();
+    p.lda = c->Cp;
+    p.W = c->ctx16.as<half_t>();
+    p.ldw = c->Cp;
+    p.M = (int)(c->L_ * C);
+    p.N = (int)R;
+    p.K = (int)c->Cp;
+    p.bias = c->b_v_all.as<float>();
+    p.mode = sana::kGemmVT;
+    p.out16 = c->vt.as<half_t>();
+    p.vt_rows = (int)C;
+    p.vt_cols = (int)L;
+    p.vt_batch = (int)B;
+    p.vt_ld = c->ctx_Lp;
+    launch_check(sana::gemm(p, s), "gemm_vt");
+}
+
+void ensure_forward_buffers(sana_dit * c, int64_t B, int64_t N) {
+    const int64_t M = B * N;
+    if (M > c->ws_M || B > c->ws_B) {
+        drop_graphs(c);
+        const int64_t C = c->C;
+        c->x32.ensure((size_t)M * C * 4);
+        c->xa16.ensure((size_t)M * c->Cp * 2);
+        c->qkv16.ensure((size_t)M * 3 * C * 2);
+        c->o16.ensure((size_t)M * c->Cp * 2);
+        c->r16.ensure((size_t)M * c->Cp * 2);
+        c->q16.ensure((size_t)M * C * 2);
+        c->hid16.ensure((size_t)M * c->E * 2);
+        c->glu16.ensure((size_t)M * c->Fp * 2);
+        c->la_ws.ensure(sana::linattn_workspace_floats((int)B, (int)N, (int)c->Hs, (int)c->Ds) * 4);
+        c->d_t.ensure((size_t)B * 4);
+        c->tp.ensure((size_t)B * 256 * 4);
+        c->e1.ensure((size_t)B * C * 4);
+        c->emb.ensure((size_t)B * C * 4);
+        c->tmod.ensure((size_t)B * 6 * C * 4);
+        c->lat_in.ensure((size_t)B * c->Cl * N * 4);
+        c->np_out.ensure((size_t)B * c->Cl * N * 4);
+        c->ws_M = M;
+        c->ws_B = B;
+    }
+}
+
+void enqueue_time(sana_dit * c, int64_t B, hipStream_t s) {
+    const int64_t C = c->C;
+    launch_check(sana::timestep_sinusoid(c->d_t.as<float>(), c->freq.as<float>(), (int)B, 128, c->tp.as<float>(), s),
+                 "sinusoid");
+    launch_check(sana::gemv_f32(c->tp.as<float>(), c->w_t1.as<float>(), c->b_t1.as<float>(), c->e1.as<float>(), (int)B,
+                                256, (int)C, 0, s),
+                 "time linear_1");
+    launch_check(sana::gemv_f32(c->e1.as<float>(), c->w_t2.as<float>(), c->b_t2.as<float>(), c->emb.as<float>(),
+                                (int)B, (int)C, (int)C, 1, s),
+                 "time linear_2");
+    launch_check(sana::gemv_f32(c->emb.as<float>(), c->w_tp.as<float>(), c->b_tp.as<float>(), c->tmod.as<float>(),
+                                (int)B, (int)C, (int)(6 * C), 1, s),
+                 "time projection");
+}
+
+// Stage hook: called after each stage of a block (0 self, 1 cross, 2 ff).
+typedef void (*StageHook)(void *, int);
+
+void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * xbias, hipStream_t s,
+                   StageHook hook = nullptr, void * hook_ctx = nullptr) {
+    BlockDev & w = *c->blocks[i];
+    const int64_t C = c->C, M = B * N, side = (int64_t)std::llround(std::sqrt((double)N));
+    const float * tmod = c->tmod.as<float>();
+    const float * sst = w.sst.as<float>();
+    // self attention: LN + modulate(shift_msa, scale_msa)
+    launch_check(sana::ln_modulate(c->x32.as<float>(), C, c->xa16.as<half_t>(), c->Cp, (int)M, (int)C, (int)N, 1e-6f,
+                                   w.has_ln1 ? w.ln1_g.as<float>() : nullptr, w.has_ln1 ? w.ln1_b.as<float>() : nullptr,
+                                   tmod, sst, 6 * C, 0, C, s),
+                 "ln_modulate");
+    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp, nullptr, sana::kActNone,
+               c->qkv16.as<half_t>(), 3 * C, nullptr, 0, s);
+    const half_t * qkv = c->qkv16.as<half_t>();
+    launch_check(sana::linear_attention(qkv, qkv + C, qkv + 2 * C, 3 * C, c->o16.as<half_t>(), c->Cp, (int)B, (int)N,
+                                        (int)c->Hs, (int)c->Ds, c->la_ws.as<float>(), s),
+                 "linear_attention");
+    // x += gate_msa * (o Wo^T + bo); r16 = fp16(x) for the cross-attention query
+    gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_out.as<half_t>(), c->Cp, M, C, c->Cp, w.b_out.as<float>(),
+               tmod + 2 * C, sst + 2 * C, 6 * C, N, c->x32.as<float>(), C, c->r16.as<half_t>(), c->Cp, s);
+    if (hook) hook(hook_ctx, 0);
+    // cross attention
+    gemm_store(c, c->r16.as<half_t>(), c->Cp, w.w_cq.as<half_t>(), c->Cp, M, C, c->Cp, w.b_cq.as<float>(),
+               sana::kActNone, c->q16.as<half_t>(), C, nullptr, 0, s);
+    const half_t * kc = c->kc.as<half_t>() + i * C;
+    const half_t * vt = c->vt.as<half_t>() + (size_t)i * B * C * c->ctx_Lp;
+    launch_check(sana::cross_attention(c->q16.as<half_t>(), C, kc, c->L_ * C, vt, c->ctx_Lp,
+                                       xbias, c->o16.as<half_t>(), c->Cp, (int)B,
+                                       (int)N, (int)c->ctx_L, (int)c->Hc, (int)c->Dc, s),
+                 "cross_attention");
+    gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_co.as<half_t>(), c->Cp, M, C, c->Cp, w.b_co.as<float>(), nullptr,
+               nullptr, 0, N, c->x32.as<float>(), C, nullptr, 0, s);
+    if (hook) hook(hook_ctx, 1);
+    // Mix-FFN
+    launch_check(sana::ln_modulate(c->x32.as<float>(), C, c->xa16.as<half_t>(), c->Cp, (int)M, (int)C, (int)N, 1e-6f,
+                                   w.has_ln2 ? w.ln2_g.as<float>() : nullptr, w.has_ln2 ? w.ln2_b.as<float>() : nullptr,
+                                   tmod, sst, 6 * C, 3 * C, 4 * C, s),
+                 "ln_modulate");
+    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_inv.as<half_t>(), c->Cp, M, c->E, c->Cp, w.b_inv.as<float>(),
+               sana::kActSilu, c->hid16.as<half_t>(), c->E, nullptr, 0, s);
+    launch_check(sana::dwconv_glu(c->hid16.as<half_t>(), c->E, w.w_dw.as<float>(), w.b_dw.as<float>(),
+                                  c->glu16.as<half_t>(), c->Fp, (int)B, (int)side, (int)side, (int)c->F, s),
+                 "dwconv_glu");
+    gemm_resid(c->glu16.as<half_t>(), c->Fp, w.w_pt.as<half_t>(), c->Fp, M, C, c->Fp, nullptr, tmod + 5 * C,
+               sst + 5 * C, 6 * C, N, c->x32.as<float>(), C, nullptr, 0, s);
+    if (hook) hook(hook_ctx, 2);
+}
+
+void enqueue_forward(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh, int64_t Ww, const float * xbias,
+                     float * out, hipStream_t s) {
+    const int64_t B = 2 * Bl, N = Hh * Ww;
+    launch_check(sana::patch_embed(latent, (int)Bl, (int)B, (int)c->Cl, (int)N, c->w_patch_t.as<float>(),
+                                   c->b_patch.as<float>(), c->x32.as<float>(), (int)c->C, s),
+                 "patch_embed");
+    enqueue_time(c, B, s);
+    for (int64_t i = 0; i < c->L_; ++i) enqueue_block(c, i, B, N, xbias, s);
+    launch_check(sana::final_layer(c->x32.as<float>(), c->emb.as<float>(), c->sst_final.as<float>(),
+                                   c->w_proj.as<float>(), c->b_proj.as<float>(), out, (int)B, (int)N, (int)c->C,
+                                   (int)c->Cl, 1e-6f, s),
+                 "final_layer");
+}
+
+void check_ready(sana_dit * c) {
+    const size_t want = 12 + 4 + (size_t)c->L_ * 19;
+    if (c->have.size() != want) {
+        // name the first missing tensor
+        static const char * top[] = {"patch_embed.proj.weight", "patch_embed.proj.bias",
+                                     "time_embed.emb.timestep_embedder.linear_1.weight",
+                                     "time_embed.emb.timestep_embedder.linear_1.bias",
+                                     "time_embed.emb.timestep_embedder.linear_2.weight",
+                                     "time_embed.emb.timestep_embedder.linear_2.bias", "time_embed.linear.weight",
+                                     "time_embed.linear.bias", "caption_norm.weight", "scale_shift_table",
+                                     "proj_out.weight", "proj_out.bias", "caption_projection.linear_1.weight",
+                                     "caption_projection.linear_1.bias", "caption_projection.linear_2.weight",
+                                     "caption_projection.linear_2.bias"};
+        for (const char * n : top)
+            if (!c->have.count(n)) throw_err(SANA_ERR_STATE, std::string("weight not uploaded: ") + n);
+        throw_err(SANA_ERR_STATE, "block weights incomplete (" + std::to_string(c->have.size()) + " of " +
+                                      std::to_string(want) + " tensors uploaded)");
+    }
+}
+
+void set_t(sana_dit * c, int64_t B, float t, hipStream_t s) {
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((B + 63) / 64)), dim3(64), 0, s, c->d_t.as<float>(), (int)B, t);
+    hip_check(hipGetLastError(), "fill");
+}
+
+bool graphs_enabled() {
+    const char * e = std::getenv("SANA_DIT_NO_GRAPH");
+    return !(e && e[0] == '1');
+}
+
+// Run `body` on stream s through a cached HIP graph (captured on the context
+// stream on first use for this key).
+template <class Body>
+void run_graph(sana_dit * c,
+               const std::tuple<int, int64_t, int64_t, int64_t, int64_t, const void *, const void *, const void *,
+                                const void *> & key,
+               hipStream_t s, Body body) {
+    if (!graphs_enabled()) {
+        body(s);
+        return;
+    }
+    auto it = c->graphs.find(key);
+    if (it == c->graphs.end()) {
+        hipGraph_t g = nullptr;
+        hip_check(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            body(c->stream);
+        } catch (...) {
+            (void)hipStreamEndCapture(c->stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        hip_check(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
+        GraphEntry e;
+        hipError_t r = hipGraphInstantiate(&e.exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        hip_check(r, "hipGraphInstantiate");
+        it = c->graphs.emplace(key, e).first;
+    }
+    hip_check(hipGraphLaunch(it->second.exec, s), "hipGraphLaunch");
+}
+
+template <class F>
+int guarded(F f) {
+    try {
+        f();
+        return SANA_OK;
+    } catch (const SanaError & e) {
+        g_last_error = e.msg;
+        return e.code;
+    } catch (const std::bad_alloc &) {
+        return set_err(SANA_ERR_OUT_OF_MEMORY, "host allocation failed");
+    } catch (const std::exception & e) {
+        return set_err(SANA_ERR_HIP, "%s", e.what());
+    }
+}
+
+struct BlockSuffix {
+    const char * name;
+    int kind;
+};
+
+}  // namespace
+
+extern "C" {
+
+const char * sana_dit_last_error(void) { return g_last_error.c_str(); }
+
+int sana_dit_create(const sana_dit_config * cfg, sana_dit ** out) {
+    if (!cfg || !out) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (cfg->layers <= 0 || cfg->hidden <= 0 || cfg->ffn <= 0 || cfg->ffn % 2 || cfg->caption_dim <= 0 ||
+        cfg->latent_channels <= 0 || cfg->self_heads <= 0 || cfg->cross_heads <= 0)
+        return set_err(SANA_ERR_INVALID_ARGUMENT, "config dimensions must be positive (ffn even)");
+    if (cfg->hidden % cfg->self_heads != 0)
+        return set_err(SANA_ERR_INVALID_ARGUMENT, "self attention hidden size must be divisible by self_num_heads");
+    if (cfg->hidden % cfg->cross_heads != 0)
+        return set_err(SANA_ERR_INVALID_ARGUMENT, "cross attention hidden size must be divisible by cross_num_heads");
+    if (cfg->hidden > 2048) return set_err(SANA_ERR_INVALID_ARGUMENT, "hidden > 2048 not supported");
+    if (cfg->hidden / cfg->self_heads > 100) return set_err(SANA_ERR_INVALID_ARGUMENT, "self head_dim > 100");
+    if (cfg->hidden / cfg->cross_heads > 256) return set_err(SANA_ERR_INVALID_ARGUMENT, "cross head_dim > 256");
+    auto c = std::make_unique<sana_dit>();
+    int rc = guarded([&] {
+        c->cfg = *cfg;
+        c->C = cfg->hidden;
+        c->E = cfg->ffn;
+        c->F = cfg->ffn / 2;
+        c->Ccap = cfg->caption_dim;
+        c->Cl = cfg->latent_channels;
+        c->L_ = cfg->layers;
+        c->Hs = cfg->self_heads;
+        c->Hc = cfg->cross_heads;
+        c->Ds = c->C / c->Hs;
+        c->Dc = c->C / c->Hc;
+        c->Cp = round_up(c->C, 64);
+        c->Fp = round_up(c->F, 64);
+        c->Ccap_p = round_up(c->Ccap, 64);
+        hip_check(hipSetDevice(cfg->device), "hipSetDevice");
+        hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+        for (int64_t i = 0; i < c->L_; ++i) c->blocks.emplace_back(new BlockDev());
+        // sinusoid frequencies exactly as the reference computes them in fp32
+        // (src/transformer.cpp:89,97-99)
+        std::vector<float> f(128);
+        const float ls = -std::log(10000.0f) / 128.0f;
+        for (int i = 0; i < 128; ++i) f[i] = std::exp(static_cast<float>(i) * ls);
+        upload_f32(c->freq, f.data(), 128);
+        const int64_t C = c->C;
+        c->w_k_all.ensure((size_t)c->L_ * C * c->Cp * 2);
+        c->w_v_all.ensure((size_t)c->L_ * C * c->Cp * 2);
+        c->b_k_all.ensure((size_t)c->L_ * C * 4);
+        c->b_v_all.ensure((size_t)c->L_ * C * 4);
+    });
+    if (rc != SANA_OK) return rc;
+    *out = c.release();
+    return SANA_OK;
+}
+
+void sana_dit_destroy(sana_dit * c) { delete c; }
+
+int sana_dit_set_weight(sana_dit * c, const char * name, const float * data, const int64_t * shape, int ndim,
+                        int transposed) {
+    if (!c || !name || !data || !shape) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] {
+        const std::string n = name;
+        const int64_t C = c->C, Cl = c->Cl, Ccap = c->Ccap;
+        const bool tr = transposed != 0;
+        if (n == "patch_embed.proj.weight") {
+            expect_shape(name, shape, ndim, {C, Cl, 1, 1});
+            upload_f32_transposed(c->w_patch_t, data, Cl, C, true);  // -> [Cl, C]
+        } else if (n == "patch_embed.proj.bias") {
+            expect_shape(name, shape, ndim, {C});
+            upload_f32(c->b_patch, data, C);
+        } else if (n == "time_embed.emb.timestep_embedder.linear_1.weight") {
+            expect_shape(name, shape, ndim, tr ? std::vector<int64_t>{256, C} : std::vector<int64_t>{C, 256});
+            upload_f32_transposed(c->w_t1, data, C, 256, tr);
+        } else if (n == "time_embed.emb.timestep_embedder.linear_1.bias") {
+            expect_shape(name, shape, ndim, {C});
+            upload_f32(c->b_t1, data, C);
+        } else if (n == "time_embed.emb.timestep_embedder.linear_2.weight") {
+            expect_shape(name, shape, ndim, {C, C});
+            upload_f32_transposed(c->w_t2, data, C, C, tr);
+        } else if (n == "time_embed.emb.timestep_embedder.linear_2.bias") {
+            expect_shape(name, shape, ndim, {C});
+            upload_f32(c->b_t2, data, C);
+        } else if (n == "time_embed.linear.weight") {
+            expect_shape(name, shape, ndim, tr ? std::vector<int64_t>{C, 6 * C} : std::vector<int64_t>{6 * C, C});
+            upload_f32_transposed(c->w_tp, data, 6 * C, C, tr);
+        } else if (n == "time_embed.linear.bias") {
+            expect_shape(name, shape, ndim, {6 * C});
+            upload_f32(c->b_tp, data, 6 * C);
+        } else if (n == "caption_norm.weight") {
+            expect_shape(name, shape, ndim, {C});
+            upload_f32(c->cap_norm, data, C);
+        } else if (n == "scale_shift_table") {
+            expect_shape(name, shape, ndim, {2, C});
+            upload_f32(c->sst_final, data, 2 * C);
+        } else if (n == "proj_out.weight") {
+            expect_shape(name, shape, ndim, tr ? std::vector<int64_t>{C, Cl} : std::vector<int64_t>{Cl, C});
+            upload_f32_transposed(c->w_proj, data, Cl, C, tr);
+        } else if (n == "proj_out.bias") {
+            expect_shape(name, shape, ndim, {Cl});
+            upload_f32(c->b_proj, data, Cl);
+        } else if (n == "caption_projection.linear_1.weight") {
+            expect_shape(name, shape, ndim, tr ? std::vector<int64_t>{Ccap, C} : std::vector<int64_t>{C, Ccap});
+            upload_f16(c->w_cap1, data, C, Ccap, c->Ccap_p, tr);
+        } else if (n == "caption_projection.linear_1.bias") {
+            expect_shape(name, shape, ndim, {C});
+            upload_f32(c->b_cap1, data, C);
+        } else if (n == "caption_projection.linear_2.weight") {
+            expect_shape(name, shape, ndim, {C, C});
+            upload_f16(c->w_cap2, data, C, C, c->Cp, tr);
+        } else if (n == "caption_projection.linear_2.bias") {
+            expect_shape(name, shape, ndim, {C});
+            upload_f32(c->b_cap2, data, C);
+        } else {
+            throw_err(SANA_ERR_INVALID_ARGUMENT, "unknown weight name: " + n);
+        }
+        c->have[n] = 1;
+        drop_graphs(c);
+    });
+}
+
+int sana_dit_set_block_weight(sana_dit * c, int64_t blk, const char * suffix, const float * data, const int64_t * shape,
+                              int ndim, int transposed) {
+    if (!c || !suffix || !data || !shape) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    if (blk < 0 || blk >= c->L_) return set_err(SANA_ERR_INVALID_ARGUMENT, "block index out of range");
+    return guarded([&] {
+        const std::string s = suffix;
+        BlockDev & w = *c->blocks[blk];
+        const int64_t C = c->C, E = c->E, F = c->F;
+        const bool tr = transposed != 0;
+        auto lin = [&](DevMem & dst, int64_t out_rows, int64_t in_cols, int64_t ld, int64_t row_off, int64_t total) {
+            expect_shape(suffix, shape, ndim,
+                         tr ? std::vector<int64_t>{in_cols, out_rows} : std::vector<int64_t>{out_rows, in_cols});
+            upload_f16(dst, data, out_rows, in_cols, ld, tr, row_off, total);
+        };
+        if (s == "scale_shift_table") {
+            expect_shape(suffix, shape, ndim, {6, C});
+            upload_f32(w.sst, data, 6 * C);
+        } else if (s == "attn1.to_q.weight") {
+            lin(w.w_qkv, C, C, c->Cp, 0, 3 * C);
+        } else if (s == "attn1.to_k.weight") {
+            lin(w.w_qkv, C, C, c->Cp, C, 3 * C);
+        } else if (s == "attn1.to_v.weight") {
+            lin(w.w_qkv, C, C, c->Cp, 2 * C, 3 * C);
+        } else if (s == "attn1.to_out.0.weight") {
+            lin(w.w_out, C, C, c->Cp, 0, C);
+        } else if (s == "attn1.to_out.0.bias") {
+            expect_shape(suffix, shape, ndim, {C});
+            upload_f32(w.b_out, data, C);
+        } else if (s == "attn2.to_q.weight") {
+            lin(w.w_cq, C, C, c->Cp, 0, C);
+        } else if (s == "attn2.to_q.bias") {
+            expect_shape(suffix, shape, ndim, {C});
+            upload_f32(w.b_cq, data, C);
+        } else if (s == "attn2.to_k.weight") {
+            lin(c->w_k_all, C, C, c->Cp, blk * C, c->L_ * C);
+        } else if (s == "attn2.to_k.bias") {
+            expect_shape(suffix, shape, ndim, {C});
+            upload_f32(c->b_k_all, data, C, blk * C, c->L_ * C);
+        } else if (s == "attn2.to_v.weight") {
+            lin(c->w_v_all, C, C, c->Cp, blk * C, c->L_ * C);
+        } else if (s == "attn2.to_v.bias") {
+            expect_shape(suffix, shape, ndim, {C});
+            upload_f32(c->b_v_all, data, C, blk * C, c->L_ * C);
+        } else if (s == "attn2.to_out.0.weight") {
+            lin(w.w_co, C, C, c->Cp, 0, C);
+        } else if (s == "attn2.to_out.0.bias") {
+            expect_shape(suffix, shape, ndim, {C});
+            upload_f32(w.b_co, data, C);
+        } else if (s == "ff.conv_inverted.weight") {
+            expect_shape(suffix, shape, ndim, {E, C, 1, 1});
+            upload_f16(w.w_inv, data, E, C, c->Cp, false);
+        } else if (s == "ff.conv_inverted.bias") {
+            expect_shape(suffix, shape, ndim, {E});
+            upload_f32(w.b_inv, data, E);
+        } else if (s == "ff.conv_depth.weight") {
+            expect_shape(suffix, shape, ndim, {E, 1, 3, 3});
+            std::vector<float> t((size_t)9 * E);
+            for (int64_t e = 0; e < E; ++e)
+                for (int k = 0; k < 9; ++k) t[(size_t)k * E + e] = data[e * 9 + k];
+            upload_f32(w.w_dw, t.data(), t.size());
+        } else if (s == "ff.conv_depth.bias") {
+            expect_shape(suffix, shape, ndim, {E});
+            upload_f32(w.b_dw, data, E);
+        } else if (s == "ff.conv_point.weight") {
+            expect_shape(suffix, shape, ndim, {C, F, 1, 1});
+            upload_f16(w.w_pt, data, C, F, c->Fp, false);
+        } else {
+            throw_err(SANA_ERR_INVALID_ARGUMENT, "unknown block weight suffix: " + s);
+        }
+        c->have["blk" + std::to_string(blk) + "." + s] = 1;
+        drop_graphs(c);
+    });
+}
+
+int sana_dit_set_block_norm(sana_dit * c, int64_t blk, int which, const float * gamma, const float * beta) {
+    if (!c) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    if (blk < 0 || blk >= c->L_ || (which != 0 && which != 1))
+        return set_err(SANA_ERR_INVALID_ARGUMENT, "bad block or norm index");
+    return guarded([&] {
+        BlockDev & w = *c->blocks[blk];
+        DevMem & g = which == 0 ? w.ln1_g : w.ln2_g;
+        DevMem & b = which == 0 ? w.ln1_b : w.ln2_b;
+        bool & has = which == 0 ? w.has_ln1 : w.has_ln2;
+        if (!gamma && !beta) {
+            has = false;
+        } else {
+            std::vector<float> one(c->C, 1.0f), zero(c->C, 0.0f);
+            upload_f32(g, gamma ? gamma : one.data(), c->C);
+            upload_f32(b, beta ? beta : zero.data(), c->C);
+            has = true;
+        }
+        drop_graphs(c);
+    });
+}
+
+int sana_dit_check_weights(sana_dit * c) {
+    if (!c) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] { check_ready(c); });
+}
+
+int sana_dit_set_context(sana_dit * c, const float * data, int64_t B, int64_t L, int64_t dim, int projected,
+                         const float * bias) {
+    if (!c || !data) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    if (B <= 0 || L <= 0 || L > 512) return set_err(SANA_ERR_INVALID_ARGUMENT, "context batch/length out of range");
+    if (dim != (projected ? c->C : c->Ccap))
+        return set_err(SANA_ERR_SHAPE, "context feature width %lld does not match %s", (long long)dim,
+                       projected ? "hidden" : "caption_dim");
+    return guarded([&] {
+        check_ready(c);
+        ensure_context_buffers(c, B, L);
+        const size_t n = (size_t)B * L * dim;
+        DevMem & dst = projected ? c->ctx32 : c->cap32;
+        hip_check(hipMemcpyAsync(dst.p, data, n * 4, hipMemcpyHostToDevice, c->stream), "upload context");
+        c->ctx_bias = bias != nullptr;
+        if (bias)
+            hip_check(hipMemcpyAsync(c->bias.p, bias, (size_t)B * L * 4, hipMemcpyHostToDevice, c->stream),
+                      "upload bias");
+        enqueue_context(c, dst.as<float>(), projected != 0, B, L, c->stream);
+        hip_check(hipStreamSynchronize(c->stream), "context");
+        c->ctx_ready = true;
+    });
+}
+
+int sana_dit_get_context(sana_dit * c, float * out) {
+    if (!c || !out) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    if (!c->ctx_ready) return set_err(SANA_ERR_STATE, "no context set");
+    return guarded([&] {
+        hip_check(hipMemcpy(out, c->ctx32.p, (size_t)c->ctx_B * c->ctx_L * c->C * 4, hipMemcpyDeviceToHost),
+                  "download context");
+    });
+}
+
+static int check_forward_args(sana_dit * c, int64_t Bl, int64_t Hh, int64_t Ww) {
+    if (Bl <= 0 || Hh <= 0 || Ww <= 0) return set_err(SANA_ERR_INVALID_ARGUMENT, "latent dims must be positive");
+    if (Hh != Ww) return set_err(SANA_ERR_INVALID_ARGUMENT, "token count must form a square grid");
+    if (Hh * Ww > 65535) return set_err(SANA_ERR_INVALID_ARGUMENT, "grid too large");
+    (void)c;
+    return SANA_OK;
+}
+
+int sana_dit_forward_device(sana_dit * c, const float * d_latent, int64_t Bl, int64_t Hh, int64_t Ww, float t,
+                            float * d_out, void * stream) {
+    if (!c || !d_latent || !d_out) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = check_forward_args(c, Bl, Hh, Ww);
+    if (rc) return rc;
+    if (!c->ctx_ready) return set_err(SANA_ERR_STATE, "no context set");
+    if (c->ctx_B != 2 * Bl)
+        return set_err(SANA_ERR_INVALID_ARGUMENT, "context batch size must equal 2 * latent batch size for CFG");
+    return guarded([&] {
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        const int64_t B = 2 * Bl, N = Hh * Ww;
+        ensure_forward_buffers(c, B, N);
+        c->last_M = B * N;
+        c->last_B = B;
+        c->last_N = N;
+        set_t(c, B, t, s);
+        run_graph(c, std::make_tuple(1, Bl, Hh, Ww, c->ctx_L, (const void *)d_latent, (const void *)d_out,
+                                     (const void *)nullptr, (const void *)(intptr_t)c->ctx_bias),
+                  s, [&](hipStream_t gs) {
+                      enqueue_forward(c, d_latent, Bl, Hh, Ww, c->ctx_bias ? c->bias.as<float>() : nullptr, d_out, gs);
+                  });
+    });
+}
+
+int sana_dit_forward(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh, int64_t Ww, float t,
+                     float * noise_pred) {
+    if (!c || !latent || !noise_pred) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = check_forward_args(c, Bl, Hh, Ww);
+    if (rc) return rc;
+    return guarded([&] {
+        const int64_t B = 2 * Bl, N = Hh * Ww;
+        ensure_forward_buffers(c, B, N);
+        hip_check(hipMemcpyAsync(c->lat_in.p, latent, (size_t)Bl * c->Cl * N * 4, hipMemcpyHostToDevice, c->stream),
+                  "upload latent");
+        int r = sana_dit_forward_device(c, c->lat_in.as<float>(), Bl, Hh, Ww, t, c->np_out.as<float>(), c->stream);
+        if (r != SANA_OK) throw_err(r, g_last_error);
+        hip_check(hipMemcpyAsync(noise_pred, c->np_out.p, (size_t)B * c->Cl * N * 4, hipMemcpyDeviceToHost, c->stream),
+                  "download");
+        hip_check(hipStreamSynchronize(c->stream), "forward");
+    });
+}
+
+int sana_dit_step_device(sana_dit * c, const float * d_caption, int64_t L, const float * d_bias,
+                         const float * d_latent, int64_t Bl, int64_t Hh, int64_t Ww, float t, float * d_out,
+                         void * stream) {
+    if (!c || !d_caption || !d_latent || !d_out) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = check_forward_args(c, Bl, Hh, Ww);
+    if (rc) return rc;
+    if (L <= 0 || L > 512) return set_err(SANA_ERR_INVALID_ARGUMENT, "caption length out of range");
+    return guarded([&] {
+        check_ready(c);
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        const int64_t B = 2 * Bl, N = Hh * Ww;
+        ensure_context_buffers(c, B, L);
+        ensure_forward_buffers(c, B, N);
+        c->last_M = B * N;
+        c->last_B = B;
+        c->last_N = N;
+        set_t(c, B, t, s);
+        run_graph(c, std::make_tuple(2, Bl, Hh, Ww, L, (const void *)d_caption, (const void *)d_bias,
+                                     (const void *)d_latent, (const void *)d_out),
+                  s, [&](hipStream_t gs) {
+                      enqueue_context(c, d_caption, false, B, L, gs);
+                      enqueue_forward(c, d_latent, Bl, Hh, Ww, d_bias, d_out, gs);
+                  });
+        // keep the context state consistent for later sana_dit_forward* calls
+        c->ctx_bias = d_bias != nullptr;
+        if (d_bias)
+            hip_check(hipMemcpyAsync(c->bias.p, d_bias, (size_t)B * L * 4, hipMemcpyDeviceToDevice, s), "bias");
+        c->ctx_ready = true;
+    });
+}
+
+int sana_dit_block_forward(sana_dit * c, int64_t blk, const float * x, const float * t_mod, int64_t B, int64_t N,
+                           float * a_self, float * a_cross, float * a_ff) {
+    if (!c || !x || !t_mod) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    if (blk < 0 || blk >= c->L_) return set_err(SANA_ERR_INVALID_ARGUMENT, "block index out of range");
+    if (!c->ctx_ready) return set_err(SANA_ERR_STATE, "no context set");
+    if (B != c->ctx_B) return set_err(SANA_ERR_INVALID_ARGUMENT, "input and context batch size must match");
+    const int64_t side = (int64_t)std::llround(std::sqrt((double)N));
+    if (N <= 0 || side * side != N) return set_err(SANA_ERR_INVALID_ARGUMENT, "token count must form a square grid");
+    return guarded([&] {
+        check_ready(c);
+        ensure_forward_buffers(c, B, N);
+        const size_t n = (size_t)B * N * c->C;
+        hip_check(hipMemcpyAsync(c->x32.p, x, n * 4, hipMemcpyHostToDevice, c->stream), "upload x");
+        hip_check(hipMemcpyAsync(c->tmod.p, t_mod, (size_t)B * 6 * c->C * 4, hipMemcpyHostToDevice, c->stream),
+                  "upload t_mod");
+        struct Hook {
+            sana_dit * c;
+            size_t n;
+            float * outs[3];
+        } h{c, n, {a_self, a_cross, a_ff}};
+        enqueue_block(c, blk, B, N, c->ctx_bias ? c->bias.as<float>() : nullptr, c->stream, [](void * p, int stage) {
+            Hook * hk = static_cast<Hook *>(p);
+            if (hk->outs[stage])
+                hip_check(hipMemcpyAsync(hk->outs[stage], hk->c->x32.p, hk->n * 4, hipMemcpyDeviceToHost, hk->c->stream),
+                          "download stage");
+        }, &h);
+        hip_check(hipStreamSynchronize(c->stream), "block_forward");
+    });
+}
+
+int sana_dit_time_embed(sana_dit * c, const float * t, int64_t B, float * embedded, float * t_mod) {
+    if (!c || !t) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    if (B <= 0) return set_err(SANA_ERR_INVALID_ARGUMENT, "batch must be positive");
+    return guarded([&] {
+        check_ready(c);
+        ensure_forward_buffers(c, B, 1);
+        hip_check(hipMemcpyAsync(c->d_t.p, t, (size_t)B * 4, hipMemcpyHostToDevice, c->stream), "upload t");
+        enqueue_time(c, B, c->stream);
+        if (embedded)
+            hip_check(hipMemcpyAsync(embedded, c->emb.p, (size_t)B * c->C * 4, hipMemcpyDeviceToHost, c->stream), "dl");
+        if (t_mod)
+            hip_check(hipMemcpyAsync(t_mod, c->tmod.p, (size_t)B * 6 * c->C * 4, hipMemcpyDeviceToHost, c->stream),
+                      "dl");
+        hip_check(hipStreamSynchronize(c->stream), "time_embed");
+    });
+}
+
+int sana_dit_time_gemm(sana_dit * c, int which, int iters, float * avg_ms, double * flops) {
+    if (!c || !avg_ms || iters <= 0) return set_err(SANA_ERR_INVALID_ARGUMENT, "bad argument");
+    if (c->last_M <= 0) return set_err(SANA_ERR_STATE, "run a forward first");
+    if (which < 0 || which > 5) return set_err(SANA_ERR_INVALID_ARGUMENT, "which must be 0..5");
+    return guarded([&] {
+        BlockDev & w = *c->blocks[0];
+        const int64_t M = c->last_M, C = c->C, N = c->last_N;
+        // Scratch outputs: the dedicated buffers of each GEMM in the forward.
+        auto run = [&]() {
+            switch (which) {
+                case 0:
+                    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp, nullptr,
+                               sana::kActNone, c->qkv16.as<half_t>(), 3 * C, nullptr, 0, c->stream);
+                    break;
+                case 1:
+                    gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_out.as<half_t>(), c->Cp, M, C, c->Cp,
+                               w.b_out.as<float>(), c->tmod.as<float>() + 2 * C, w.sst.as<float>() + 2 * C, 6 * C, N,
+                               c->x32.as<float>(), C, c->r16.as<half_t>(), c->Cp, c->stream);
+                    break;
+                case 2:
+                    gemm_store(c, c->r16.as<half_t>(), c->Cp, w.w_cq.as<half_t>(), c->Cp, M, C, c->Cp,
+                               w.b_cq.as<float>(), sana::kActNone, c->q16.as<half_t>(), C, nullptr, 0, c->stream);
+                    break;
+                case 3:
+                    gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_co.as<half_t>(), c->Cp, M, C, c->Cp, w.b_co.as<float>(),
+                               nullptr, nullptr, 0, N, c->x32.as<float>(), C, nullptr, 0, c->stream);
+                    break;
+                case 4:
+                    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_inv.as<half_t>(), c->Cp, M, c->E, c->Cp,
+                               w.b_inv.as<float>(), sana::kActSilu, c->hid16.as<half_t>(), c->E, nullptr, 0, c->stream);
+                    break;
+                default:
+                    gemm_resid(c->glu16.as<half_t>(), c->Fp, w.w_pt.as<half_t>(), c->Fp, M, C, c->Fp, nullptr,
+                               c->tmod.as<float>() + 5 * C, w.sst.as<float>() + 5 * C, 6 * C, N, c->x32.as<float>(), C,
+                               nullptr, 0, c->stream);
+            }
+        };
+        const double f[6] = {2.0 * M * 3 * C * C, 2.0 * M * C * C, 2.0 * M * C * C, 2.0 * M * C * C,
+                             2.0 * M * c->E * C, 2.0 * M * C * c->F};
+        run();  // warm
+        hipEvent_t e0, e1;
+        hip_check(hipEventCreate(&e0), "event");
+        hip_check(hipEventCreate(&e1), "event");
+        hip_check(hipEventRecord(e0, c->stream), "record");
+        for (int i = 0; i < iters; ++i) run();
+        hip_check(hipEventRecord(e1, c->stream), "record");
+        hip_check(hipEventSynchronize(e1), "sync");
+        float ms = 0.0f;
+        hip_check(hipEventElapsedTime(&ms, e0, e1), "elapsed");
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        *avg_ms = ms / iters;
+        if (flops) *flops = f[which];
+    });
+}
+
+// ---------------------------------------------------------------- kernel-level launchers
+int sana_hip_gemm(const void * A, int64_t lda, const void * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                  const float * bias, int act, void * out16, int64_t ldo16, float * out32, int64_t ldo32,
+                  void * stream) {
+    if (act < 0 || act > 2) return set_err(SANA_ERR_INVALID_ARGUMENT, "act must be 0..2");
+    return guarded([&] {
+        gemm_store(nullptr, static_cast<const half_t *>(A), lda, static_cast<const half_t *>(W), ldw, M, N, K, bias, act,
+                   static_cast<half_t *>(out16), ldo16, out32, ldo32, static_cast<hipStream_t>(stream));
+    });
+}
+
+int sana_hip_gemm_residual(const void * A, int64_t lda, const void * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                           const float * bias, const float * gate_a, const float * gate_t, int64_t gate_stride,
+                           int64_t rpb, float * x, int64_t ldx, void * out16, int64_t ldo16, void * stream) {
+    return guarded([&] {
+        gemm_resid(static_cast<const half_t *>(A), lda, static_cast<const half_t *>(W), ldw, M, N, K, bias, gate_a,
+                   gate_t, gate_stride, rpb, x, ldx, static_cast<half_t *>(out16), ldo16,
+                   static_cast<hipStream_t>(stream));
+    });
+}
+
+int sana_hip_ln_modulate(const float * x, int64_t ldx, void * out16, int64_t ldo, int64_t M, int64_t C, int64_t rpb,
+                         float eps, const float * gamma, const float * beta, const float * mod_a, const float * mod_t,
+                         int64_t mod_stride, int64_t shift_off, int64_t scale_off, void * stream) {
+    return guarded([&] {
+        launch_check(sana::ln_modulate(x, ldx, static_cast<half_t *>(out16), ldo, (int)M, (int)C, (int)rpb, eps, gamma,
+                                       beta, mod_a, mod_t, mod_stride, shift_off, scale_off,
+                                       static_cast<hipStream_t>(stream)),
+                     "ln_modulate");
+    });
+}
+
+size_t sana_hip_linear_attention_workspace(int64_t B, int64_t N, int64_t H, int64_t D) {
+    return sana::linattn_workspace_floats((int)B, (int)N, (int)H, (int)D) * sizeof(float);
+}
+
+int sana_hip_linear_attention(const void * q, const void * k, const void * v, int64_t ld, void * out, int64_t ldo,
+                              int64_t B, int64_t N, int64_t H, int64_t D, float * ws, void * stream) {
+    return guarded([&] {
+        launch_check(sana::linear_attention(static_cast<const half_t *>(q), static_cast<const half_t *>(k),
+                                            static_cast<const half_t *>(v), ld, static_cast<half_t *>(out), ldo,
+                                            (int)B, (int)N, (int)H, (int)D, ws, static_cast<hipStream_t>(stream)),
+                     "linear_attention");
+    });
+}
+
+int sana_hip_cross_attention(const void * q, int64_t ldq, const void * k, int64_t ldk, const void * vt, int64_t ldvt,
+                             const float * bias, void * out, int64_t ldo, int64_t B, int64_t N, int64_t L, int64_t H,
+                             int64_t D, void * stream) {
+    return guarded([&] {
+        launch_check(sana::cross_attention(static_cast<const half_t *>(q), ldq, static_cast<const half_t *>(k), ldk,
+                                           static_cast<const half_t *>(vt), ldvt, bias, static_cast<half_t *>(out), ldo,
+                                           (int)B, (int)N, (int)L, (int)H, (int)D, static_cast<hipStream_t>(stream)),
+                     "cross_attention");
+    });
+}
+
+int sana_hip_dwconv_glu(const void * x, int64_t ldx, const float * wt, const float * bias, void * out, int64_t ldo,
+                        int64_t B, int64_t Hh, int64_t Ww, int64_t F, void * stream) {
+    return guarded([&] {
+        launch_check(sana::dwconv_glu(static_cast<const half_t *>(x), ldx, wt, bias, static_cast<half_t *>(out), ldo,
+                                      (int)B, (int)Hh, (int)Ww, (int)F, static_cast<hipStream_t>(stream)),
+                     "dwconv_glu");
+    });
+}
+
+}  // extern "C"

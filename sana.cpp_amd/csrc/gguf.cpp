@@ -1,0 +1,175 @@
+// GGUF index reader and mmap helper; see gguf.h for the format summary.
+#include "gguf.h"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cstring>
+#include <set>
+#include <stdexcept>
+
+namespace sana {
+namespace gguf {
+namespace {
+
+enum ValueType : uint32_t {
+    kU8 = 0, kI8 = 1, kU16 = 2, kI16 = 3, kU32 = 4, kI32 = 5, kF32v = 6, kBool = 7, kString = 8, kArray = 9,
+    kU64 = 10, kI64 = 11, kF64 = 12,
+};
+
+struct Reader {
+    const unsigned char * p;
+    uint64_t n, pos = 0;
+    const std::string & path;
+
+    void need(uint64_t k) {
+        if (k > n || pos > n - k) throw std::runtime_error("truncated gguf file: " + path);
+    }
+    template <class T>
+    T get() {
+        need(sizeof(T));
+        T v;
+        std::memcpy(&v, p + pos, sizeof(T));
+        pos += sizeof(T);
+        return v;
+    }
+    std::string str() {
+        const uint64_t len = get<uint64_t>();
+        need(len);
+        std::string s(reinterpret_cast<const char *>(p + pos), len);
+        pos += len;
+        return s;
+    }
+    void skip_value(uint32_t t, int depth = 0) {
+        switch (t) {
+            case kU8: case kI8: case kBool: need(1); pos += 1; break;
+            case kU16: case kI16: need(2); pos += 2; break;
+            case kU32: case kI32: case kF32v: need(4); pos += 4; break;
+            case kU64: case kI64: case kF64: need(8); pos += 8; break;
+            case kString: (void)str(); break;
+            case kArray: {
+                if (depth > 4) throw std::runtime_error("gguf array nesting too deep: " + path);
+                const uint32_t et = get<uint32_t>();
+                const uint64_t cnt = get<uint64_t>();
+                for (uint64_t i = 0; i < cnt; ++i) skip_value(et, depth + 1);
+                break;
+            }
+            default: throw std::runtime_error("unknown gguf metadata type in " + path);
+        }
+    }
+};
+
+}  // namespace
+
+MappedFile::MappedFile(const std::string & path) {
+    const int fd = ::open(path.c_str(), O_RDONLY);
+    if (fd < 0) throw std::runtime_error("failed to open gguf weight file: " + path);
+    struct stat st;
+    if (::fstat(fd, &st) != 0) {
+        ::close(fd);
+        throw std::runtime_error("failed to stat gguf weight file: " + path);
+    }
+    size_ = static_cast<uint64_t>(st.st_size);
+    if (size_ > 0) {
+        void * m = ::mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (m == MAP_FAILED) {
+            ::close(fd);
+            throw std::runtime_error("failed to map gguf weight file: " + path);
+        }
+        data_ = static_cast<const unsigned char *>(m);
+    }
+    ::close(fd);
+}
+
+MappedFile::~MappedFile() {
+    if (data_) ::munmap(const_cast<unsigned char *>(data_), size_);
+}
+
+Index read_index(const std::string & path) {
+    MappedFile f(path);
+    Reader r{f.data(), f.size(), 0, path};
+    Index idx;
+    idx.path = path;
+    idx.file_size = f.size();
+    if (r.get<uint32_t>() != 0x46554747u) throw std::runtime_error("not a gguf file (bad magic): " + path);
+    idx.version = r.get<uint32_t>();
+    if (idx.version != 2 && idx.version != 3) throw std::runtime_error("unsupported gguf version in " + path);
+    const uint64_t n_tensors = r.get<uint64_t>();
+    const uint64_t n_kv = r.get<uint64_t>();
+    if (n_tensors > (1u << 24) || n_kv > (1u << 24)) throw std::runtime_error("implausible gguf counts: " + path);
+    for (uint64_t i = 0; i < n_kv; ++i) {
+        const std::string key = r.str();
+        const uint32_t t = r.get<uint32_t>();
+        if (key == "general.alignment") {
+            if (t != kU32) throw std::runtime_error("general.alignment must be u32: " + path);
+            idx.alignment = r.get<uint32_t>();
+            if (idx.alignment == 0 || (idx.alignment & (idx.alignment - 1)))
+                throw std::runtime_error("general.alignment must be a power of two: " + path);
+        } else {
+            r.skip_value(t);
+        }
+    }
+    std::set<std::string> seen;
+    for (uint64_t i = 0; i < n_tensors; ++i) {
+        TensorInfo ti;
+        ti.name = r.str();
+        const uint32_t nd = r.get<uint32_t>();
+        if (nd == 0 || nd > 4) throw std::runtime_error("bad tensor rank for " + ti.name + " in " + path);
+        std::vector<int64_t> ne(nd);
+        for (uint32_t d = 0; d < nd; ++d) {
+            const uint64_t v = r.get<uint64_t>();
+            if (v == 0 || v > (1ull << 40)) throw std::runtime_error("bad tensor dim for " + ti.name);
+            ne[d] = static_cast<int64_t>(v);
+        }
+        ti.shape.assign(ne.rbegin(), ne.rend());
+        ti.type = r.get<uint32_t>();
+        ti.offset = r.get<uint64_t>();
+        if (!seen.insert(ti.name).second) throw std::runtime_error("duplicate tensor " + ti.name + " in " + path);
+        uint64_t numel = 1;
+        for (int64_t v : ti.shape) numel *= static_cast<uint64_t>(v);
+        ti.nbytes = ti.type == kF32 ? numel * 4 : (ti.type == kF16 || ti.type == kBF16) ? numel * 2 : 0;
+        idx.tensors.push_back(ti);
+    }
+    idx.data_offset = (r.pos + idx.alignment - 1) / idx.alignment * idx.alignment;
+    for (TensorInfo & ti : idx.tensors) {
+        if (ti.offset % idx.alignment) throw std::runtime_error("misaligned tensor data for " + ti.name);
+        ti.offset += idx.data_offset;
+        if (ti.nbytes && (ti.offset > idx.file_size || ti.nbytes > idx.file_size - ti.offset))
+            throw std::runtime_error("failed to read gguf tensor payload for: " + ti.name);
+    }
+    return idx;
+}
+
+namespace {
+bool trailing_index(const std::string & p, std::string * stem, uint64_t * idx) {
+    const size_t dot = p.rfind('.');
+    if (dot == std::string::npos || dot + 1 >= p.size()) return false;
+    for (size_t i = dot + 1; i < p.size(); ++i)
+        if (p[i] < '0' || p[i] > '9') return false;
+    *stem = p.substr(0, dot);
+    *idx = std::stoull(p.substr(dot + 1));
+    return true;
+}
+}  // namespace
+
+std::vector<std::string> block_prefixes(const std::vector<std::string> & names) {
+    const std::string suf = ".scale_shift_table";
+    std::set<std::string> u;
+    for (const std::string & n : names)
+        if (n.size() >= suf.size() && n.compare(n.size() - suf.size(), suf.size(), suf) == 0)
+            u.insert(n.substr(0, n.size() - suf.size()));
+    std::vector<std::string> v(u.begin(), u.end());
+    std::sort(v.begin(), v.end(), [](const std::string & a, const std::string & b) {
+        std::string sa, sb;
+        uint64_t ia = 0, ib = 0;
+        if (trailing_index(a, &sa, &ia) && trailing_index(b, &sb, &ib) && sa == sb) return ia < ib;
+        return a < b;
+    });
+    return v;
+}
+
+}  // namespace gguf
+}  // namespace sana

@@ -1,0 +1,164 @@
+// GGUF entry points of the C ABI: sana_dit_load_gguf (the three-file loader of
+// load_denoiser_weights, src/transformer.cpp:453-488) and the index
+// inspection helpers.
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/sana_dit.h"
+#include "gguf.h"
+
+namespace sana {
+void set_last_error(const std::string & m);  // dit.hip: storage behind sana_dit_last_error()
+}
+
+namespace {
+
+// Block tensors the reference loads per prefix (src/transformer.cpp:214-308).
+const char * const kBlockSuffixes[] = {
+    "scale_shift_table", "attn1.to_q.weight", "attn1.to_k.weight", "attn1.to_v.weight", "attn1.to_out.0.weight",
+    "attn1.to_out.0.bias", "attn2.to_q.weight", "attn2.to_q.bias", "attn2.to_k.weight", "attn2.to_k.bias",
+    "attn2.to_v.weight", "attn2.to_v.bias", "attn2.to_out.0.weight", "attn2.to_out.0.bias",
+    "ff.conv_inverted.weight", "ff.conv_inverted.bias", "ff.conv_depth.weight", "ff.conv_depth.bias",
+    "ff.conv_point.weight",
+};
+const char * const kCaptionNames[] = {
+    "caption_projection.linear_1.weight", "caption_projection.linear_1.bias", "caption_projection.linear_2.weight",
+    "caption_projection.linear_2.bias",
+};
+const char * const kDenoiserNames[] = {
+    "patch_embed.proj.weight", "patch_embed.proj.bias", "time_embed.emb.timestep_embedder.linear_1.weight",
+    "time_embed.emb.timestep_embedder.linear_1.bias", "time_embed.emb.timestep_embedder.linear_2.weight",
+    "time_embed.emb.timestep_embedder.linear_2.bias", "time_embed.linear.weight", "time_embed.linear.bias",
+    "caption_norm.weight", "scale_shift_table", "proj_out.weight", "proj_out.bias",
+};
+
+
+struct Err {
+    int code;
+    std::string msg;
+};
+
+const float * payload(const sana::gguf::MappedFile & f, const sana::gguf::TensorInfo & t) {
+    if (t.type != sana::gguf::kF32)
+        throw Err{SANA_ERR_FORMAT, "only float32 gguf tensors are supported: " + t.name};
+    return reinterpret_cast<const float *>(f.data() + t.offset);
+}
+
+const sana::gguf::TensorInfo & find(const sana::gguf::Index & idx, const std::string & n) {
+    for (const auto & t : idx.tensors)
+        if (t.name == n) return t;
+    throw Err{SANA_ERR_INVALID_ARGUMENT, "weight name not found in weight index: " + n};
+}
+
+void call(int rc) {
+    if (rc != SANA_OK) throw Err{rc, sana_dit_last_error()};
+}
+
+// Small cache so the per-index inspection calls do not re-parse the file.
+std::mutex g_cache_mu;
+std::string g_cache_path;
+std::shared_ptr<sana::gguf::Index> g_cache;
+
+std::shared_ptr<sana::gguf::Index> cached_index(const std::string & path) {
+    std::lock_guard<std::mutex> lk(g_cache_mu);
+    if (!g_cache || g_cache_path != path) {
+        g_cache = std::make_shared<sana::gguf::Index>(sana::gguf::read_index(path));
+        g_cache_path = path;
+    }
+    return g_cache;
+}
+
+template <class F>
+int guarded(F f) {
+    try {
+        f();
+        return SANA_OK;
+    } catch (const Err & e) {
+        sana::set_last_error(e.msg);
+        return e.code;
+    } catch (const std::exception & e) {
+        sana::set_last_error(e.what());
+        return SANA_ERR_IO;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * caption_path, const char * denoiser_path) {
+    if (!ctx || !model_path || !caption_path || !denoiser_path) {
+        sana::set_last_error("null argument");
+        return SANA_ERR_INVALID_ARGUMENT;
+    }
+    return guarded([&] {
+        using namespace sana::gguf;
+        // model blocks
+        {
+            const Index idx = read_index(model_path);
+            MappedFile f(model_path);
+            std::vector<std::string> names;
+            for (const auto & t : idx.tensors) names.push_back(t.name);
+            const std::vector<std::string> pre = block_prefixes(names);
+            if (pre.empty()) throw Err{SANA_ERR_INVALID_ARGUMENT, "weight index does not contain any prefixed model blocks"};
+            for (size_t b = 0; b < pre.size(); ++b) {
+                for (const char * s : kBlockSuffixes) {
+                    const std::string full = pre[b].empty() ? std::string(s) : pre[b] + "." + s;
+                    const TensorInfo & t = find(idx, full);
+                    int rc = sana_dit_set_block_weight(ctx, (int64_t)b, s, payload(f, t), t.shape.data(),
+                                                       (int)t.shape.size(), 0);
+                    if (rc == SANA_ERR_INVALID_ARGUMENT && b > 0)
+                        throw Err{SANA_ERR_SHAPE, "gguf holds more blocks than the model's layer count"};
+                    call(rc);
+                }
+            }
+        }
+        for (int which = 0; which < 2; ++which) {
+            const char * path = which == 0 ? caption_path : denoiser_path;
+            const Index idx = read_index(path);
+            MappedFile f(path);
+            const size_t n = which == 0 ? sizeof(kCaptionNames) / sizeof(kCaptionNames[0])
+                                        : sizeof(kDenoiserNames) / sizeof(kDenoiserNames[0]);
+            for (size_t i = 0; i < n; ++i) {
+                const char * name = which == 0 ? kCaptionNames[i] : kDenoiserNames[i];
+                const TensorInfo & t = find(idx, name);
+                call(sana_dit_set_weight(ctx, name, payload(f, t), t.shape.data(), (int)t.shape.size(), 0));
+            }
+        }
+        call(sana_dit_check_weights(ctx));
+    });
+}
+
+int sana_gguf_num_tensors(const char * path, int64_t * n) {
+    if (!path || !n) {
+        sana::set_last_error("null argument");
+        return SANA_ERR_INVALID_ARGUMENT;
+    }
+    return guarded([&] { *n = (int64_t)cached_index(path)->tensors.size(); });
+}
+
+int sana_gguf_tensor_info(const char * path, int64_t i, char * name, size_t name_cap, int64_t * shape, int * ndim,
+                          int * type, uint64_t * offset) {
+    if (!path || !name || !shape || !ndim || !type || !offset) {
+        sana::set_last_error("null argument");
+        return SANA_ERR_INVALID_ARGUMENT;
+    }
+    return guarded([&] {
+        auto idx = cached_index(path);
+        if (i < 0 || i >= (int64_t)idx->tensors.size()) throw Err{SANA_ERR_INVALID_ARGUMENT, "tensor index out of range"};
+        const auto & t = idx->tensors[i];
+        if (t.name.size() + 1 > name_cap) throw Err{SANA_ERR_INVALID_ARGUMENT, "name buffer too small"};
+        std::memcpy(name, t.name.c_str(), t.name.size() + 1);
+        *ndim = (int)t.shape.size();
+        for (size_t d = 0; d < t.shape.size(); ++d) shape[d] = t.shape[d];
+        *type = (int)t.type;
+        *offset = t.offset;
+    });
+}
+
+}  // extern "C"

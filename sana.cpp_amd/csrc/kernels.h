@@ -1,0 +1,100 @@
+// Host-side launchers of the gfx950 kernels.  Every launcher validates the
+// shapes its kernel assumes and returns hipErrorInvalidValue instead of
+// launching when they do not hold, so no kernel runs out of bounds.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sana {
+
+typedef _Float16 half_t;
+
+enum GemmMode {
+    kGemmStore = 0,     // out16/out32[m, n] = act(acc + bias[n])
+    kGemmResidual = 1,  // out32[m, n] += gate(m, n) * (acc + bias[n]); out16 = f16(out32) if set
+    kGemmVT = 2,        // transposed-batched store of V^T (see GemmParams::vt_*)
+};
+
+enum GemmAct { kActNone = 0, kActSilu = 1, kActGelu = 2 };
+
+// C[m, n] = sum_k A[m, k] * W[n, k]; fp16 operands, fp32 accumulation.
+// K must be a multiple of 64 and both lda and ldw >= K, multiples of 8.
+struct GemmParams {
+    const half_t * A = nullptr;
+    int64_t lda = 0;
+    const half_t * W = nullptr;
+    int64_t ldw = 0;
+    int M = 0, N = 0, K = 0;
+    const float * bias = nullptr;     // [N] (kGemmVT: [M], per output row)
+    int mode = kGemmStore;
+    int act = kActNone;
+    half_t * out16 = nullptr;
+    int64_t ldo16 = 0;
+    float * out32 = nullptr;
+    int64_t ldo32 = 0;
+    // Residual gate: gate(m, n) = gate_a[(m / rows_per_batch) * gate_stride + n] + gate_t[n]
+    // (t_mod row slice + scale_shift_table row); gate_a == nullptr means gate 1.
+    const float * gate_a = nullptr;
+    const float * gate_t = nullptr;
+    int64_t gate_stride = 0;
+    int rows_per_batch = 1;
+    // kGemmVT: element (m, n) with m = blk * vt_rows + r, n = b * vt_cols + j is
+    // stored at out16[((blk * vt_batch + b) * vt_rows + r) * vt_ld + j].
+    int vt_rows = 0, vt_cols = 0, vt_batch = 0;
+    int64_t vt_ld = 0;
+};
+
+hipError_t gemm(const GemmParams & p, hipStream_t s);
+
+// LayerNorm (eps, optional gamma/beta) + adaLN modulate, fp32 in, fp16 out:
+// out[m, c] = f16(ln(x)[m, c] * (1 + scale) + shift), with
+// shift = mod_a[b * mod_stride + shift_off + c] + mod_t[shift_off + c] (same for scale; mod_t may be null).
+hipError_t ln_modulate(const float * x, int64_t ldx, half_t * out, int64_t ldo, int M, int C, int rows_per_batch,
+                       float eps, const float * gamma, const float * beta, const float * mod_a, const float * mod_t,
+                       int64_t mod_stride, int64_t shift_off, int64_t scale_off, hipStream_t s);
+
+// RMSNorm (eps, weight) fp32 -> fp16 (and optionally fp32 [M, C] into out32).
+hipError_t rms_norm_f16(const float * x, int64_t ldx, const float * weight, half_t * out, int64_t ldo, float * out32,
+                        int M, int C, float eps, hipStream_t s);
+
+// fp32 -> fp16 copy of a [M, C] matrix into a buffer with leading dim ldo
+// (columns C..ldo-1 are written as zero).
+hipError_t to_f16_padded(const float * x, int M, int C, half_t * out, int64_t ldo, hipStream_t s);
+
+// Time MLP pieces (fp32): sinusoid [cos(t f_i), sin(t f_i)] of B timesteps read
+// from device memory, f_i = freq[i] for i < half.
+hipError_t timestep_sinusoid(const float * t, const float * freq, int B, int half, float * out, hipStream_t s);
+// out[b, n] = bias[n] + sum_k act_in(in[b, k]) * W[n, k] (W fp32 [N, K]); act_in: 0 none, 1 silu.
+hipError_t gemv_f32(const float * in, const float * W, const float * bias, float * out, int B, int K, int N,
+                    int act_in, hipStream_t s);
+
+// Patch embed: NCHW latent [Bl, Cl, S] (batch b reads latent batch b % Bl) -> tokens [B, S, C] fp32.
+hipError_t patch_embed(const float * latent, int Bl, int B, int Cl, int S, const float * W, const float * bias,
+                       float * out, int C, hipStream_t s);
+
+// Final layer: LN(eps, no affine) + modulate(shift = emb + T[0], scale = emb + T[1])
+// + proj (W [Cl, C] fp32, bias [Cl]) stored NCHW [B, Cl, S].
+hipError_t final_layer(const float * x, const float * emb, const float * table, const float * W, const float * bias,
+                       float * out, int B, int S, int C, int Cl, float eps, hipStream_t s);
+
+// ReLU linear attention.  q/k/v fp16 token-major with row stride ld (head h at
+// columns h*D..), out fp16 with row stride ldo.  Workspace: partial states.
+size_t linattn_workspace_floats(int B, int N, int H, int D);
+hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v, int64_t ld, half_t * out,
+                            int64_t ldo, int B, int N, int H, int D, float * workspace, hipStream_t s);
+
+// Softmax cross attention.  q fp16 [B*N, ldq]; k fp16 rows (b*L + j) with stride
+// ldk (head h at columns h*D..); vt fp16 [B][H*D][ldvt] (keys contiguous);
+// bias fp32 [B, L] or null; out fp16 [B*N, ldo].
+hipError_t cross_attention(const half_t * q, int64_t ldq, const half_t * k, int64_t ldk, const half_t * vt,
+                           int64_t ldvt, const float * bias, half_t * out, int64_t ldo, int B, int N, int L, int H,
+                           int D, hipStream_t s);
+
+// Depthwise 3x3 (zero pad, bias) + GLU gate on a token-major grid:
+// x fp16 [B, H*W, ldx] (E = 2F channels), wt fp32 tap-major [9][E], bias [E],
+// out[b, t, c] = f16(d(c) * silu(d(F + c))), out fp16 [B*H*W, ldo].
+hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const float * bias, half_t * out, int64_t ldo,
+                      int B, int Hh, int Ww, int F, hipStream_t s);
+
+}  // namespace sana

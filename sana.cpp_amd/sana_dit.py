@@ -1,0 +1,217 @@
+"""ctypes binding of libsana_dit.so (the C ABI declared in include/sana_dit.h).
+
+This is the Python-side stub a caller binds; tests and bench.py use it.  It
+never falls back to anything: if the library is missing or a call fails, it
+raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsana_dit.so")
+
+SANA_OK = 0
+SANA_ERR_INVALID_ARGUMENT = -1
+SANA_ERR_SHAPE = -2
+SANA_ERR_IO = -3
+SANA_ERR_FORMAT = -4
+SANA_ERR_HIP = -5
+SANA_ERR_OUT_OF_MEMORY = -6
+SANA_ERR_STATE = -7
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_fp = ctypes.POINTER(ctypes.c_float)
+
+
+class Config(ctypes.Structure):
+    _fields_ = [("layers", _i64), ("hidden", _i64), ("ffn", _i64), ("caption_dim", _i64),
+                ("latent_channels", _i64), ("self_heads", _i64), ("cross_heads", _i64), ("device", ctypes.c_int)]
+
+
+# name -> (restype, argtypes); exactly the entry points of include/sana_dit.h
+PROTOTYPES = {
+    "sana_dit_last_error": (ctypes.c_char_p, []),
+    "sana_dit_create": (ctypes.c_int, [ctypes.POINTER(Config), ctypes.POINTER(_vp)]),
+    "sana_dit_destroy": (None, [_vp]),
+    "sana_dit_set_weight": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, ctypes.POINTER(_i64), ctypes.c_int,
+                                           ctypes.c_int]),
+    "sana_dit_set_block_weight": (ctypes.c_int, [_vp, _i64, ctypes.c_char_p, _vp, ctypes.POINTER(_i64),
+                                                 ctypes.c_int, ctypes.c_int]),
+    "sana_dit_set_block_norm": (ctypes.c_int, [_vp, _i64, ctypes.c_int, _vp, _vp]),
+    "sana_dit_check_weights": (ctypes.c_int, [_vp]),
+    "sana_dit_load_gguf": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
+    "sana_dit_set_context": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
+    "sana_dit_get_context": (ctypes.c_int, [_vp, _vp]),
+    "sana_dit_forward": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp]),
+    "sana_dit_forward_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp, _vp]),
+    "sana_dit_step_device": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp, _vp]),
+    "sana_dit_block_forward": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "sana_dit_time_embed": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
+    "sana_dit_time_gemm": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _fp, ctypes.POINTER(ctypes.c_double)]),
+    "sana_gguf_num_tensors": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_i64)]),
+    "sana_gguf_tensor_info": (ctypes.c_int, [ctypes.c_char_p, _i64, ctypes.c_char_p, ctypes.c_size_t,
+                                             ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_int),
+                                             ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_uint64)]),
+    "sana_hip_gemm": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, ctypes.c_int, _vp, _i64, _vp,
+                                     _i64, _vp]),
+    "sana_hip_gemm_residual": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
+                                              _vp, _i64, _vp, _i64, _vp]),
+    "sana_hip_ln_modulate": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _vp,
+                                            _vp, _i64, _i64, _i64, _vp]),
+    "sana_hip_linear_attention": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "sana_hip_linear_attention_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
+    "sana_hip_cross_attention": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
+                                                _i64, _i64, _vp]),
+    "sana_hip_dwconv_glu": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in PROTOTYPES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+class SanaError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def check(rc):
+    if rc != SANA_OK:
+        raise SanaError(rc, lib().sana_dit_last_error().decode())
+
+
+def ptr(x):
+    """Address of a numpy array, a torch tensor, an int or None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if isinstance(x, np.ndarray):
+        assert x.flags["C_CONTIGUOUS"]
+        return x.ctypes.data
+    return x.data_ptr()  # torch tensor
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Dit:
+    """One device context (weights, workspace, graphs) of the DiT."""
+
+    def __init__(self, layers=28, hidden=1152, ffn=5760, caption_dim=2304, latent_channels=32, self_heads=36,
+                 cross_heads=16, device=0):
+        cfg = Config(layers, hidden, ffn, caption_dim, latent_channels, self_heads, cross_heads, device)
+        self.cfg = cfg
+        h = _vp()
+        check(lib().sana_dit_create(ctypes.byref(cfg), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().sana_dit_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def set_weight(self, name, arr, transposed=False):
+        arr = _f32(arr)
+        shape = (_i64 * arr.ndim)(*arr.shape)
+        if name.startswith("transformer_blocks."):
+            _, idx, suffix = name.split(".", 2)
+            check(lib().sana_dit_set_block_weight(self.h, int(idx), suffix.encode(), ptr(arr), shape, arr.ndim,
+                                                  int(transposed)))
+        else:
+            check(lib().sana_dit_set_weight(self.h, name.encode(), ptr(arr), shape, arr.ndim, int(transposed)))
+
+    def set_block_norm(self, block, which, gamma=None, beta=None):
+        g = None if gamma is None else _f32(gamma)
+        b = None if beta is None else _f32(beta)
+        check(lib().sana_dit_set_block_norm(self.h, block, which, ptr(g), ptr(b)))
+
+    def check_weights(self):
+        check(lib().sana_dit_check_weights(self.h))
+
+    def load_gguf(self, model, caption, denoiser):
+        check(lib().sana_dit_load_gguf(self.h, model.encode(), caption.encode(), denoiser.encode()))
+
+    def set_context(self, data, projected, bias=None):
+        data = _f32(data)
+        B, L, dim = data.shape
+        b = None if bias is None else _f32(bias)
+        check(lib().sana_dit_set_context(self.h, ptr(data), B, L, dim, int(projected), ptr(b)))
+
+    def get_context(self, shape):
+        out = np.empty(shape, np.float32)
+        check(lib().sana_dit_get_context(self.h, ptr(out)))
+        return out
+
+    def forward(self, latent, t):
+        latent = _f32(latent)
+        Bl, Cl, H, W = latent.shape
+        out = np.empty((2 * Bl, Cl, H, W), np.float32)
+        check(lib().sana_dit_forward(self.h, ptr(latent), Bl, H, W, float(t), ptr(out)))
+        return out
+
+    def forward_device(self, d_latent, shape, t, d_out, stream=None):
+        Bl, Cl, H, W = shape
+        check(lib().sana_dit_forward_device(self.h, ptr(d_latent), Bl, H, W, float(t), ptr(d_out), stream))
+
+    def step_device(self, d_caption, L, d_bias, d_latent, shape, t, d_out, stream=None):
+        Bl, Cl, H, W = shape
+        check(lib().sana_dit_step_device(self.h, ptr(d_caption), L, ptr(d_bias), ptr(d_latent), Bl, H, W, float(t),
+                                         ptr(d_out), stream))
+
+    def block_forward(self, block, x, t_mod):
+        x = _f32(x)
+        t_mod = _f32(t_mod)
+        B, N, C = x.shape
+        outs = [np.empty_like(x) for _ in range(3)]
+        check(lib().sana_dit_block_forward(self.h, block, ptr(x), ptr(t_mod), B, N, *[ptr(o) for o in outs]))
+        return outs
+
+    def time_embed(self, t):
+        t = _f32(np.atleast_1d(t))
+        C = self.cfg.hidden
+        emb = np.empty((t.size, C), np.float32)
+        tmod = np.empty((t.size, 6 * C), np.float32)
+        check(lib().sana_dit_time_embed(self.h, ptr(t), t.size, ptr(emb), ptr(tmod)))
+        return emb, tmod
+
+    def time_gemm(self, which, iters):
+        ms = ctypes.c_float()
+        fl = ctypes.c_double()
+        check(lib().sana_dit_time_gemm(self.h, which, iters, ctypes.byref(ms), ctypes.byref(fl)))
+        return ms.value, fl.value
+
+
+def gguf_index(path):
+    """[(name, shape, ggml_type, absolute_offset)] of a GGUF file (CPU only)."""
+    n = _i64()
+    check(lib().sana_gguf_num_tensors(path.encode(), ctypes.byref(n)))
+    out = []
+    for i in range(n.value):
+        name = ctypes.create_string_buffer(1024)
+        shape = (_i64 * 4)()
+        nd, ty, off = ctypes.c_int(), ctypes.c_int(), ctypes.c_uint64()
+        check(lib().sana_gguf_tensor_info(path.encode(), i, name, 1024, shape, ctypes.byref(nd), ctypes.byref(ty),
+                                          ctypes.byref(off)))
+        out.append((name.value.decode(), tuple(shape[:nd.value]), ty.value, off.value))
+    return out

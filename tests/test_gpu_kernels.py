@@ -1,0 +1,229 @@
+"""Kernel-level parity of the gfx950 HIP kernels, called through the C ABI.
+
+Each kernel is compared with the CPU oracle (or an fp64 numpy product for the
+GEMM) evaluated on the same fp16-rounded operands, so the only differences
+left are accumulation order and the fp16 rounding of the kernel's own output.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible to torch")
+
+
+def dev(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda").to(dtype)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+@pytest.fixture(scope="module")
+def L():
+    _need_gpu()
+    import sana_dit
+    return sana_dit
+
+
+GEMM_SHAPES = [
+    (2048, 3456, 1152),   # fused QKV at 1024 px
+    (2048, 5760, 1152),   # Mix-FFN inverted
+    (2048, 1152, 2880),   # Mix-FFN point
+    (2048, 1152, 1152),   # attention out / cross q / cross out
+    (600, 4608, 1152),    # cross K of 4 blocks
+    (100, 70, 64),        # ragged M and N
+    (7, 3, 64),           # tiny
+]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_gemm_store(L, M, N, K):
+    rng = np.random.default_rng(M * 7 + N)
+    A = f16(rng.standard_normal((M, K)))
+    W = f16(rng.standard_normal((N, K)) * 0.03)
+    bias = rng.standard_normal(N).astype(np.float32) * 0.1
+    ref = A.astype(np.float64) @ W.astype(np.float64).T + bias
+    dA, dW, db = dev(A, torch.float16), dev(W, torch.float16), dev(bias, torch.float32)
+    o32 = torch.empty((M, N), device="cuda", dtype=torch.float32)
+    o16 = torch.empty((M, N), device="cuda", dtype=torch.float16)
+    L.check(L.lib().sana_hip_gemm(dA.data_ptr(), K, dW.data_ptr(), K, M, N, K, db.data_ptr(), 0, o16.data_ptr(), N,
+                                  o32.data_ptr(), N, stream()))
+    got32, got16 = host(o32), host(o16)
+    assert rel_l2(got32, ref) < 1e-5, rel_l2(got32, ref)
+    assert rel_l2(got16, ref) < 1e-3
+    assert np.abs(got32 - ref).max() < 1e-3 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("act", [1, 2])
+def test_gemm_activation(L, act):
+    M, N, K = 300, 200, 128
+    rng = np.random.default_rng(act)
+    A = f16(rng.standard_normal((M, K)))
+    W = f16(rng.standard_normal((N, K)) * 0.1)
+    bias = rng.standard_normal(N).astype(np.float32)
+    z = A.astype(np.float64) @ W.astype(np.float64).T + bias
+    ref = z / (1 + np.exp(-z)) if act == 1 else 0.5 * z * (1 + np.tanh(np.sqrt(2 / np.pi) * (z + 0.044715 * z ** 3)))
+    o32 = torch.empty((M, N), device="cuda", dtype=torch.float32)
+    dA, dW, db = dev(A, torch.float16), dev(W, torch.float16), dev(bias, torch.float32)
+    L.check(L.lib().sana_hip_gemm(dA.data_ptr(), K, dW.data_ptr(), K, M, N, K, db.data_ptr(), act, None, 0,
+                                  o32.data_ptr(), N, stream()))
+    assert rel_l2(host(o32), ref) < 1e-5
+
+
+def test_gemm_residual_gate(L):
+    B, Ntok, C, K = 2, 96, 160, 128
+    M = B * Ntok
+    rng = np.random.default_rng(5)
+    A = f16(rng.standard_normal((M, K)))
+    W = f16(rng.standard_normal((C, K)) * 0.1)
+    bias = rng.standard_normal(C).astype(np.float32)
+    x = rng.standard_normal((M, C)).astype(np.float32)
+    tmod = rng.standard_normal((B, 6 * C)).astype(np.float32)
+    table = rng.standard_normal((6, C)).astype(np.float32)
+    gate = tmod[:, 2 * C:3 * C] + table[2]
+    y = A.astype(np.float64) @ W.astype(np.float64).T + bias
+    ref = x + np.repeat(gate, Ntok, axis=0) * y
+    dx = dev(x, torch.float32)
+    o16 = torch.empty((M, C), device="cuda", dtype=torch.float16)
+    dA, dW, db = dev(A, torch.float16), dev(W, torch.float16), dev(bias, torch.float32)
+    dt, dtab = dev(tmod, torch.float32), dev(table, torch.float32)
+    L.check(L.lib().sana_hip_gemm_residual(dA.data_ptr(), K, dW.data_ptr(), K, M, C, K, db.data_ptr(),
+                                           dt.data_ptr() + 2 * C * 4, dtab.data_ptr() + 2 * C * 4, 6 * C, Ntok,
+                                           dx.data_ptr(), C,
+                                           o16.data_ptr(), C, stream()))
+    got = host(dx)
+    assert rel_l2(got, ref) < 1e-5
+    assert rel_l2(host(o16), got) < 1e-3
+
+
+def test_gemm_rejects_bad_k(L):
+    M, N, K = 64, 64, 100
+    a = torch.zeros((M, 128), device="cuda", dtype=torch.float16)
+    o = torch.empty((M, N), device="cuda", dtype=torch.float32)
+    rc = L.lib().sana_hip_gemm(a.data_ptr(), 128, a.data_ptr(), 128, M, N, K, None, 0, None, 0, o.data_ptr(), N,
+                               stream())
+    assert rc == L.SANA_ERR_SHAPE
+
+
+@pytest.mark.parametrize("C", [1152, 2, 130])
+def test_ln_modulate(L, C):
+    B, N = 2, 33
+    rng = np.random.default_rng(C)
+    x = (rng.standard_normal((B, N, C)) * 3 + 1).astype(np.float32)
+    tmod = (rng.standard_normal((B, 6 * C)) * 0.1).astype(np.float32)
+    table = (rng.standard_normal((6, C)) * 0.1).astype(np.float32)
+    mod = tmod + table.reshape(-1)
+    ref = O.modulate(O.layer_norm(x, 1e-6), mod[:, :C], mod[:, C:2 * C])
+    out = torch.empty((B * N, C), device="cuda", dtype=torch.float16)
+    dx, dt, dtab = dev(x, torch.float32), dev(tmod, torch.float32), dev(table, torch.float32)
+    L.check(L.lib().sana_hip_ln_modulate(dx.data_ptr(), C, out.data_ptr(), C, B * N, C, N, 1e-6, None, None,
+                                         dt.data_ptr(), dtab.data_ptr(), 6 * C, 0, C, stream()))
+    got = host(out).reshape(B, N, C)
+    assert rel_l2(got, ref) < 1e-3
+
+
+@pytest.mark.parametrize("B,N,H,D", [(2, 1024, 36, 32), (2, 4096, 16, 72), (1, 256, 16, 72), (1, 5, 1, 2),
+                                     (2, 300, 3, 7)])
+def test_linear_attention(L, B, N, H, D):
+    rng = np.random.default_rng(N + D)
+    C = H * D
+    q, k, v = (f16(rng.standard_normal((B, N, C))) for _ in range(3))
+    ref = O.linear_attention(q, k, v, H)
+    ws = torch.empty(L.lib().sana_hip_linear_attention_workspace(B, N, H, D) // 4 + 1, device="cuda",
+                     dtype=torch.float32)
+    dq, dk, dv = dev(q, torch.float16), dev(k, torch.float16), dev(v, torch.float16)
+    out = torch.empty((B * N, C), device="cuda", dtype=torch.float16)
+    L.check(L.lib().sana_hip_linear_attention(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), C, out.data_ptr(), C, B,
+                                              N, H, D, ws.data_ptr(), stream()))
+    got = host(out).reshape(B, N, C)
+    assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
+
+
+def test_linear_attention_negative_query_gives_zero(L):
+    # relu(q) == 0 for a whole head row -> numerator 0, denominator 1e-15 -> exactly 0
+    B, N, H, D = 1, 64, 2, 32
+    rng = np.random.default_rng(1)
+    q = f16(rng.standard_normal((B, N, H * D)))
+    q[0, 5, :D] = -np.abs(q[0, 5, :D]) - 0.1
+    k, v = (f16(rng.standard_normal((B, N, H * D))) for _ in range(2))
+    ws = torch.empty(L.lib().sana_hip_linear_attention_workspace(B, N, H, D) // 4 + 1, device="cuda",
+                     dtype=torch.float32)
+    out = torch.empty((B * N, H * D), device="cuda", dtype=torch.float16)
+    dq, dk, dv = dev(q, torch.float16), dev(k, torch.float16), dev(v, torch.float16)
+    L.check(L.lib().sana_hip_linear_attention(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), H * D, out.data_ptr(),
+                                              H * D, B, N, H, D, ws.data_ptr(), stream()))
+    got = host(out)
+    assert np.all(got[5, :D] == 0.0)
+
+
+def _xattn(L, q, k, v, H, bias):
+    B, N, C = q.shape
+    Lk = k.shape[1]
+    D = C // H
+    Lp = (Lk + 31) // 32 * 32
+    vt = np.zeros((B, C, Lp), np.float32)
+    vt[:, :, :Lk] = np.transpose(v, (0, 2, 1))
+    dq, dk, dvt = dev(q, torch.float16), dev(k, torch.float16), dev(vt, torch.float16)
+    db = None if bias is None else dev(bias, torch.float32)
+    out = torch.empty((B * N, C), device="cuda", dtype=torch.float16)
+    L.check(L.lib().sana_hip_cross_attention(dq.data_ptr(), C, dk.data_ptr(), C, dvt.data_ptr(), Lp,
+                                             None if db is None else db.data_ptr(), out.data_ptr(), C, B, N, Lk, H, D,
+                                             stream()))
+    return host(out).reshape(B, N, C)
+
+
+@pytest.mark.parametrize("B,N,Lk,H,D,masked", [(2, 1024, 300, 16, 72, False), (2, 256, 300, 16, 72, True),
+                                               (1, 70, 33, 4, 32, False), (1, 2, 2, 1, 2, False),
+                                               (1, 17, 5, 3, 12, True)])
+def test_cross_attention(L, B, N, Lk, H, D, masked):
+    rng = np.random.default_rng(N + Lk)
+    C = H * D
+    q = f16(rng.standard_normal((B, N, C)))
+    k = f16(rng.standard_normal((B, Lk, C)))
+    v = f16(rng.standard_normal((B, Lk, C)))
+    bias = None
+    if masked:
+        bias = np.full((B, Lk), -10000.0, np.float32)
+        bias[0, :1] = 0
+        if B > 1:
+            bias[1, :min(Lk, 40)] = 0
+    ref = O.attention(q, k, v, H, bias)
+    got = _xattn(L, q, k, v, H, bias)
+    assert rel_l2(got, ref) < 2e-3, rel_l2(got, ref)
+
+
+@pytest.mark.parametrize("B,S,F", [(2, 32, 2880), (1, 16, 64), (1, 3, 5), (2, 1, 8)])
+def test_dwconv_glu(L, B, S, F):
+    rng = np.random.default_rng(S + F)
+    E = 2 * F
+    x = f16(rng.standard_normal((B, S, S, E)))
+    w = (rng.standard_normal((E, 3, 3)) * 0.3).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    d = O.depthwise3x3(x, w, bias)
+    ref = d[..., :F] * (d[..., F:] / (1 + np.exp(-d[..., F:])))
+    wt = np.ascontiguousarray(w.reshape(E, 9).T)
+    dx, dw, db = dev(x, torch.float16), dev(wt, torch.float32), dev(bias, torch.float32)
+    out = torch.empty((B * S * S, F), device="cuda", dtype=torch.float16)
+    L.check(L.lib().sana_hip_dwconv_glu(dx.data_ptr(), E, dw.data_ptr(), db.data_ptr(), out.data_ptr(), F, B, S, S, F,
+                                        stream()))
+    got = host(out).reshape(B, S, S, F)
+    assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
