@@ -215,3 +215,34 @@ def gguf_index(path):
                                           ctypes.byref(off)))
         out.append((name.value.decode(), tuple(shape[:nd.value]), ty.value, off.value))
     return out
+
+
+def manifest(layers=28, hidden=1152, ffn=5760, caption_dim=2304, latent_channels=32, time_freq=256):
+    """{GGUF tensor name: PyTorch-order shape} of the three weight files the
+    loader reads (src/transformer.cpp:171-190 caption, :214-308 per block,
+    :473-484 denoiser)."""
+    C, E = hidden, ffn
+    shapes = {}
+    for i in range(layers):
+        p = f"transformer_blocks.{i}."
+        shapes.update({
+            p + "scale_shift_table": (6, C), p + "attn1.to_q.weight": (C, C), p + "attn1.to_k.weight": (C, C),
+            p + "attn1.to_v.weight": (C, C), p + "attn1.to_out.0.weight": (C, C), p + "attn1.to_out.0.bias": (C,),
+            p + "attn2.to_q.weight": (C, C), p + "attn2.to_q.bias": (C,), p + "attn2.to_k.weight": (C, C),
+            p + "attn2.to_k.bias": (C,), p + "attn2.to_v.weight": (C, C), p + "attn2.to_v.bias": (C,),
+            p + "attn2.to_out.0.weight": (C, C), p + "attn2.to_out.0.bias": (C,),
+            p + "ff.conv_inverted.weight": (E, C, 1, 1), p + "ff.conv_inverted.bias": (E,),
+            p + "ff.conv_depth.weight": (E, 1, 3, 3), p + "ff.conv_depth.bias": (E,),
+            p + "ff.conv_point.weight": (C, E // 2, 1, 1)})
+    shapes.update({
+        "caption_projection.linear_1.weight": (C, caption_dim), "caption_projection.linear_1.bias": (C,),
+        "caption_projection.linear_2.weight": (C, C), "caption_projection.linear_2.bias": (C,),
+        "patch_embed.proj.weight": (C, latent_channels, 1, 1), "patch_embed.proj.bias": (C,),
+        "time_embed.emb.timestep_embedder.linear_1.weight": (C, time_freq),
+        "time_embed.emb.timestep_embedder.linear_1.bias": (C,),
+        "time_embed.emb.timestep_embedder.linear_2.weight": (C, C),
+        "time_embed.emb.timestep_embedder.linear_2.bias": (C,),
+        "time_embed.linear.weight": (6 * C, C), "time_embed.linear.bias": (6 * C,),
+        "caption_norm.weight": (C,), "scale_shift_table": (2, C), "proj_out.weight": (latent_channels, C),
+        "proj_out.bias": (latent_channels,)})
+    return shapes
