@@ -331,6 +331,32 @@ void block_forward(const oracle_block_weights & w, const float * x, const float 
     for (size_t i = 0; i < M * C; ++i) after_ff[i] = after_cross[i] + br[i];
 }
 
+// attention_block_3d (src/transformer_ops.cpp:545-570).
+void attention_block(const float * x, const float * wq, const float * bq, const float * wk, const float * bk,
+                     const float * wv, const float * bv, const float * wo, const float * bo, float * out, size_t B,
+                     size_t N, size_t C, size_t heads) {
+    const size_t M = B * N;
+    std::vector<float> q(M * C), k(M * C), v(M * C), o(M * C);
+    linear(x, wq, bq, q.data(), M, C, C);
+    linear(x, wk, bk, k.data(), M, C, C);
+    linear(x, wv, bv, v.data(), M, C, C);
+    linear_attention(q.data(), k.data(), v.data(), o.data(), C, B, N, N, heads, C / heads);
+    linear(o.data(), wo, bo, out, M, C, C);
+}
+
+// cross_attention_block_3d (src/transformer_ops.cpp:572-608).
+void cross_attention_block(const float * x, const float * ctx, const float * bias, const float * wq, const float * bq,
+                           const float * wk, const float * bk, const float * wv, const float * bv, const float * wo,
+                           const float * bo, float * out, size_t B, size_t N, size_t L, size_t C, size_t heads) {
+    const size_t M = B * N;
+    std::vector<float> q(M * C), k(B * L * C), v(B * L * C), o(M * C);
+    linear(x, wq, bq, q.data(), M, C, C);
+    linear(ctx, wk, bk, k.data(), B * L, C, C);
+    linear(ctx, wv, bv, v.data(), B * L, C, C);
+    attention(q.data(), k.data(), v.data(), bias, o.data(), C, C, B, N, L, heads, C / heads);
+    linear(o.data(), wo, bo, out, M, C, C);
+}
+
 // ---------------------------------------------------------------- randn
 // torch CPU randn as restated in src/torch_rng.cpp:14-68: one mt19937 draw per
 // element mapped to a 24-bit uniform, then Box-Muller over blocks of 16
@@ -393,37 +419,51 @@ float lambda_of(float sigma) {  // flow sigmas: alpha = 1 - sigma (src/scheduler
     return std::log(1.0f - sigma) - std::log(sigma);
 }
 
-// step_sana_scheduler (src/scheduler.cpp:272-318) with order 2, midpoint, lower_order_final.
+// convert_sana_scheduler_model_output (src/scheduler.cpp:155-173): x0 = sample - sigma * v.
+void sched_convert(const float * mo, const float * sample, size_t n, float sigma, float * out) {
+    for (size_t i = 0; i < n; ++i) out[i] = sample[i] - sigma * mo[i];
+}
+
+// sana_scheduler_first_order_update (src/scheduler.cpp:175-205).
+void sched_first(const float * conv, const float * sample, size_t n, float st_v, float ss_v, float * out) {
+    const float alpha_t = 1.0f - st_v, sigma_t = st_v, sigma_s = ss_v;
+    const float h = lambda_of(st_v) - lambda_of(ss_v);
+    const float a = sigma_t / sigma_s, bcoef = -alpha_t * (std::exp(-h) - 1.0f);
+    for (size_t i = 0; i < n; ++i) out[i] = a * sample[i] + bcoef * conv[i];
+}
+
+// sana_scheduler_second_order_update, midpoint (src/scheduler.cpp:207-260).
+void sched_second(const float * sample, const float * m0, const float * m1, size_t n, float st_v, float s0_v,
+                  float s1_v, float * out) {
+    const float alpha_t = 1.0f - st_v, sigma_t = st_v, sigma_s0 = s0_v;
+    const float lt = lambda_of(st_v), l0 = lambda_of(s0_v), l1 = lambda_of(s1_v);
+    const float h = lt - l0, h0 = l0 - l1, r0 = h0 / h;
+    const float a = sigma_t / sigma_s0, bcoef = -alpha_t * (std::exp(-h) - 1.0f);
+    const float ccoef = -0.5f * alpha_t * (std::exp(-h) - 1.0f);
+    for (size_t i = 0; i < n; ++i) {
+        const float d1 = (1.0f / r0) * (m0[i] - m1[i]);
+        out[i] = a * sample[i] + bcoef * m0[i] + ccoef * d1;
+    }
+}
+
+// step_sana_scheduler (src/scheduler.cpp:272-318) with order 2, midpoint,
+// lower_order_final: first order at the first and last step, second order
+// otherwise (the "lower_order_second" branch also takes the second-order path).
 std::vector<float> sched_step(const std::vector<float> & model_out, const std::vector<float> & sample, SchedState & st) {
     const size_t n = sample.size();
-    const float sigma_now = st.sig[st.step];
     std::vector<float> conv(n);
-    for (size_t i = 0; i < n; ++i) conv[i] = sample[i] - sigma_now * model_out[i];
+    sched_convert(model_out.data(), sample.data(), n, st.sig[st.step], conv.data());
     st.prev.push_back(conv);
     if (st.prev.size() > 2) st.prev.erase(st.prev.begin());
     const bool last = st.step == st.ts.size() - 1;
-    const bool second_last = (st.step == st.ts.size() - 2) && st.ts.size() < 15;
     std::vector<float> out(n);
     if (st.lower < 1 || last) {
-        const float st_v = st.sig[st.step + 1], ss_v = st.sig[st.step];
-        const float alpha_t = 1.0f - st_v, sigma_t = st_v, sigma_s = ss_v;
-        const float h = lambda_of(st_v) - lambda_of(ss_v);
-        const float a = sigma_t / sigma_s, bcoef = -alpha_t * (std::exp(-h) - 1.0f);
-        for (size_t i = 0; i < n; ++i) out[i] = a * sample[i] + bcoef * conv[i];
+        sched_first(conv.data(), sample.data(), n, st.sig[st.step + 1], st.sig[st.step], out.data());
     } else {
-        (void)second_last;  // order 2 takes the same branch either way
-        const float st_v = st.sig[st.step + 1], s0_v = st.sig[st.step], s1_v = st.sig[st.step - 1];
-        const float alpha_t = 1.0f - st_v, sigma_t = st_v, sigma_s0 = s0_v;
-        const float lt = lambda_of(st_v), l0 = lambda_of(s0_v), l1 = lambda_of(s1_v);
         const std::vector<float> & m0 = st.prev.back();
         const std::vector<float> & m1 = st.prev[st.prev.size() - 2];
-        const float h = lt - l0, h0 = l0 - l1, r0 = h0 / h;
-        const float a = sigma_t / sigma_s0, bcoef = -alpha_t * (std::exp(-h) - 1.0f);
-        const float ccoef = -0.5f * alpha_t * (std::exp(-h) - 1.0f);
-        for (size_t i = 0; i < n; ++i) {
-            const float d1 = (1.0f / r0) * (m0[i] - m1[i]);
-            out[i] = a * sample[i] + bcoef * m0[i] + ccoef * d1;
-        }
+        sched_second(sample.data(), m0.data(), m1.data(), n, st.sig[st.step + 1], st.sig[st.step],
+                     st.sig[st.step - 1], out.data());
     }
     if (st.lower < 2) st.lower += 1;
     st.step += 1;
@@ -625,6 +665,37 @@ int oracle_block_forward(const oracle_block_weights * w, const float * x, const 
     return guard([&] { block_forward(*w, x, ctx, t_mod, bias, B, N, L, a, c, f); });
 }
 
+int oracle_attention_block(const float * x, const float * wq, const float * bq, const float * wk, const float * bk,
+                           const float * wv, const float * bv, const float * wo, const float * bo, float * out,
+                           size_t B, size_t N, size_t C, size_t heads) {
+    if (heads == 0 || C % heads != 0) return fail("hidden size must be divisible by num_heads");
+    return guard([&] { attention_block(x, wq, bq, wk, bk, wv, bv, wo, bo, out, B, N, C, heads); });
+}
+
+int oracle_cross_attention_block(const float * x, const float * ctx, const float * bias, const float * wq,
+                                 const float * bq, const float * wk, const float * bk, const float * wv,
+                                 const float * bv, const float * wo, const float * bo, float * out, size_t B,
+                                 size_t N, size_t L, size_t C, size_t heads) {
+    if (heads == 0 || C % heads != 0) return fail("hidden size must be divisible by num_heads");
+    return guard([&] { cross_attention_block(x, ctx, bias, wq, bq, wk, bk, wv, bv, wo, bo, out, B, N, L, C, heads); });
+}
+
+int oracle_sched_convert(const float * mo, const float * sample, size_t n, float sigma, float * out) {
+    sched_convert(mo, sample, n, sigma, out);
+    return 0;
+}
+
+int oracle_sched_first_order(const float * conv, const float * sample, size_t n, float st, float ss, float * out) {
+    sched_first(conv, sample, n, st, ss, out);
+    return 0;
+}
+
+int oracle_sched_second_order(const float * sample, const float * m0, const float * m1, size_t n, float st,
+                              float s0, float s1, float * out) {
+    sched_second(sample, m0, m1, n, st, s0, s1, out);
+    return 0;
+}
+
 oracle_model * oracle_model_create(size_t layers, size_t hidden, size_t ffn, size_t caption_dim, size_t latent,
                                    size_t self_heads, size_t cross_heads) {
     auto * m = new oracle_model();
@@ -677,7 +748,7 @@ int oracle_model_get(const oracle_model * m, const char * name, float * out, siz
 }
 
 uint64_t oracle_digest(const float * data, size_t n) {
-    uint64_t h = 1469598103934665603ULL;
+    uint64_t h = 14695981039346656037ULL;
     const unsigned char * p = reinterpret_cast<const unsigned char *>(data);
     for (size_t i = 0; i < n * 4; ++i) {
         h ^= p[i];

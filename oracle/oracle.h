@@ -67,6 +67,27 @@ int oracle_timestep_embedding(const float * t, float * out, size_t B, size_t dim
 /* u + g (c - u); src/transformer.cpp:570-602. */
 int oracle_cfg(const float * noise_pred, float * out, size_t half_numel, float guidance);
 
+/* attention_block_3d (src/transformer_ops.cpp:545-570): x [B,N,C]; linear
+ * weights PyTorch order [C,C]; any bias may be NULL. */
+int oracle_attention_block(const float * x, const float * wq, const float * bq, const float * wk, const float * bk,
+                           const float * wv, const float * bv, const float * wo, const float * bo, float * out,
+                           size_t B, size_t N, size_t C, size_t heads);
+/* cross_attention_block_3d (src/transformer_ops.cpp:572-608): x [B,N,C],
+ * context [B,L,C], bias [B,L] or NULL. */
+int oracle_cross_attention_block(const float * x, const float * ctx, const float * bias, const float * wq,
+                                 const float * bq, const float * wk, const float * bk, const float * wv,
+                                 const float * bv, const float * wo, const float * bo, float * out, size_t B,
+                                 size_t N, size_t L, size_t C, size_t heads);
+
+/* DPM-Solver++ pieces of src/scheduler.cpp with explicit sigmas (flow sigmas:
+ * alpha = 1 - sigma).  convert: :155-173; first order: :175-205; second
+ * order (midpoint): :207-270. */
+int oracle_sched_convert(const float * model_out, const float * sample, size_t n, float sigma, float * out);
+int oracle_sched_first_order(const float * converted, const float * sample, size_t n, float sigma_t, float sigma_s,
+                             float * out);
+int oracle_sched_second_order(const float * sample, const float * m0, const float * m1, size_t n, float sigma_t,
+                              float sigma_s0, float sigma_s1, float * out);
+
 /* One DiT block with explicit weights (all 26 tensors of SanaBlockWeights,
  * src/transformer.h:26-55).  t_mod [B, 6C]; context [B, L, C]; bias [B, L] or NULL. */
 typedef struct {

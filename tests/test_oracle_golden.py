@@ -1,0 +1,99 @@
+"""Pins the CPU oracle bit for bit against the reference's own CPU code.
+
+The fixtures in tests/golden/ were written by tests/golden/make_golden.py from
+oracle/_ref/ref_harness, i.e. the reference's src/*.cpp compiled from source
+with the same flags as the oracle.  Same seeded inputs and weights here; every
+comparison is on the SHA-256 of the fp32 bytes (bit-exact), plus the stored
+subsample for a readable diff when it fails.
+"""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load(name):
+    path = os.path.join(GOLDEN, name + ".npz")
+    return np.load(path, allow_pickle=False)
+
+
+def check_tensor(fx, name, got):
+    got = np.ascontiguousarray(got, np.float32)
+    stride = int(fx[name + "__stride"])
+    sub = fx[name + "__sub"]
+    diff = np.abs(got.reshape(-1)[::stride] - sub)
+    assert hashlib.sha256(got.tobytes()).hexdigest() == str(fx[name + "__sha256"]), \
+        f"{name}: not bit-exact (subsample max |diff| {diff.max():.3e})"
+
+
+@pytest.fixture(scope="module")
+def model():
+    # The reference harness draws every weight from the 28-block manifest
+    # (seed = 1000 + sorted index), so the oracle model is the full one.
+    return O.Model(layers=28, self_heads=36, cross_heads=16)
+
+
+def test_fnv_digest_function():
+    # 64-bit FNV-1a of "" and of the bytes of 1.0f, from the published definition.
+    h = 0xcbf29ce484222325
+    for b in np.float32(1.0).tobytes():
+        h = ((h ^ b) * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
+    assert O.digest(np.array([1.0], np.float32)) == h
+
+
+def test_weight_digests(model):
+    fx = load("weights")
+    shapes = {}
+    import sana_dit
+    shapes = sana_dit.manifest(28)
+    assert sorted(shapes) == sorted(fx["names"].tolist())
+    for name, want in zip(fx["names"].tolist(), fx["fnv1a"].tolist()):
+        got = O.digest(model.get(name, shapes[name]))
+        assert got == want, name
+
+
+@pytest.mark.parametrize("case,heads", [("cfg1_self16", 16), ("cfg1_self36", 36)])
+def test_single_block(model, case, heads):
+    fx = load(case)
+    m = model if heads == 36 else None
+    if m is None:
+        m = O.Model(layers=28, self_heads=heads, cross_heads=16)
+    latent = O.randn((1, 32, 16, 16), 42)
+    x = m.patch_embed(latent)
+    emb, tmod = m.time(np.array([500.0], np.float32))
+    ctx = O.randn((1, 300, 1152), 43)
+    check_tensor(fx, "x", x)
+    check_tensor(fx, "t_mod", tmod)
+    a, c, f = m.block(0, x, ctx, tmod)
+    check_tensor(fx, "after_self", a)
+    check_tensor(fx, "after_cross", c)
+    check_tensor(fx, "after_ff", f)
+
+
+@pytest.mark.parametrize("case,masked", [("cfg2", False), ("cfg2_mask", True)])
+def test_full_forward_1024px(model, case, masked):
+    fx = load(case)
+    latent = O.randn((1, 32, 32, 32), 42)
+    caption = O.randn((2, 300, 2304), 43)
+    ctx = model.project_caption(caption)
+    check_tensor(fx, "context", ctx)
+    bias = O.mask_bias(300, 1, 40) if masked else None
+    np_ = model.forward(latent, ctx, 999.0, bias)
+    check_tensor(fx, "noise_pred", np_)
+    guided = np_[:1] + np.float32(4.5) * (np_[1:] - np_[:1])
+    check_tensor(fx, "guided", guided)
+
+
+@pytest.mark.skipif(os.environ.get("SANA_SLOW_ORACLE") != "1",
+                    reason="20 full forwards on the CPU (~10 min); set SANA_SLOW_ORACLE=1")
+def test_denoise_loop_1024px(model):
+    fx = load("cfg3")
+    latent = O.randn((1, 32, 32, 32), 42)
+    caption = O.randn((2, 300, 2304), 43)
+    fin = model.loop(latent, caption, 20, 4.5)
+    check_tensor(fx, "final_latent", fin)
