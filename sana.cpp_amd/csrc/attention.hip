@@ -11,111 +11,223 @@ namespace {
 // K3: linear attention (src/transformer_ops.cpp:496-537).  Per (b, h) the
 // state is the (D+1) x D matrix S[r][d] = sum_t v[t][r] relu(k[t][d]) with the
 // extra row r = D holding ksum[d] = sum_t relu(k[t][d]) (the "padded
-// denominator column").  The token reduction is split over chunks (one
-// workgroup each), the chunk partials are summed in fixed order by a second
-// kernel (deterministic, no atomics), and a third kernel applies
-// out[t][r] = sum_d S[r][d] relu(q[t][d]) / (sum_d S[D][d] relu(q[t][d]) + 1e-15).
+// denominator column"); then
+//   out[t][r] = sum_d S[r][d] relu(q[t][d]) / (sum_d S[D][d] relu(q[t][d]) + 1e-15).
+//
+// la_state_kernel: one wave per (token chunk, h, b).  Sub-chunks of 64 tokens
+//   of relu(K) and V are staged in LDS transposed (token-contiguous rows), so
+//   S^T = relu(K)^T . V is a chain of v_mfma_f32_32x32x16_f16 over tokens with
+//   16-byte operand reads; fp32 accumulation of exact fp16 products.  ksum is
+//   summed on the VALU from the same LDS rows.  Each chunk writes its partial
+//   (D+1) x D state.
+// la_reduce_kernel: sums the chunk partials in fixed chunk order (no atomics,
+//   bit-reproducible) into an fp16 hi/lo pair of the state.
+// la_apply_kernel: relu(Q) . [S | ksum]^T on MFMA (hi and lo halves), one wave
+//   per 32 tokens, then the division by the denominator column.
 
-constexpr int kLaTok = 32;      // tokens per LDS sub-tile
-constexpr int kLaChunk = 256;   // tokens per partial-state workgroup
-constexpr int kLaApplyTok = 32; // tokens per apply workgroup
+constexpr int kLaSub = 64;                 // tokens per LDS sub-chunk
+constexpr int kLaChunks = 16;              // partial states per (b, h)
+constexpr int kLaRow = kLaSub + 8;         // halves per transposed LDS row (144 B: conflict-free reads)
 
-template <int EPT>
-__global__ __launch_bounds__(256) void la_state_kernel(const f16 * __restrict__ k, const f16 * __restrict__ v,
-                                                       int64_t ld, int N, int H, int D, int nch,
-                                                       float * __restrict__ part) {
-    __shared__ float Ks[kLaTok][128];
-    __shared__ float Vs[kLaTok][129];
+template <int TD>  // ceil(D / 32): 32x32 MFMA tiles per side of the state
+__global__ __launch_bounds__(64) void la_state_kernel(const f16 * __restrict__ k, const f16 * __restrict__ v,
+                                                      int64_t ld, int N, int H, int D, int T, int nch, int vec,
+                                                      float * __restrict__ part) {
+    constexpr int DP = TD * 32;
+    __shared__ __attribute__((aligned(16))) f16 Kt[DP][kLaRow];
+    __shared__ __attribute__((aligned(16))) f16 Vt[DP][kLaRow];
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x;
-    const int E = (D + 1) * D;
-    const int t0 = c * kLaChunk, t1 = min(N, t0 + kLaChunk);
-    float acc[EPT];
-    int er[EPT], ed[EPT];
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        acc[e] = 0.0f;
-        const int g = tid + 256 * e;
-        // entries past E read row D / column 0 (in bounds) and are never stored
-        er[e] = g < E ? g / D : D;
-        ed[e] = g < E ? g - er[e] * D : 0;
+    const int lane = threadIdx.x;
+    for (int i = lane; i < DP * kLaRow; i += 64) {
+        (&Kt[0][0])[i] = (f16)0.0f;
+        (&Vt[0][0])[i] = (f16)0.0f;
     }
-    for (int ts = t0; ts < t1; ts += kLaTok) {
-        for (int idx = tid; idx < kLaTok * D; idx += 256) {
-            const int t = idx / D, d = idx - t * D;
-            const int gt = ts + t;
-            float kv = 0.0f, vv = 0.0f;
-            if (gt < t1) {
-                const int64_t off = ((int64_t)b * N + gt) * ld + (int64_t)h * D + d;
-                kv = fmaxf(0.0f, (float)k[off]);
-                vv = (float)v[off];
+    f32x16 acc[TD][TD];
+#pragma unroll
+    for (int i = 0; i < TD; ++i)
+#pragma unroll
+        for (int j = 0; j < TD; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    float ks[(DP + 63) / 64];
+#pragma unroll
+    for (int i = 0; i < (DP + 63) / 64; ++i) ks[i] = 0.0f;
+
+    const int t_begin = c * T, t_end = min(N, t_begin + T);
+    const f16 * kb = k + (int64_t)b * N * ld + (int64_t)h * D;
+    const f16 * vb = v + (int64_t)b * N * ld + (int64_t)h * D;
+    const int G = D / 8;
+    for (int t0 = t_begin; t0 < t_end; t0 += kLaSub) {
+        __syncthreads();
+        if (vec) {
+            for (int idx = lane; idx < kLaSub * G; idx += 64) {
+                const int t = idx / G, g = idx - t * G;
+                const int gt = t0 + t;
+                f16x8 kv, vv;
+                if (gt < t_end) {
+                    kv = *reinterpret_cast<const f16x8 *>(kb + (int64_t)gt * ld + g * 8);
+                    vv = *reinterpret_cast<const f16x8 *>(vb + (int64_t)gt * ld + g * 8);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) kv[e] = vv[e] = (f16)0.0f;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    Kt[g * 8 + e][t] = kv[e] > (f16)0.0f ? kv[e] : (f16)0.0f;
+                    Vt[g * 8 + e][t] = vv[e];
+                }
             }
-            Ks[t][d] = kv;
-            Vs[t][d] = vv;
+        } else {
+            for (int idx = lane; idx < kLaSub * D; idx += 64) {
+                const int t = idx / D, d = idx - t * D;
+                const int gt = t0 + t;
+                f16 kv = (f16)0.0f, vv = (f16)0.0f;
+                if (gt < t_end) {
+                    kv = kb[(int64_t)gt * ld + d];
+                    vv = vb[(int64_t)gt * ld + d];
+                }
+                Kt[d][t] = kv > (f16)0.0f ? kv : (f16)0.0f;
+                Vt[d][t] = vv;
+            }
         }
-        if (tid < kLaTok) Vs[tid][D] = 1.0f;
         __syncthreads();
-#pragma unroll 4
-        for (int t = 0; t < kLaTok; ++t) {
 #pragma unroll
-            for (int e = 0; e < EPT; ++e) acc[e] += Vs[t][er[e]] * Ks[t][ed[e]];
+        for (int i = 0; i < (DP + 63) / 64; ++i) {
+            const int d = lane + 64 * i;
+            if (d < D) {
+                float s = 0.0f;
+                for (int t = 0; t < kLaSub; t += 8) {
+                    const f16x8 x = *reinterpret_cast<const f16x8 *>(&Kt[d][t]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) s += (float)x[e];
+                }
+                ks[i] += s;
+            }
         }
-        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kLaSub; kk += 16) {
+            const int col = kk + 8 * (lane >> 5);
+            f16x8 af[TD], bf[TD];
+#pragma unroll
+            for (int i = 0; i < TD; ++i) af[i] = *reinterpret_cast<const f16x8 *>(&Kt[i * 32 + (lane & 31)][col]);
+#pragma unroll
+            for (int j = 0; j < TD; ++j) bf[j] = *reinterpret_cast<const f16x8 *>(&Vt[j * 32 + (lane & 31)][col]);
+#pragma unroll
+            for (int i = 0; i < TD; ++i)
+#pragma unroll
+                for (int j = 0; j < TD; ++j) acc[i][j] = mfma_32x32x16(af[i], bf[j], acc[i][j]);
+        }
     }
+    // acc[i][j]: lane holds r = j*32 + (lane & 31) and d = i*32 + 8*(q/4) + 4*(lane/32) + q%4.
+    const int E = (D + 1) * D;
     float * out = part + (((int64_t)b * H + h) * nch + c) * E;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        const int g = tid + 256 * e;
-        if (g < E) out[g] = acc[e];
+    for (int i = 0; i < TD; ++i)
+#pragma unroll
+        for (int j = 0; j < TD; ++j) {
+            const int r = j * 32 + (lane & 31);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int d = i * 32 + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                if (r < D && d < D) out[r * D + d] = acc[i][j][q];
+            }
+        }
+#pragma unroll
+    for (int i = 0; i < (DP + 63) / 64; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) out[D * D + d] = ks[i];
     }
 }
 
-__global__ __launch_bounds__(256) void la_reduce_kernel(const float * __restrict__ part, int nch, int E,
-                                                        float * __restrict__ state) {
-    const int bh = blockIdx.x;
-    for (int e = threadIdx.x; e < E; e += 256) {
-        float s = 0.0f;
-        for (int c = 0; c < nch; ++c) s += part[((int64_t)bh * nch + c) * E + e];
-        state[(int64_t)bh * E + e] = s;
+// Sums the chunk partials in fixed order and writes the state, transposed to
+// the apply kernel's MFMA operand layout, as an fp16 hi/lo pair:
+// S[r][d] = hi[r][d] + lo[r][d] with hi = f16(S), lo = f16(S - hi), so the fp16
+// products of the apply step carry the fp32 state to ~2^-22 relative error.
+// Layout [NP][KP] (r rows incl. the ksum row r = D, d contiguous), zero padded.
+__global__ __launch_bounds__(256) void la_reduce_kernel(const float * __restrict__ part, int nch, int D, int NP, int KP,
+                                                        f16 * __restrict__ hi, f16 * __restrict__ lo) {
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    const int bh = blockIdx.y;
+    if (e >= NP * KP) return;
+    const int r = e / KP, d = e - r * KP;
+    float s = 0.0f;
+    if (r <= D && d < D) {
+        const int E = (D + 1) * D;
+        const float * p = part + (int64_t)bh * nch * E + r * D + d;
+        for (int c = 0; c < nch; ++c) s += p[(int64_t)c * E];
     }
+    const f16 h = (f16)s;
+    hi[(int64_t)bh * NP * KP + e] = h;
+    lo[(int64_t)bh * NP * KP + e] = (f16)(s - (float)h);
 }
 
+// out[t][r] = (relu(q) . S^T)[t][r] / ((relu(q) . S^T)[t][D] + 1e-15) on
+// v_mfma_f32_32x32x16_f16: one wave per 32 tokens of one (b, h).  The A
+// operand (8 consecutive head dims of one token) comes straight from the
+// token-major q rows; columns past D are masked to zero.
+template <int NT, int KS>  // NT: 32-wide column tiles of [S | ksum]; KS: 16-deep steps over d
 __global__ __launch_bounds__(256) void la_apply_kernel(const f16 * __restrict__ q, int64_t ld,
-                                                       const float * __restrict__ state, f16 * __restrict__ out,
-                                                       int64_t ldo, int N, int H, int D) {
-    extern __shared__ float smem[];
-    // St[d][r] (r = 0..D, transposed so consecutive r are contiguous), Qs[t][d], den[t].
-    float * St = smem;                          // D * (D + 1)
-    float * Qs = St + D * (D + 1);              // kLaApplyTok * D
-    float * den = Qs + kLaApplyTok * D;         // kLaApplyTok
-    const int tb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x;
-    const int E = (D + 1) * D;
-    const float * S = state + ((int64_t)b * H + h) * E;
-    for (int e = tid; e < E; e += 256) {
-        const int r = e / D, d = e - r * D;
-        St[d * (D + 1) + r] = S[e];
+                                                       const f16 * __restrict__ shi, const f16 * __restrict__ slo,
+                                                       f16 * __restrict__ out, int64_t ldo, int N, int H, int D,
+                                                       int vec) {
+    constexpr int NP = NT * 32, KP = KS * 16;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int t0 = (blockIdx.x * 4 + w) * 32;
+    if (t0 >= N) return;
+    const int trow = min(t0 + (lane & 31), N - 1);
+    const f16 * qr = q + ((int64_t)b * N + trow) * ld + (int64_t)h * D;
+    const int64_t sbase = ((int64_t)b * H + h) * NP * KP;
+    f32x16 acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[j][i] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+        const int d0 = kk * 16 + 8 * (lane >> 5);
+        f16x8 af;
+        if (vec && d0 + 8 <= D) {
+            af = *reinterpret_cast<const f16x8 *>(qr + d0);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) af[e] = af[e] > (f16)0.0f ? af[e] : (f16)0.0f;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const f16 x = d0 + e < D ? qr[d0 + e] : (f16)0.0f;
+                af[e] = x > (f16)0.0f ? x : (f16)0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int64_t off = sbase + (int64_t)(j * 32 + (lane & 31)) * KP + kk * 16 + 8 * (lane >> 5);
+            const f16x8 bh = *reinterpret_cast<const f16x8 *>(shi + off);
+            const f16x8 bl = *reinterpret_cast<const f16x8 *>(slo + off);
+            acc[j] = mfma_32x32x16(af, bh, acc[j]);
+            acc[j] = mfma_32x32x16(af, bl, acc[j]);
+        }
     }
-    const int t0 = tb * kLaApplyTok;
-    for (int idx = tid; idx < kLaApplyTok * D; idx += 256) {
-        const int t = idx / D, d = idx - t * D;
-        const int gt = t0 + t;
-        Qs[idx] = gt < N ? fmaxf(0.0f, (float)q[((int64_t)b * N + gt) * ld + (int64_t)h * D + d]) : 0.0f;
+    // Lane holds column r = 32 j + (lane & 31), rows t0 + 8*(i/4) + 4*(lane/32) + i%4.
+    // The denominator is column D, held by lane (lane & 32) | (D % 32) of tile D / 32.
+    const int jd = D >> 5, cd = D & 31;
+    float den[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+            if (j == jd) v = acc[j][i];
+        den[i] = __shfl(v, (lane & 32) | cd, 64) + 1e-15f;
     }
-    __syncthreads();
-    if (tid < kLaApplyTok) {
-        float s = 0.0f;
-        for (int d = 0; d < D; ++d) s += St[d * (D + 1) + D] * Qs[tid * D + d];
-        den[tid] = s + 1e-15f;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < kLaApplyTok * D; idx += 256) {
-        const int t = idx / D, r = idx - t * D;
-        const int gt = t0 + t;
-        if (gt >= N) continue;
-        float s = 0.0f;
-        for (int d = 0; d < D; ++d) s += St[d * (D + 1) + r] * Qs[t * D + d];
-        out[((int64_t)b * N + gt) * ldo + (int64_t)h * D + r] = (f16)(s / den[t]);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int r = j * 32 + (lane & 31);
+        if (r >= D) continue;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int t = t0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+            if (t < N) out[((int64_t)b * N + t) * ldo + (int64_t)h * D + r] = (f16)(acc[j][i] / den[i]);
+        }
     }
 }
 
@@ -248,6 +360,162 @@ __global__ __launch_bounds__(256) void xattn_kernel(const f16 * __restrict__ q, 
     }
 }
 
+// Fast path of K4 for L <= 32 * LT (<= 320 keys) and D <= 96, D % 8 == 0.
+// One workgroup per (b, h, 128 queries); the head's K [keys][d] and V^T
+// [d][keys] are staged in LDS once and shared by the 4 waves (32 queries
+// each).  Scores are computed transposed, S^T = K . Q^T on
+// v_mfma_f32_32x32x16_f16, so each lane holds one query column: the softmax
+// max and sum over keys are in-lane plus one cross-half shuffle.  exp(S^T) in
+// fp16 then feeds O^T = V^T . P^T directly from registers as the B operand; the
+// key order inside each 16-key MFMA step is permuted identically in both
+// operands (lane half h supplies keys 4h..4h+3 and 8+4h..8+4h+3), which leaves
+// the sum over keys unchanged.  Keys >= L get probability exactly 0.
+constexpr int kXaQ = 128;  // queries per workgroup
+template <int LT>
+__global__ __launch_bounds__(256) void xattn_fast_kernel(const f16 * __restrict__ q, int64_t ldq,
+                                                         const f16 * __restrict__ k, int64_t ldk,
+                                                         const f16 * __restrict__ vt, int64_t ldvt,
+                                                         const float * __restrict__ bias, f16 * __restrict__ out,
+                                                         int64_t ldo, int N, int L, int H, int D, float scale) {
+    constexpr int LP = LT * 32;
+    constexpr int KROW = 96 + 8;    // halves per K row (d padded, 208 B rows)
+    constexpr int VROW = LP + 8;    // halves per V^T row
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    f16 * Ks = reinterpret_cast<f16 *>(smem);                       // [LP][KROW]
+    f16 * Vs = Ks + LP * KROW;                                       // [96][VROW]
+    float * bs = reinterpret_cast<float *>(Vs + 96 * VROW);          // [LP]
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int KS = (D + 15) / 16;   // 16-deep steps over head dims
+    const int DT = (D + 31) / 32;   // 32-wide output dim tiles
+    // stage K rows (zero past D and past L), V^T rows (zero past D; keys past L are zero in vt), bias
+    const f16 * kb = k + (int64_t)b * L * ldk + (int64_t)h * D;
+    for (int idx = tid; idx < LP * (KROW / 8); idx += 256) {
+        const int key = idx / (KROW / 8), c8 = (idx - key * (KROW / 8)) * 8;
+        f16x8 v8;
+        if (key < L && c8 < D) {
+            v8 = *reinterpret_cast<const f16x8 *>(kb + (int64_t)key * ldk + c8);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v8[e] = (f16)0.0f;
+        }
+        *reinterpret_cast<f16x8 *>(Ks + key * KROW + c8) = v8;
+    }
+    const f16 * vb = vt + ((int64_t)b * H * D + (int64_t)h * D) * ldvt;
+    for (int idx = tid; idx < 96 * (VROW / 8); idx += 256) {
+        const int dim = idx / (VROW / 8), c8 = (idx - dim * (VROW / 8)) * 8;
+        f16x8 v8;
+        if (dim < D && c8 < LP) {
+            v8 = *reinterpret_cast<const f16x8 *>(vb + (int64_t)dim * ldvt + c8);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v8[e] = (f16)0.0f;
+        }
+        *reinterpret_cast<f16x8 *>(Vs + dim * VROW + c8) = v8;
+    }
+    for (int key = tid; key < LP; key += 256) bs[key] = (key < L && bias) ? bias[(int64_t)b * L + key] : 0.0f;
+    __syncthreads();
+
+    const int q0 = blockIdx.x * kXaQ + w * 32;
+    if (q0 >= N) return;
+    const int hh = lane >> 5;
+    const int qcol = min(q0 + (lane & 31), N - 1);
+    const f16 * qr = q + ((int64_t)b * N + qcol) * ldq + (int64_t)h * D;
+
+    // S^T[key][q]: tile t holds keys 32t + 8*(i/4) + 4*hh + i%4 for the lane's query.
+    f32x16 st[LT];
+#pragma unroll
+    for (int t = 0; t < LT; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st[t][i] = 0.0f;
+    for (int ks = 0; ks < KS; ++ks) {
+        const int d0 = ks * 16 + 8 * hh;
+        f16x8 qf;
+        if (d0 + 8 <= D) {
+            qf = *reinterpret_cast<const f16x8 *>(qr + d0);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[e] = (f16)0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < LT; ++t) {
+            const f16x8 kf = *reinterpret_cast<const f16x8 *>(Ks + (t * 32 + (lane & 31)) * KROW + d0);
+            st[t] = mfma_32x32x16(kf, qf, st[t]);
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < LT; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int key = t * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+            const float sv = key < L ? st[t][i] * scale + bs[key] : -INFINITY;
+            st[t][i] = sv;
+            mx = fmaxf(mx, sv);
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.0f;
+    f16x8 pf[LT][2];  // P^T as the B operand: [tile][16-key step], slot u -> i = 8*step + u
+#pragma unroll
+    for (int t = 0; t < LT; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int key = t * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+            const float e = key < L ? expf(st[t][i] - mx) : 0.0f;
+            sum += e;
+            pf[t][i >> 3][i & 7] = (f16)e;
+        }
+    sum += __shfl_xor(sum, 32, 64);
+    const float rs = 1.0f / sum;
+
+    // O^T[dim][q] = V^T . P^T; A lane (dim, hh) supplies keys 16s + 4hh + {0..3} and 16s + 8 + 4hh + {0..3}.
+    for (int dt = 0; dt < DT; ++dt) {
+        f32x16 o;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] = 0.0f;
+        const f16 * vrow = Vs + (dt * 32 + (lane & 31)) * VROW;
+#pragma unroll
+        for (int t = 0; t < LT; ++t)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int kbase = t * 32 + 16 * s2 + 4 * hh;
+                const f16x4 lo4 = *reinterpret_cast<const f16x4 *>(vrow + kbase);
+                const f16x4 hi4 = *reinterpret_cast<const f16x4 *>(vrow + kbase + 8);
+                f16x8 af;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    af[e] = lo4[e];
+                    af[4 + e] = hi4[e];
+                }
+                o = mfma_32x32x16(af, pf[t][s2], o);
+            }
+        // lane holds query column (lane & 31), dims dt*32 + 8*(i/4) + 4*hh + i%4
+        const int qq = q0 + (lane & 31);
+        if (qq < N) {
+            f16 * orow = out + ((int64_t)b * N + qq) * ldo + (int64_t)h * D;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int dim = dt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+                if (dim < D) orow[dim] = (f16)(o[i] * rs);
+            }
+        }
+    }
+}
+
+template <int LT>
+hipError_t launch_xattn_fast(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
+                             const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D,
+                             float scale, hipStream_t s) {
+    constexpr int LP = LT * 32;
+    const size_t lds = (size_t)LP * (96 + 8) * 2 + (size_t)96 * (LP + 8) * 2 + (size_t)LP * 4;
+    static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&xattn_fast_kernel<LT>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
+    (void)attr;
+    hipLaunchKernelGGL((xattn_fast_kernel<LT>), dim3((N + kXaQ - 1) / kXaQ, H, B), dim3(256), lds, s, q, ldq, k, ldk,
+                       vt, ldvt, bias, out, ldo, N, L, H, D, scale);
+    return hipGetLastError();
+}
+
 template <int LT>
 hipError_t launch_xattn(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
                         const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D, float scale,
@@ -259,33 +527,65 @@ hipError_t launch_xattn(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, 
 
 }  // namespace
 
+namespace {
+int la_chunk_tokens(int N) {
+    // sub-chunk multiple giving at most kLaChunks partial states per (b, h)
+    const int per = (N + kLaChunks - 1) / kLaChunks;
+    return (per + kLaSub - 1) / kLaSub * kLaSub;
+}
+}  // namespace
+
 size_t linattn_workspace_floats(int B, int N, int H, int D) {
-    const size_t nch = (size_t)(N + kLaChunk - 1) / kLaChunk;
+    const int T = la_chunk_tokens(N);
+    const size_t nch = (size_t)(N + T - 1) / T;
     const size_t E = (size_t)(D + 1) * D;
-    return (size_t)B * H * E * (nch + 1);
+    const size_t NP = (size_t)(D + 1 + 31) / 32 * 32, KP = (size_t)(D + 15) / 16 * 16;
+    // partial states (fp32, rounded up to 16 bytes) + the hi/lo fp16 state pair (counted in floats)
+    return ((size_t)B * H * E * nch + 3) / 4 * 4 + (size_t)B * H * NP * KP;
 }
 
 hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v, int64_t ld, half_t * out,
                             int64_t ldo, int B, int N, int H, int D, float * ws, hipStream_t s) {
-    if (B <= 0 || N <= 0 || H <= 0 || D <= 0 || D > 100 || ld < (int64_t)H * D || ldo < (int64_t)H * D || !ws)
+    if (B <= 0 || N <= 0 || H <= 0 || D <= 0 || D > 112 || ld < (int64_t)H * D || ldo < (int64_t)H * D || !ws ||
+        H > 65535 || B > 65535)
         return hipErrorInvalidValue;
-    const int nch = (N + kLaChunk - 1) / kLaChunk;
+    const int T = la_chunk_tokens(N);
+    const int nch = (N + T - 1) / T;
     const int E = (D + 1) * D;
+    const int NT = (D + 1 + 31) / 32, KS = (D + 15) / 16;
+    const int NP = NT * 32, KP = KS * 16;
     float * part = ws;
-    float * state = ws + (size_t)B * H * E * nch;
+    f16 * shi = reinterpret_cast<f16 *>(ws + ((size_t)B * H * E * nch + 3) / 4 * 4);
+    f16 * slo = shi + (size_t)B * H * NP * KP;
+    const f16 * qq = reinterpret_cast<const f16 *>(q);
     const f16 * kq = reinterpret_cast<const f16 *>(k);
     const f16 * vq = reinterpret_cast<const f16 *>(v);
+    const auto al16 = [](const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const int vec_kv = (D % 8 == 0 && ld % 8 == 0 && al16(k) && al16(v)) ? 1 : 0;
+    const int vec_q = (D % 8 == 0 && ld % 8 == 0 && al16(q)) ? 1 : 0;
     const dim3 g1(nch, H, B);
-    if (E <= 256 * 8)
-        hipLaunchKernelGGL((la_state_kernel<8>), g1, dim3(256), 0, s, kq, vq, ld, N, H, D, nch, part);
-    else if (E <= 256 * 24)
-        hipLaunchKernelGGL((la_state_kernel<24>), g1, dim3(256), 0, s, kq, vq, ld, N, H, D, nch, part);
-    else
-        hipLaunchKernelGGL((la_state_kernel<40>), g1, dim3(256), 0, s, kq, vq, ld, N, H, D, nch, part);
-    hipLaunchKernelGGL(la_reduce_kernel, dim3(B * H), dim3(256), 0, s, part, nch, E, state);
-    const size_t lds = sizeof(float) * ((size_t)D * (D + 1) + (size_t)kLaApplyTok * D + kLaApplyTok);
-    hipLaunchKernelGGL(la_apply_kernel, dim3((N + kLaApplyTok - 1) / kLaApplyTok, H, B), dim3(256), lds, s,
-                       reinterpret_cast<const f16 *>(q), ld, state, reinterpret_cast<f16 *>(out), ldo, N, H, D);
+    const int td = (D + 31) / 32;
+    if (td == 1) hipLaunchKernelGGL((la_state_kernel<1>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part);
+    else if (td == 2) hipLaunchKernelGGL((la_state_kernel<2>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part);
+    else if (td == 3) hipLaunchKernelGGL((la_state_kernel<3>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part);
+    else hipLaunchKernelGGL((la_state_kernel<4>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part);
+    hipLaunchKernelGGL(la_reduce_kernel, dim3((NP * KP + 255) / 256, B * H), dim3(256), 0, s, part, nch, D, NP, KP,
+                       shi, slo);
+    const dim3 g3((N + 127) / 128, H, B);
+    f16 * oo = reinterpret_cast<f16 *>(out);
+#define SANA_LA_APPLY(nt, ks)                                                                                     \
+    hipLaunchKernelGGL((la_apply_kernel<nt, ks>), g3, dim3(256), 0, s, qq, ld, shi, slo, oo, ldo, N, H, D, vec_q)
+    // NT = ceil((D + 1) / 32) in 1..4, KS = ceil(D / 16) in 1..7
+    if (NT == 1) {
+        if (KS == 1) SANA_LA_APPLY(1, 1); else SANA_LA_APPLY(1, 2);
+    } else if (NT == 2) {
+        if (KS == 2) SANA_LA_APPLY(2, 2); else if (KS == 3) SANA_LA_APPLY(2, 3); else SANA_LA_APPLY(2, 4);
+    } else if (NT == 3) {
+        if (KS == 4) SANA_LA_APPLY(3, 4); else if (KS == 5) SANA_LA_APPLY(3, 5); else SANA_LA_APPLY(3, 6);
+    } else {
+        if (KS == 6) SANA_LA_APPLY(4, 6); else SANA_LA_APPLY(4, 7);
+    }
+#undef SANA_LA_APPLY
     return hipGetLastError();
 }
 
@@ -304,6 +604,13 @@ hipError_t cross_attention(const half_t * q, int64_t ldq, const half_t * k, int6
     const f16 * kk = reinterpret_cast<const f16 *>(k);
     const f16 * vv = reinterpret_cast<const f16 *>(vt);
     f16 * oo = reinterpret_cast<f16 *>(out);
+    // fast path: LDS-staged head, transposed scores (ldvt >= the 32-padded key count)
+    const int lt32 = (L + 31) / 32;
+    if (vec && D <= 96 && lt32 <= 10 && ldvt >= (int64_t)lt32 * 32) {
+        if (lt32 <= 2) return launch_xattn_fast<2>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
+        if (lt32 <= 4) return launch_xattn_fast<4>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
+        return launch_xattn_fast<10>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
+    }
     const int lt = (L + 15) / 16;
     if (lt <= 2) return launch_xattn<2>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, vec, s);
     if (lt <= 8) return launch_xattn<8>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, vec, s);

@@ -93,7 +93,7 @@ struct DevMem {
 };
 
 struct BlockDev {
-    DevMem sst, w_qkv, w_out, b_out, w_cq, b_cq, w_co, b_co, w_inv, b_inv, w_dw, b_dw, w_pt;
+    DevMem w_qkv, w_out, b_out, w_cq, b_cq, w_co, b_co, w_inv, b_inv, w_dw, b_dw, w_pt;
     DevMem ln1_g, ln1_b, ln2_g, ln2_b;
     bool has_ln1 = false, has_ln2 = false;
 };
@@ -119,7 +119,7 @@ struct sana_dit {
     int64_t Cp = 0, Fp = 0, Ccap_p = 0;  // K-padded row strides of GEMM operands
     hipStream_t stream = nullptr;
     std::vector<std::unique_ptr<BlockDev>> blocks;
-    DevMem w_k_all, b_k_all, w_v_all, b_v_all;
+    DevMem w_k_all, b_k_all, w_v_all, b_v_all, sst_all;  // stacked over blocks
     DevMem w_cap1, b_cap1, w_cap2, b_cap2, cap_norm;
     DevMem w_patch_t, b_patch, w_t1, b_t1, w_t2, b_t2, w_tp, b_tp, sst_final, w_proj, b_proj, freq;
     std::map<std::string, int> have;  // uploaded tensor names
@@ -129,7 +129,7 @@ struct sana_dit {
     DevMem cap32, cap16, caph16, capf32, ctx32, ctx16, kc, vt, bias;
     // forward workspace
     int64_t ws_M = 0, ws_B = 0;
-    DevMem x32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, d_t, tp, e1, emb, tmod, lat_in, np_out;
+    DevMem x32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, d_t, tp, e1, emb, tmod, mod_all, lat_in, np_out;
     // graphs keyed by (kind, Bl, H, W, L, pointers)
     std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, const void *, const void *, const void *, const void *>,
              GraphEntry>
@@ -312,11 +312,19 @@ void ensure_forward_buffers(sana_dit * c, int64_t B, int64_t N) {
         c->e1.ensure((size_t)B * C * 4);
         c->emb.ensure((size_t)B * C * 4);
         c->tmod.ensure((size_t)B * 6 * C * 4);
+        c->mod_all.ensure((size_t)c->L_ * B * 6 * C * 4);
         c->lat_in.ensure((size_t)B * c->Cl * N * 4);
         c->np_out.ensure((size_t)B * c->Cl * N * 4);
         c->ws_M = M;
         c->ws_B = B;
     }
+}
+
+// Per-block adaLN modulation of every block (t_mod + table), for B batch rows.
+void enqueue_mod(sana_dit * c, int64_t B, hipStream_t s) {
+    launch_check(sana::mod_combine(c->tmod.as<float>(), c->sst_all.as<float>(), (int)c->L_, (int)B, (int)(6 * c->C),
+                                   c->mod_all.as<float>(), s),
+                 "mod_combine");
 }
 
 void enqueue_time(sana_dit * c, int64_t B, hipStream_t s) {
@@ -332,6 +340,7 @@ void enqueue_time(sana_dit * c, int64_t B, hipStream_t s) {
     launch_check(sana::gemv_f32(c->emb.as<float>(), c->w_tp.as<float>(), c->b_tp.as<float>(), c->tmod.as<float>(),
                                 (int)B, (int)C, (int)(6 * C), 1, s),
                  "time projection");
+    enqueue_mod(c, B, s);
 }
 
 // Stage hook: called after each stage of a block (0 self, 1 cross, 2 ff).
@@ -341,12 +350,12 @@ void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * 
                    StageHook hook = nullptr, void * hook_ctx = nullptr) {
     BlockDev & w = *c->blocks[i];
     const int64_t C = c->C, M = B * N, side = (int64_t)std::llround(std::sqrt((double)N));
-    const float * tmod = c->tmod.as<float>();
-    const float * sst = w.sst.as<float>();
+    // modulation rows of this block: [B][6C] = shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp
+    const float * mod = c->mod_all.as<float>() + (size_t)i * B * 6 * C;
     // self attention: LN + modulate(shift_msa, scale_msa)
     launch_check(sana::ln_modulate(c->x32.as<float>(), C, c->xa16.as<half_t>(), c->Cp, (int)M, (int)C, (int)N, 1e-6f,
                                    w.has_ln1 ? w.ln1_g.as<float>() : nullptr, w.has_ln1 ? w.ln1_b.as<float>() : nullptr,
-                                   tmod, sst, 6 * C, 0, C, s),
+                                   mod, nullptr, 6 * C, 0, C, s),
                  "ln_modulate");
     gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp, nullptr, sana::kActNone,
                c->qkv16.as<half_t>(), 3 * C, nullptr, 0, s);
@@ -356,7 +365,7 @@ void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * 
                  "linear_attention");
     // x += gate_msa * (o Wo^T + bo); r16 = fp16(x) for the cross-attention query
     gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_out.as<half_t>(), c->Cp, M, C, c->Cp, w.b_out.as<float>(),
-               tmod + 2 * C, sst + 2 * C, 6 * C, N, c->x32.as<float>(), C, c->r16.as<half_t>(), c->Cp, s);
+               mod + 2 * C, nullptr, 6 * C, N, c->x32.as<float>(), C, c->r16.as<half_t>(), c->Cp, s);
     if (hook) hook(hook_ctx, 0);
     // cross attention
     gemm_store(c, c->r16.as<half_t>(), c->Cp, w.w_cq.as<half_t>(), c->Cp, M, C, c->Cp, w.b_cq.as<float>(),
@@ -373,15 +382,15 @@ void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * 
     // Mix-FFN
     launch_check(sana::ln_modulate(c->x32.as<float>(), C, c->xa16.as<half_t>(), c->Cp, (int)M, (int)C, (int)N, 1e-6f,
                                    w.has_ln2 ? w.ln2_g.as<float>() : nullptr, w.has_ln2 ? w.ln2_b.as<float>() : nullptr,
-                                   tmod, sst, 6 * C, 3 * C, 4 * C, s),
+                                   mod, nullptr, 6 * C, 3 * C, 4 * C, s),
                  "ln_modulate");
     gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_inv.as<half_t>(), c->Cp, M, c->E, c->Cp, w.b_inv.as<float>(),
                sana::kActSilu, c->hid16.as<half_t>(), c->E, nullptr, 0, s);
     launch_check(sana::dwconv_glu(c->hid16.as<half_t>(), c->E, w.w_dw.as<float>(), w.b_dw.as<float>(),
                                   c->glu16.as<half_t>(), c->Fp, (int)B, (int)side, (int)side, (int)c->F, s),
                  "dwconv_glu");
-    gemm_resid(c->glu16.as<half_t>(), c->Fp, w.w_pt.as<half_t>(), c->Fp, M, C, c->Fp, nullptr, tmod + 5 * C,
-               sst + 5 * C, 6 * C, N, c->x32.as<float>(), C, nullptr, 0, s);
+    gemm_resid(c->glu16.as<half_t>(), c->Fp, w.w_pt.as<half_t>(), c->Fp, M, C, c->Fp, nullptr, mod + 5 * C,
+               nullptr, 6 * C, N, c->x32.as<float>(), C, nullptr, 0, s);
     if (hook) hook(hook_ctx, 2);
 }
 
@@ -530,6 +539,7 @@ int sana_dit_create(const sana_dit_config * cfg, sana_dit ** out) {
         c->w_v_all.ensure((size_t)c->L_ * C * c->Cp * 2);
         c->b_k_all.ensure((size_t)c->L_ * C * 4);
         c->b_v_all.ensure((size_t)c->L_ * C * 4);
+        c->sst_all.ensure((size_t)c->L_ * 6 * C * 4);
     });
     if (rc != SANA_OK) return rc;
     *out = c.release();
@@ -577,7 +587,7 @@ int sana_dit_set_weight(sana_dit * c, const char * name, const float * data, con
             upload_f32(c->sst_final, data, 2 * C);
         } else if (n == "proj_out.weight") {
             expect_shape(name, shape, ndim, tr ? std::vector<int64_t>{C, Cl} : std::vector<int64_t>{Cl, C});
-            upload_f32_transposed(c->w_proj, data, Cl, C, tr);
+            upload_f32_transposed(c->w_proj, data, C, Cl, !tr);  // -> [C, Cl]
         } else if (n == "proj_out.bias") {
             expect_shape(name, shape, ndim, {Cl});
             upload_f32(c->b_proj, data, Cl);
@@ -617,7 +627,7 @@ int sana_dit_set_block_weight(sana_dit * c, int64_t blk, const char * suffix, co
         };
         if (s == "scale_shift_table") {
             expect_shape(suffix, shape, ndim, {6, C});
-            upload_f32(w.sst, data, 6 * C);
+            upload_f32(c->sst_all, data, 6 * C, (size_t)blk * 6 * C, (size_t)c->L_ * 6 * C);
         } else if (s == "attn1.to_q.weight") {
             lin(w.w_qkv, C, C, c->Cp, 0, 3 * C);
         } else if (s == "attn1.to_k.weight") {
@@ -829,6 +839,7 @@ int sana_dit_block_forward(sana_dit * c, int64_t blk, const float * x, const flo
         hip_check(hipMemcpyAsync(c->x32.p, x, n * 4, hipMemcpyHostToDevice, c->stream), "upload x");
         hip_check(hipMemcpyAsync(c->tmod.p, t_mod, (size_t)B * 6 * c->C * 4, hipMemcpyHostToDevice, c->stream),
                   "upload t_mod");
+        enqueue_mod(c, B, c->stream);
         struct Hook {
             sana_dit * c;
             size_t n;
@@ -877,7 +888,7 @@ int sana_dit_time_gemm(sana_dit * c, int which, int iters, float * avg_ms, doubl
                     break;
                 case 1:
                     gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_out.as<half_t>(), c->Cp, M, C, c->Cp,
-                               w.b_out.as<float>(), c->tmod.as<float>() + 2 * C, w.sst.as<float>() + 2 * C, 6 * C, N,
+                               w.b_out.as<float>(), c->mod_all.as<float>() + 2 * C, nullptr, 6 * C, N,
                                c->x32.as<float>(), C, c->r16.as<half_t>(), c->Cp, c->stream);
                     break;
                 case 2:
@@ -894,7 +905,7 @@ int sana_dit_time_gemm(sana_dit * c, int which, int iters, float * avg_ms, doubl
                     break;
                 default:
                     gemm_resid(c->glu16.as<half_t>(), c->Fp, w.w_pt.as<half_t>(), c->Fp, M, C, c->Fp, nullptr,
-                               c->tmod.as<float>() + 5 * C, w.sst.as<float>() + 5 * C, 6 * C, N, c->x32.as<float>(), C,
+                               c->mod_all.as<float>() + 5 * C, nullptr, 6 * C, N, c->x32.as<float>(), C,
                                nullptr, 0, c->stream);
             }
         };

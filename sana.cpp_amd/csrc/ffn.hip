@@ -7,68 +7,99 @@
 // producing GEMM's epilogue, so the input here is already silu(inv(x) + b).
 //
 // Layout: channels are contiguous per token, so 8 channels of one token are
-// one 16-byte load; a thread owns 8 data channels and the matching 8 gate
-// channels of one output token and reads the 3x3 neighbourhood (halo rows come
-// from L2).  Depthwise weights are stored tap-major [9][E] so the 8 weights of
-// a tap are two float4 loads.
+// one 16-byte load and consecutive lanes read consecutive 16-byte channel
+// groups of the same token (coalesced).  Depthwise weights are stored
+// tap-major [9][E] so the 8 weights of a tap are two float4 loads.
 #include "hip_common.h"
 #include "kernels.h"
 
 namespace sana {
 namespace {
 
-__global__ __launch_bounds__(256) void dwglu_vec_kernel(const f16 * __restrict__ x, int64_t ldx,
-                                                        const float * __restrict__ wt, const float * __restrict__ bias,
-                                                        f16 * __restrict__ out, int64_t ldo, int B, int Hh, int Ww,
-                                                        int F) {
-    const int groups = F / 8;
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = (int64_t)B * Hh * Ww * groups;
-    if (gid >= total) return;
-    const int g = (int)(gid % groups);
-    const int64_t m = gid / groups;
-    const int xx = (int)(m % Ww);
-    const int64_t r = m / Ww;
-    const int y = (int)(r % Hh);
-    const int b = (int)(r / Hh);
-    const int c0 = g * 8;
-    const int E = 2 * F;
-    float ad[8], ag[8];
+// Register-tiled variant: a thread owns 8 data channels (and the matching 8
+// gate channels) of one row segment of XS output tokens.  Its 9 taps x 16
+// channels of weights and its biases are loaded once; a 3 x 3 window of input
+// vectors slides along the row, so each new output token loads one new input
+// column (3 rows) instead of all 9 taps.  Taps are summed in (ky, kx) order
+// with zero padding, then the bias, as the reference accumulates.
+template <int XS>
+__global__ __launch_bounds__(64) void dwglu_row_kernel(const f16 * __restrict__ x, int64_t ldx,
+                                                       const float * __restrict__ wt, const float * __restrict__ bias,
+                                                       f16 * __restrict__ out, int64_t ldo, int Hh, int Ww, int F) {
+    const int G = F / 8;
+    const int g = blockIdx.x * 64 + threadIdx.x;
+    const int nseg = (Ww + XS - 1) / XS;
+    const int y = blockIdx.y / nseg, seg = blockIdx.y - (blockIdx.y / nseg) * nseg;
+    const int b = blockIdx.z;
+    if (g >= G) return;
+    const int c0 = g * 8, E = 2 * F;
+    float wd[9][8], wg[9][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ad[e] = ag[e] = 0.0f;
-#pragma unroll
-    for (int ky = 0; ky < 3; ++ky) {
-        const int iy = y + ky - 1;
-        if (iy < 0 || iy >= Hh) continue;
-#pragma unroll
-        for (int kx = 0; kx < 3; ++kx) {
-            const int ix = xx + kx - 1;
-            if (ix < 0 || ix >= Ww) continue;
-            const f16 * px = x + (((int64_t)b * Hh + iy) * Ww + ix) * ldx + c0;
-            const f16x8 vd = *reinterpret_cast<const f16x8 *>(px);
-            const f16x8 vg = *reinterpret_cast<const f16x8 *>(px + F);
-            const float * wp = wt + (int64_t)(ky * 3 + kx) * E + c0;
-            const float4 wd0 = *reinterpret_cast<const float4 *>(wp);
-            const float4 wd1 = *reinterpret_cast<const float4 *>(wp + 4);
-            const float4 wg0 = *reinterpret_cast<const float4 *>(wp + F);
-            const float4 wg1 = *reinterpret_cast<const float4 *>(wp + F + 4);
-            const float wd[8] = {wd0.x, wd0.y, wd0.z, wd0.w, wd1.x, wd1.y, wd1.z, wd1.w};
-            const float wg[8] = {wg0.x, wg0.y, wg0.z, wg0.w, wg1.x, wg1.y, wg1.z, wg1.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                ad[e] += (float)vd[e] * wd[e];
-                ag[e] += (float)vg[e] * wg[e];
-            }
-        }
+    for (int k = 0; k < 9; ++k) {
+        const float4 * wp = reinterpret_cast<const float4 *>(wt + (int64_t)k * E + c0);
+        const float4 * wq = reinterpret_cast<const float4 *>(wt + (int64_t)k * E + F + c0);
+        const float4 a0 = wp[0], a1 = wp[1], b0 = wq[0], b1 = wq[1];
+        wd[k][0] = a0.x; wd[k][1] = a0.y; wd[k][2] = a0.z; wd[k][3] = a0.w;
+        wd[k][4] = a1.x; wd[k][5] = a1.y; wd[k][6] = a1.z; wd[k][7] = a1.w;
+        wg[k][0] = b0.x; wg[k][1] = b0.y; wg[k][2] = b0.z; wg[k][3] = b0.w;
+        wg[k][4] = b1.x; wg[k][5] = b1.y; wg[k][6] = b1.z; wg[k][7] = b1.w;
     }
-    f16x8 o;
+    float bd[8], bg[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float d = ad[e] + bias[c0 + e];
-        const float gt = ag[e] + bias[F + c0 + e];
-        o[e] = (f16)(d * silu_f(gt));
+        bd[e] = bias[c0 + e];
+        bg[e] = bias[F + c0 + e];
     }
-    *reinterpret_cast<f16x8 *>(out + m * ldo + c0) = o;
+    const f16 * xb = x + (int64_t)b * Hh * Ww * ldx + c0;
+    f16 * ob = out + (int64_t)b * Hh * Ww * ldo + c0;
+    const int x0 = seg * XS;
+    f16x8 vd[3][3], vg[3][3];  // [row ky][column slot]
+    auto load = [&](int ky, int xx, int slot) {
+        const int yy = y + ky - 1;
+        if (yy >= 0 && yy < Hh && xx >= 0 && xx < Ww) {
+            const f16 * p = xb + ((int64_t)yy * Ww + xx) * ldx;
+            vd[ky][slot] = *reinterpret_cast<const f16x8 *>(p);
+            vg[ky][slot] = *reinterpret_cast<const f16x8 *>(p + F);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vd[ky][slot][e] = vg[ky][slot][e] = (f16)0.0f;
+        }
+    };
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky) {
+        load(ky, x0 - 1, 0);
+        load(ky, x0, 1);
+    }
+#pragma unroll
+    for (int i = 0; i < XS; ++i) {
+        const int xx = x0 + i;
+        if (xx < Ww) {
+#pragma unroll
+            for (int ky = 0; ky < 3; ++ky) load(ky, xx + 1, (i + 2) % 3);
+            float ad[8], ag[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ad[e] = ag[e] = 0.0f;
+#pragma unroll
+            for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx) {
+                    const int slot = (i + kx) % 3;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        ad[e] += (float)vd[ky][slot][e] * wd[ky * 3 + kx][e];
+                        ag[e] += (float)vg[ky][slot][e] * wg[ky * 3 + kx][e];
+                    }
+                }
+            f16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = ad[e] + bd[e];
+                const float gt = ag[e] + bg[e];
+                o[e] = (f16)(d * silu_f(gt));
+            }
+            *reinterpret_cast<f16x8 *>(ob + ((int64_t)y * Ww + xx) * ldo) = o;
+        }
+    }
 }
 
 // Scalar variant for channel counts that are not a multiple of 8.
@@ -114,9 +145,11 @@ hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const flo
     const f16 * xx = reinterpret_cast<const f16 *>(x);
     f16 * oo = reinterpret_cast<f16 *>(out);
     if (vec) {
-        const int64_t total = (int64_t)B * Hh * Ww * (F / 8);
-        hipLaunchKernelGGL(dwglu_vec_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, xx, ldx, wt, bias,
-                           oo, ldo, B, Hh, Ww, F);
+        constexpr int XS = 8;
+        const int nseg = (Ww + XS - 1) / XS;
+        if ((int64_t)Hh * nseg > 2147483647 || B > 65535) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((dwglu_row_kernel<XS>), dim3((F / 8 + 63) / 64, Hh * nseg, B), dim3(64), 0, s, xx, ldx, wt,
+                           bias, oo, ldo, Hh, Ww, F);
     } else {
         const int64_t total = (int64_t)B * Hh * Ww * F;
         hipLaunchKernelGGL(dwglu_scalar_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, xx, ldx, wt,

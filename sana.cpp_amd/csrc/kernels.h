@@ -43,6 +43,7 @@ struct GemmParams {
     // stored at out16[((blk * vt_batch + b) * vt_rows + r) * vt_ld + j].
     int vt_rows = 0, vt_cols = 0, vt_batch = 0;
     int64_t vt_ld = 0;
+    int vec = 0;  // set by gemm(): 16-byte epilogue accesses are aligned
 };
 
 hipError_t gemm(const GemmParams & p, hipStream_t s);
@@ -53,6 +54,9 @@ hipError_t gemm(const GemmParams & p, hipStream_t s);
 hipError_t ln_modulate(const float * x, int64_t ldx, half_t * out, int64_t ldo, int M, int C, int rows_per_batch,
                        float eps, const float * gamma, const float * beta, const float * mod_a, const float * mod_t,
                        int64_t mod_stride, int64_t shift_off, int64_t scale_off, hipStream_t s);
+
+// comb[l][b][i] = tmod[b][i] + tables[l][i] (l < L, b < B, i < W).
+hipError_t mod_combine(const float * tmod, const float * tables, int L, int B, int W, float * comb, hipStream_t s);
 
 // RMSNorm (eps, weight) fp32 -> fp16 (and optionally fp32 [M, C] into out32).
 hipError_t rms_norm_f16(const float * x, int64_t ldx, const float * weight, half_t * out, int64_t ldo, float * out32,
@@ -74,8 +78,8 @@ hipError_t patch_embed(const float * latent, int Bl, int B, int Cl, int S, const
                        float * out, int C, hipStream_t s);
 
 // Final layer: LN(eps, no affine) + modulate(shift = emb + T[0], scale = emb + T[1])
-// + proj (W [Cl, C] fp32, bias [Cl]) stored NCHW [B, Cl, S].
-hipError_t final_layer(const float * x, const float * emb, const float * table, const float * W, const float * bias,
+// + proj (Wt [C, Cl] fp32, bias [Cl]) stored NCHW [B, Cl, S].
+hipError_t final_layer(const float * x, const float * emb, const float * table, const float * Wt, const float * bias,
                        float * out, int B, int S, int C, int Cl, float eps, hipStream_t s);
 
 // ReLU linear attention.  q/k/v fp16 token-major with row stride ld (head h at

@@ -1,0 +1,45 @@
+"""The C ABI library loads on a host without a GPU and exports exactly the
+entry points that include/sana_dit.h declares; the Python binding binds all
+of them.  No compute call is made here."""
+import ctypes
+import os
+import re
+
+import sana_dit
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    text = open(os.path.join(ROOT, "include", "sana_dit.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sana_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "sana_dit_forward" in names and "sana_hip_gemm" in names
+    assert len(names) >= 20
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(sana_dit.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_every_declared_symbol():
+    assert sorted(sana_dit.PROTOTYPES) == declared()
+
+
+def test_last_error_is_empty_string_initially():
+    assert sana_dit.lib().sana_dit_last_error() in (b"",)
+
+
+def test_create_rejects_bad_config_without_gpu():
+    # argument validation happens before any device call
+    cfg = sana_dit.Config(28, 1152, 5760, 2304, 32, 35, 16, 0)   # 1152 % 35 != 0
+    h = ctypes.c_void_p()
+    rc = sana_dit.lib().sana_dit_create(ctypes.byref(cfg), ctypes.byref(h))
+    assert rc == sana_dit.SANA_ERR_INVALID_ARGUMENT
+    assert b"divisible" in sana_dit.lib().sana_dit_last_error()
