@@ -64,7 +64,9 @@ void sana_dit_destroy(sana_dit * ctx);
 int sana_dit_set_weight(sana_dit * ctx, const char * name, const float * data, const int64_t * shape, int ndim,
                         int transposed);
 /* Upload one tensor of block `block` by its suffix after the block prefix
- * (load_block_weights, src/transformer.cpp:214-308), e.g. "attn1.to_q.weight". */
+ * (load_block_weights, src/transformer.cpp:214-308), e.g. "attn1.to_q.weight".
+ * "attn1.to_{q,k,v}.bias" are optional (the reference loader injects zeros,
+ * src/transformer.cpp:361-362; SanaBlockWeights built in memory may set them). */
 int sana_dit_set_block_weight(sana_dit * ctx, int64_t block, const char * suffix, const float * data,
                               const int64_t * shape, int ndim, int transposed);
 /* Optional LayerNorm affine of a block (which = 0: attn norm, 1: mlp norm).
@@ -108,6 +110,25 @@ int sana_dit_step_device(sana_dit * ctx, const float * d_caption, int64_t L, con
  * above: x [B, N, C], t_mod [B, 6C] -> the three stage outputs [B, N, C]. */
 int sana_dit_block_forward(sana_dit * ctx, int64_t block, const float * x, const float * t_mod, int64_t B,
                            int64_t N, float * after_self, float * after_cross, float * after_ff);
+/* run_model_blocks (src/transformer.cpp:544-568) on the context set above:
+ * blocks [begin, end) applied to x [B, N, C] with t_mod [B, 6C] -> out [B, N, C]. */
+int sana_dit_run_blocks(sana_dit * ctx, int64_t begin, int64_t end, const float * x, const float * t_mod, int64_t B,
+                        int64_t N, float * out);
+/* run_full_denoising_loop_with_cfg (src/transformer.cpp:692-724) with the
+ * default scheduler (DPM-Solver++ order 2, midpoint, flow sigmas,
+ * lower_order_final; src/scheduler.cpp:272-318) entirely on the device: per
+ * step one forward at timesteps[i], classifier-free guidance (uncond = first
+ * half of the context batch) and the solver update, fused.  timesteps [steps]
+ * and sigmas [steps + 1] are the schedule of build_sana_scheduler_timesteps;
+ * the context (caption projection and cross K/V) must be set.  latent and
+ * final_latent are [Bl, Cl, H, W]. */
+int sana_dit_denoise_loop(sana_dit * ctx, const float * latent, int64_t Bl, int64_t H, int64_t W,
+                          const float * timesteps, const float * sigmas, int64_t steps, float guidance,
+                          float * final_latent);
+/* Same with device latent pointers, asynchronous on `stream` (timesteps and sigmas stay host arrays). */
+int sana_dit_denoise_loop_device(sana_dit * ctx, const float * d_latent, int64_t Bl, int64_t H, int64_t W,
+                                 const float * timesteps, const float * sigmas, int64_t steps, float guidance,
+                                 float * d_final_latent, void * stream);
 /* Time MLP of the forward (src/transformer.cpp:638-656): B timesteps ->
  * embedded [B, C] (pre-SiLU) and t_mod [B, 6C]. */
 int sana_dit_time_embed(sana_dit * ctx, const float * t, int64_t B, float * embedded, float * t_mod);

@@ -93,14 +93,37 @@ struct DevMem {
 };
 
 struct BlockDev {
-    DevMem w_qkv, w_out, b_out, w_cq, b_cq, w_co, b_co, w_inv, b_inv, w_dw, b_dw, w_pt;
+    DevMem w_qkv, b_qkv, w_out, b_out, w_cq, b_cq, w_co, b_co, w_inv, b_inv, w_dw, b_dw, w_pt;
     DevMem ln1_g, ln1_b, ln2_g, ln2_b;
     bool has_ln1 = false, has_ln2 = false;
+    bool has_qkv_bias = false;  // attn1 q/k/v biases (zero in every checkpoint the loader reads)
 };
 
 __global__ void fill_kernel(float * p, int n, float v) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
+}
+
+// Classifier-free guidance and one DPM-Solver++ update, fused, per latent element:
+//   v  = u + g (c - u)                       (apply_classifier_free_guidance, src/transformer.cpp:586-598)
+//   x0 = x - sigma_s v                        (convert_sana_scheduler_model_output, src/scheduler.cpp:155-173)
+//   first order : x' = ca x + cb x0           (src/scheduler.cpp:175-205)
+//   second order: x' = ca x + cb x0 + cc (x0 - x0_prev) / r0   (midpoint, :207-260)
+// noise_pred holds the uncond half first, then the cond half (batch order of the context).
+__global__ void cfg_dpm_kernel(const float * __restrict__ np, const float * __restrict__ x,
+                               const float * __restrict__ x0_prev, float * __restrict__ x_out,
+                               float * __restrict__ x0_out, int n, float g, float sigma_s, float ca, float cb, float cc,
+                               float inv_r0, int second) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float u = np[i], c = np[n + i];
+    const float v = u + g * (c - u);
+    const float xi = x[i];
+    const float x0 = xi - sigma_s * v;
+    float out = ca * xi + cb * x0;
+    if (second) out = ca * xi + cb * x0 + cc * (inv_r0 * (x0 - x0_prev[i]));
+    x_out[i] = out;
+    x0_out[i] = x0;
 }
 
 struct GraphEntry {
@@ -129,7 +152,9 @@ struct sana_dit {
     DevMem cap32, cap16, caph16, capf32, ctx32, ctx16, kc, vt, bias;
     // forward workspace
     int64_t ws_M = 0, ws_B = 0;
-    DevMem x32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, d_t, tp, e1, emb, tmod, mod_all, lat_in, np_out;
+    DevMem x32, fin32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, d_t, tp, e1, emb, tmod, mod_all, lat_in,
+        np_out;
+    DevMem loop_lat[2], loop_x0[2];  // denoise loop: latent ping-pong and converted-output history
     // graphs keyed by (kind, Bl, H, W, L, pointers)
     std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, const void *, const void *, const void *, const void *>,
              GraphEntry>
@@ -299,6 +324,7 @@ void ensure_forward_buffers(sana_dit * c, int64_t B, int64_t N) {
         drop_graphs(c);
         const int64_t C = c->C;
         c->x32.ensure((size_t)M * C * 4);
+        c->fin32.ensure((size_t)M * C * 4);
         c->xa16.ensure((size_t)M * c->Cp * 2);
         c->qkv16.ensure((size_t)M * 3 * C * 2);
         c->o16.ensure((size_t)M * c->Cp * 2);
@@ -357,8 +383,9 @@ void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * 
                                    w.has_ln1 ? w.ln1_g.as<float>() : nullptr, w.has_ln1 ? w.ln1_b.as<float>() : nullptr,
                                    mod, nullptr, 6 * C, 0, C, s),
                  "ln_modulate");
-    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp, nullptr, sana::kActNone,
-               c->qkv16.as<half_t>(), 3 * C, nullptr, 0, s);
+    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
+               w.has_qkv_bias ? w.b_qkv.as<float>() : nullptr, sana::kActNone, c->qkv16.as<half_t>(), 3 * C, nullptr,
+               0, s);
     const half_t * qkv = c->qkv16.as<half_t>();
     launch_check(sana::linear_attention(qkv, qkv + C, qkv + 2 * C, 3 * C, c->o16.as<half_t>(), c->Cp, (int)B, (int)N,
                                         (int)c->Hs, (int)c->Ds, c->la_ws.as<float>(), s),
@@ -403,29 +430,54 @@ void enqueue_forward(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh,
     enqueue_time(c, B, s);
     for (int64_t i = 0; i < c->L_; ++i) enqueue_block(c, i, B, N, xbias, s);
     launch_check(sana::final_layer(c->x32.as<float>(), c->emb.as<float>(), c->sst_final.as<float>(),
-                                   c->w_proj.as<float>(), c->b_proj.as<float>(), out, (int)B, (int)N, (int)c->C,
+                                   c->w_proj.as<float>(), c->b_proj.as<float>(), c->fin32.as<float>(), out, (int)B,
+                                   (int)N, (int)c->C,
                                    (int)c->Cl, 1e-6f, s),
                  "final_layer");
 }
 
+// Tensors every block needs (load_block_weights, src/transformer.cpp:214-308).
+const char * const kBlockRequired[] = {
+    "scale_shift_table", "attn1.to_q.weight", "attn1.to_k.weight", "attn1.to_v.weight", "attn1.to_out.0.weight",
+    "attn1.to_out.0.bias", "attn2.to_q.weight", "attn2.to_q.bias", "attn2.to_k.weight", "attn2.to_k.bias",
+    "attn2.to_v.weight", "attn2.to_v.bias", "attn2.to_out.0.weight", "attn2.to_out.0.bias",
+    "ff.conv_inverted.weight", "ff.conv_inverted.bias", "ff.conv_depth.weight", "ff.conv_depth.bias",
+    "ff.conv_point.weight",
+};
+const char * const kTopRequired[] = {
+    "patch_embed.proj.weight", "patch_embed.proj.bias", "time_embed.emb.timestep_embedder.linear_1.weight",
+    "time_embed.emb.timestep_embedder.linear_1.bias", "time_embed.emb.timestep_embedder.linear_2.weight",
+    "time_embed.emb.timestep_embedder.linear_2.bias", "time_embed.linear.weight", "time_embed.linear.bias",
+    "caption_norm.weight", "scale_shift_table", "proj_out.weight", "proj_out.bias",
+};
+const char * const kCaptionRequired[] = {
+    "caption_projection.linear_1.weight", "caption_projection.linear_1.bias", "caption_projection.linear_2.weight",
+    "caption_projection.linear_2.bias", "caption_norm.weight",
+};
+
+std::string block_key(int64_t blk, const char * suffix) { return "blk" + std::to_string(blk) + "." + suffix; }
+
+void require(sana_dit * c, const std::string & key, const std::string & shown) {
+    if (!c->have.count(key)) throw_err(SANA_ERR_STATE, "weight not uploaded: " + shown);
+}
+
+void check_block(sana_dit * c, int64_t blk) {
+    for (const char * sfx : kBlockRequired)
+        require(c, block_key(blk, sfx), "transformer_blocks." + std::to_string(blk) + "." + sfx);
+}
+
+void check_context_weights(sana_dit * c, bool caption) {
+    if (caption)
+        for (const char * n : kCaptionRequired) require(c, n, n);
+    for (int64_t i = 0; i < c->L_; ++i)
+        for (const char * sfx : {"attn2.to_k.weight", "attn2.to_k.bias", "attn2.to_v.weight", "attn2.to_v.bias"})
+            require(c, block_key(i, sfx), "transformer_blocks." + std::to_string(i) + "." + sfx);
+}
+
 void check_ready(sana_dit * c) {
-    const size_t want = 12 + 4 + (size_t)c->L_ * 19;
-    if (c->have.size() != want) {
-        // name the first missing tensor
-        static const char * top[] = {"patch_embed.proj.weight", "patch_embed.proj.bias",
-                                     "time_embed.emb.timestep_embedder.linear_1.weight",
-                                     "time_embed.emb.timestep_embedder.linear_1.bias",
-                                     "time_embed.emb.timestep_embedder.linear_2.weight",
-                                     "time_embed.emb.timestep_embedder.linear_2.bias", "time_embed.linear.weight",
-                                     "time_embed.linear.bias", "caption_norm.weight", "scale_shift_table",
-                                     "proj_out.weight", "proj_out.bias", "caption_projection.linear_1.weight",
-                                     "caption_projection.linear_1.bias", "caption_projection.linear_2.weight",
-                                     "caption_projection.linear_2.bias"};
-        for (const char * n : top)
-            if (!c->have.count(n)) throw_err(SANA_ERR_STATE, std::string("weight not uploaded: ") + n);
-        throw_err(SANA_ERR_STATE, "block weights incomplete (" + std::to_string(c->have.size()) + " of " +
-                                      std::to_string(want) + " tensors uploaded)");
-    }
+    for (const char * n : kTopRequired) require(c, n, n);
+    for (const char * n : kCaptionRequired) require(c, n, n);
+    for (int64_t i = 0; i < c->L_; ++i) check_block(c, i);
 }
 
 void set_t(sana_dit * c, int64_t B, float t, hipStream_t s) {
@@ -507,6 +559,7 @@ int sana_dit_create(const sana_dit_config * cfg, sana_dit ** out) {
     if (cfg->hidden % cfg->cross_heads != 0)
         return set_err(SANA_ERR_INVALID_ARGUMENT, "cross attention hidden size must be divisible by cross_num_heads");
     if (cfg->hidden > 2048) return set_err(SANA_ERR_INVALID_ARGUMENT, "hidden > 2048 not supported");
+    if (cfg->latent_channels > 32) return set_err(SANA_ERR_INVALID_ARGUMENT, "latent_channels > 32 not supported");
     if (cfg->hidden / cfg->self_heads > 100) return set_err(SANA_ERR_INVALID_ARGUMENT, "self head_dim > 100");
     if (cfg->hidden / cfg->cross_heads > 256) return set_err(SANA_ERR_INVALID_ARGUMENT, "cross head_dim > 256");
     auto c = std::make_unique<sana_dit>();
@@ -634,6 +687,13 @@ int sana_dit_set_block_weight(sana_dit * c, int64_t blk, const char * suffix, co
             lin(w.w_qkv, C, C, c->Cp, C, 3 * C);
         } else if (s == "attn1.to_v.weight") {
             lin(w.w_qkv, C, C, c->Cp, 2 * C, 3 * C);
+        } else if (s == "attn1.to_q.bias" || s == "attn1.to_k.bias" || s == "attn1.to_v.bias") {
+            // not in any checkpoint (the reference loader injects zeros, src/transformer.cpp:361-362);
+            // accepted for weights built in memory
+            expect_shape(suffix, shape, ndim, {C});
+            const int64_t part = s == "attn1.to_q.bias" ? 0 : (s == "attn1.to_k.bias" ? 1 : 2);
+            upload_f32(w.b_qkv, data, C, (size_t)part * C, (size_t)3 * C);
+            w.has_qkv_bias = true;
         } else if (s == "attn1.to_out.0.weight") {
             lin(w.w_out, C, C, c->Cp, 0, C);
         } else if (s == "attn1.to_out.0.bias") {
@@ -719,7 +779,7 @@ int sana_dit_set_context(sana_dit * c, const float * data, int64_t B, int64_t L,
         return set_err(SANA_ERR_SHAPE, "context feature width %lld does not match %s", (long long)dim,
                        projected ? "hidden" : "caption_dim");
     return guarded([&] {
-        check_ready(c);
+        check_context_weights(c, projected == 0);
         ensure_context_buffers(c, B, L);
         const size_t n = (size_t)B * L * dim;
         DevMem & dst = projected ? c->ctx32 : c->cap32;
@@ -833,7 +893,7 @@ int sana_dit_block_forward(sana_dit * c, int64_t blk, const float * x, const flo
     const int64_t side = (int64_t)std::llround(std::sqrt((double)N));
     if (N <= 0 || side * side != N) return set_err(SANA_ERR_INVALID_ARGUMENT, "token count must form a square grid");
     return guarded([&] {
-        check_ready(c);
+        check_block(c, blk);
         ensure_forward_buffers(c, B, N);
         const size_t n = (size_t)B * N * c->C;
         hip_check(hipMemcpyAsync(c->x32.p, x, n * 4, hipMemcpyHostToDevice, c->stream), "upload x");
@@ -855,11 +915,124 @@ int sana_dit_block_forward(sana_dit * c, int64_t blk, const float * x, const flo
     });
 }
 
+int sana_dit_run_blocks(sana_dit * c, int64_t begin, int64_t end, const float * x, const float * t_mod, int64_t B,
+                        int64_t N, float * out) {
+    if (!c || !x || !t_mod || !out) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    if (begin < 0 || begin > end || end > c->L_) return set_err(SANA_ERR_INVALID_ARGUMENT, "invalid model block range");
+    if (!c->ctx_ready) return set_err(SANA_ERR_STATE, "no context set");
+    if (B != c->ctx_B) return set_err(SANA_ERR_INVALID_ARGUMENT, "input and context batch size must match");
+    const int64_t side = (int64_t)std::llround(std::sqrt((double)N));
+    if (N <= 0 || side * side != N) return set_err(SANA_ERR_INVALID_ARGUMENT, "token count must form a square grid");
+    return guarded([&] {
+        for (int64_t i = begin; i < end; ++i) check_block(c, i);
+        ensure_forward_buffers(c, B, N);
+        const size_t n = (size_t)B * N * c->C;
+        hip_check(hipMemcpyAsync(c->x32.p, x, n * 4, hipMemcpyHostToDevice, c->stream), "upload x");
+        hip_check(hipMemcpyAsync(c->tmod.p, t_mod, (size_t)B * 6 * c->C * 4, hipMemcpyHostToDevice, c->stream),
+                  "upload t_mod");
+        enqueue_mod(c, B, c->stream);
+        for (int64_t i = begin; i < end; ++i)
+            enqueue_block(c, i, B, N, c->ctx_bias ? c->bias.as<float>() : nullptr, c->stream);
+        hip_check(hipMemcpyAsync(out, c->x32.p, n * 4, hipMemcpyDeviceToHost, c->stream), "download x");
+        hip_check(hipStreamSynchronize(c->stream), "run_blocks");
+    });
+}
+
+namespace {
+
+float flow_lambda(float sigma) {  // log(alpha) - log(sigma) with alpha = 1 - sigma
+    return std::log(1.0f - sigma) - std::log(sigma);
+}
+
+// The whole loop on `s`: step i runs the forward at timesteps[i] on latent
+// buffer i % 2 and writes buffer (i + 1) % 2; the converted outputs of the two
+// latest steps alternate in loop_x0.  Returns the buffer holding the result.
+float * enqueue_loop(sana_dit * c, const float * d_latent, int64_t Bl, int64_t Hh, int64_t Ww, const float * ts,
+                     const float * sg, int64_t steps, float guidance, hipStream_t s) {
+    const int64_t n = Bl * c->Cl * Hh * Ww;
+    for (int k = 0; k < 2; ++k) {
+        c->loop_lat[k].ensure((size_t)n * 4, false);
+        c->loop_x0[k].ensure((size_t)n * 4, false);
+    }
+    hip_check(hipMemcpyAsync(c->loop_lat[0].p, d_latent, (size_t)n * 4, hipMemcpyDeviceToDevice, s), "latent");
+    for (int64_t i = 0; i < steps; ++i) {
+        float * cur = c->loop_lat[i & 1].as<float>();
+        float * nxt = c->loop_lat[(i + 1) & 1].as<float>();
+        int r = sana_dit_forward_device(c, cur, Bl, Hh, Ww, ts[i], c->np_out.as<float>(), s);
+        if (r != SANA_OK) throw_err(r, g_last_error);
+        // step_sana_scheduler (src/scheduler.cpp:272-318) with solver_order 2, midpoint,
+        // lower_order_final: first order at the first and at the last step.
+        const bool first = i == 0 || i == steps - 1;
+        const float st_v = sg[i + 1], s0_v = sg[i];
+        const float alpha_t = 1.0f - st_v;
+        const float h = flow_lambda(st_v) - flow_lambda(s0_v);
+        const float ca = st_v / s0_v, cb = -alpha_t * (std::exp(-h) - 1.0f);
+        float cc = 0.0f, inv_r0 = 0.0f;
+        if (!first) {
+            const float h0 = flow_lambda(s0_v) - flow_lambda(sg[i - 1]);
+            inv_r0 = 1.0f / (h0 / h);
+            cc = -0.5f * alpha_t * (std::exp(-h) - 1.0f);
+        }
+        hipLaunchKernelGGL(cfg_dpm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, c->np_out.as<float>(),
+                           cur, c->loop_x0[(i + 1) & 1].as<float>(), nxt, c->loop_x0[i & 1].as<float>(), (int)n,
+                           guidance, s0_v, ca, cb, cc, inv_r0, first ? 0 : 1);
+        hip_check(hipGetLastError(), "cfg_dpm");
+    }
+    return c->loop_lat[steps & 1].as<float>();
+}
+
+int check_loop_args(sana_dit * c, int64_t Bl, int64_t Hh, int64_t Ww, const float * ts, const float * sg,
+                    int64_t steps) {
+    int rc = check_forward_args(c, Bl, Hh, Ww);
+    if (rc) return rc;
+    if (!ts || !sg || steps <= 0) return set_err(SANA_ERR_INVALID_ARGUMENT, "schedule must have at least one step");
+    if (!c->ctx_ready) return set_err(SANA_ERR_STATE, "no context set");
+    if (c->ctx_B != 2 * Bl)
+        return set_err(SANA_ERR_INVALID_ARGUMENT, "context batch size must equal 2 * latent batch size for CFG");
+    for (int64_t i = 0; i < steps; ++i)
+        if (!(sg[i] > 0.0f && sg[i] < 1.0f)) return set_err(SANA_ERR_INVALID_ARGUMENT, "sigmas must lie in (0, 1)");
+    if (sg[steps] != 0.0f) return set_err(SANA_ERR_INVALID_ARGUMENT, "final sigma must be 0");
+    return SANA_OK;
+}
+
+}  // namespace
+
+int sana_dit_denoise_loop_device(sana_dit * c, const float * d_latent, int64_t Bl, int64_t Hh, int64_t Ww,
+                                 const float * timesteps, const float * sigmas, int64_t steps, float guidance,
+                                 float * d_final, void * stream) {
+    if (!c || !d_latent || !d_final) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = check_loop_args(c, Bl, Hh, Ww, timesteps, sigmas, steps);
+    if (rc) return rc;
+    return guarded([&] {
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        ensure_forward_buffers(c, 2 * Bl, Hh * Ww);
+        float * res = enqueue_loop(c, d_latent, Bl, Hh, Ww, timesteps, sigmas, steps, guidance, s);
+        hip_check(hipMemcpyAsync(d_final, res, (size_t)Bl * c->Cl * Hh * Ww * 4, hipMemcpyDeviceToDevice, s), "final");
+    });
+}
+
+int sana_dit_denoise_loop(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh, int64_t Ww,
+                          const float * timesteps, const float * sigmas, int64_t steps, float guidance,
+                          float * final_latent) {
+    if (!c || !latent || !final_latent) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    int rc = check_loop_args(c, Bl, Hh, Ww, timesteps, sigmas, steps);
+    if (rc) return rc;
+    return guarded([&] {
+        const int64_t n = Bl * c->Cl * Hh * Ww;
+        ensure_forward_buffers(c, 2 * Bl, Hh * Ww);
+        hip_check(hipMemcpyAsync(c->lat_in.p, latent, (size_t)n * 4, hipMemcpyHostToDevice, c->stream), "latent");
+        float * res = enqueue_loop(c, c->lat_in.as<float>(), Bl, Hh, Ww, timesteps, sigmas, steps, guidance, c->stream);
+        hip_check(hipMemcpyAsync(final_latent, res, (size_t)n * 4, hipMemcpyDeviceToHost, c->stream), "final");
+        hip_check(hipStreamSynchronize(c->stream), "denoise_loop");
+    });
+}
+
 int sana_dit_time_embed(sana_dit * c, const float * t, int64_t B, float * embedded, float * t_mod) {
     if (!c || !t) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
     if (B <= 0) return set_err(SANA_ERR_INVALID_ARGUMENT, "batch must be positive");
     return guarded([&] {
-        check_ready(c);
+        for (const char * n : kTopRequired) require(c, n, n);
+        for (int64_t i = 0; i < c->L_; ++i) require(c, block_key(i, "scale_shift_table"), "block scale_shift_table");
         ensure_forward_buffers(c, B, 1);
         hip_check(hipMemcpyAsync(c->d_t.p, t, (size_t)B * 4, hipMemcpyHostToDevice, c->stream), "upload t");
         enqueue_time(c, B, c->stream);

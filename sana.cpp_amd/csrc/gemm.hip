@@ -9,10 +9,11 @@
 // Data movement (gfx950):
 //   * HBM/L2 -> LDS with global_load_lds_dwordx4: each wave instruction moves
 //     8 rows x 64 k (1 KB) straight into LDS without passing through VGPRs.
-//   * A STAGES-deep ring of LDS k-tiles (BK = 64): tile kt+STAGES-1 is in flight
-//     while tile kt is multiplied, so HBM latency is covered by STAGES-1 tiles
-//     of MFMA work.  Completion is tracked with an explicit vmcnt wait (the
-//     loads of later tiles stay outstanding) and one s_barrier per k-tile.
+//   * A STAGES-deep ring of LDS k-tiles (BK = 64): when tile kt is done its
+//     stage is refilled with tile kt+STAGES, so each load has STAGES-1 tiles
+//     of MFMA work to land.  Completion is tracked with an explicit vmcnt
+//     wait (the loads of later tiles stay outstanding) and one s_barrier per
+//     k-tile, placed after the tile's last MFMAs are issued.
 //   * LDS rows are 128 bytes; 16-byte chunk c of row r is stored in slot
 //     c ^ (r & 7).  The DMA writes lane l to slot l & 7 of row l >> 3, so lane
 //     l fetches chunk (l & 7) ^ (l >> 3); an MFMA operand read (8 consecutive
@@ -22,9 +23,10 @@
 //     global accesses.
 //
 // The workgroup -> tile map is XCD-aware: gfx950 deals workgroups round-robin
-// to 8 XCDs (each with its own L2), so workgroup id i is mapped to tile
-// (i % 8) * (T / 8) + i / 8, giving each XCD a contiguous run of tiles in
-// n-fastest order that shares A row panels in its L2.
+// to 8 XCDs (each with its own L2), so workgroup id i goes to position
+// (i % 8) * (T / 8) + i / 8 of a grouped tile order (8 row panels at a time,
+// column by column): the tiles one XCD runs concurrently form a compact 2-D
+// block whose A and W panels are shared through its L2.
 //
 // Fused epilogues (reference ops they replace):
 //   store   : bias (+SiLU | +GELU-tanh), fp16 and/or fp32 out
@@ -68,34 +70,42 @@ struct Cfg {
     static constexpr int LDS_BYTES = (STAGES * STAGE_BYTES > EPI_BYTES) ? STAGES * STAGE_BYTES : EPI_BYTES;
     static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows must split into 8-row wave loads");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
-    static_assert(LOADS * (STAGES - 1) < 64, "vmcnt range");
+    static_assert(LOADS * STAGES < 64, "vmcnt range");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 };
 
-// Wait until at most `keep` stages of this wave's loads are outstanding.
+// Wait until at most `keep` stages (0 <= keep < STAGES) of this wave's loads are outstanding.
 template <int LOADS, int STAGES>
 SANA_DEV void wait_stages(int keep) {
     if constexpr (STAGES >= 4) {
-        if (keep >= 2) { wait_vmcnt<2 * LOADS>(); return; }
+        if (keep >= 3) { wait_vmcnt<3 * LOADS>(); return; }
     }
     if constexpr (STAGES >= 3) {
-        if (keep >= 1) { wait_vmcnt<LOADS>(); return; }
+        if (keep >= 2) { wait_vmcnt<2 * LOADS>(); return; }
     }
+    if (keep >= 1) { wait_vmcnt<LOADS>(); return; }
     wait_vmcnt<0>();
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int MODE>
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, int SCHED, int ACT>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
     using G = Cfg<BM, BN, WM, WN, STAGES>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
+    // Workgroup -> tile: XCD x (= id % 8) takes a contiguous range of tiles in
+    // a grouped order (kGroup row panels, column by column), so the tiles an
+    // XCD runs together form a compact block whose A and W panels stay in its L2.
     const int ntn = (p.N + BN - 1) / BN;
     const int ntm = (p.M + BM - 1) / BM;
     const int nwg = ntn * ntm;
     const int id = blockIdx.x;
     const int per = nwg / 8;
-    const int tile = (id < per * 8) ? (id % 8) * per + id / 8 : id;
-    const int tm = tile / ntn, tn = tile % ntn;
+    const int order = (id < per * 8) ? (id % 8) * per + id / 8 : id;
+    constexpr int kGroup = 8;
+    const int gsz = kGroup * ntn;
+    const int grp = order / gsz, gm = min(kGroup, ntm - grp * kGroup);
+    const int within = order - grp * gsz;
+    const int tm = grp * kGroup + within % gm, tn = within / gm;
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int tid = threadIdx.x;
@@ -143,42 +153,87 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
     const int brow0 = wn * G::WTN + (lane & 31);
     const int khalf = lane >> 5;
 
+    // Operand fragments are double-buffered in registers: the LDS reads of
+    // k-step s+1 are in flight while the MFMAs of step s run.  The tile
+    // boundary (wait for the next tile's DMA, barrier, refill the freed stage)
+    // is placed after the last step's MFMAs are issued, so it overlaps them.
+    constexpr int NS = kBK / 16;               // MFMA k-steps per tile
+    constexpr int NB = SCHED == 1 ? NS : 2;    // fragment buffers
+    f16x8 af[NB][G::TM], bf[NB][G::TN];
+    auto load_frags = [&](int stage, int s, int buf) {
+        const unsigned char * sa = smem + stage * G::STAGE_BYTES;
+        const unsigned char * sb = sa + G::A_BYTES;
+        const int ch = 2 * s + khalf;
+#pragma unroll
+        for (int i = 0; i < G::TM; ++i) {
+            const int R = arow0 + i * 32;
+            af[buf][i] = *reinterpret_cast<const f16x8 *>(sa + R * 128 + ((ch ^ (R & 7)) << 4));
+        }
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j) {
+            const int R = brow0 + j * 32;
+            bf[buf][j] = *reinterpret_cast<const f16x8 *>(sb + R * 128 + ((ch ^ (R & 7)) << 4));
+        }
+    };
+    auto mfmas = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < G::TN; ++j) acc[i][j] = mfma_32x32x16(af[buf][i], bf[buf][j], acc[i][j]);
+    };
+
     const int KT = p.K / kBK;
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
+    for (int s = 0; s < STAGES; ++s)
         if (s < KT) issue(s, s);
-
-    for (int kt = 0; kt < KT; ++kt) {
-        // Tile kt has landed once at most min(STAGES-2, KT-1-kt) later stages are still in flight.
-        wait_stages<G::LOADS, STAGES>(min(STAGES - 2, KT - 1 - kt));
-        __builtin_amdgcn_s_barrier();
-        if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        const unsigned char * sa = smem + (kt % STAGES) * G::STAGE_BYTES;
-        const unsigned char * sb = sa + G::A_BYTES;
-        // Operand fragments are double-buffered in registers: the reads of
-        // k-step s+1 are issued before the MFMAs of step s.
-        f16x8 af[2][G::TM], bf[2][G::TN];
-        auto load_frags = [&](int s, int buf) {
-            const int ch = 2 * s + khalf;
+    wait_stages<G::LOADS, STAGES>(min(STAGES - 1, KT - 1));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (SCHED == 1) {
+        // every fragment of the tile is requested right after the barrier; the
+        // MFMAs of step s wait only for the reads of steps <= s (in-order lgkmcnt)
+        for (int kt = 0; kt < KT; ++kt) {
+            const int st = kt % STAGES;
 #pragma unroll
-            for (int i = 0; i < G::TM; ++i) {
-                const int R = arow0 + i * 32;
-                af[buf][i] = *reinterpret_cast<const f16x8 *>(sa + R * 128 + ((ch ^ (R & 7)) << 4));
+            for (int s = 0; s < NS; ++s) load_frags(st, s, s);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) mfmas(s);
+            if (kt + 1 < KT) {
+                __builtin_amdgcn_sched_barrier(0);
+                wait_stages<G::LOADS, STAGES>(min(STAGES - 2, KT - 2 - kt));
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                if (kt + STAGES < KT) issue(kt + STAGES, st);
             }
+        }
+    } else {
+        // Operand fragments double-buffered in registers: the LDS reads of
+        // k-step s+1 are in flight while the MFMAs of step s run.  The tile
+        // boundary (wait for the next tile's DMA, barrier, refill the freed
+        // stage) follows the last step's MFMAs, so it overlaps them.
+        load_frags(0, 0, 0);
+        for (int kt = 0; kt < KT; ++kt) {
+            const int st = kt % STAGES;
 #pragma unroll
-            for (int j = 0; j < G::TN; ++j) {
-                const int R = brow0 + j * 32;
-                bf[buf][j] = *reinterpret_cast<const f16x8 *>(sb + R * 128 + ((ch ^ (R & 7)) << 4));
+            for (int s = 0; s < NS - 1; ++s) {
+                load_frags(st, s + 1, (s + 1) & 1);
+                mfmas(s & 1);
+                if constexpr (SCHED == 2) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, G::TM + G::TN, 0);  // DS reads of step s+1
+                    __builtin_amdgcn_sched_group_barrier(0x008, G::TM * G::TN, 0);  // then MFMAs of step s
+                }
             }
-        };
-        load_frags(0, 0);
-#pragma unroll
-        for (int s = 0; s < kBK / 16; ++s) {
-            if (s + 1 < kBK / 16) load_frags(s + 1, (s + 1) & 1);
-#pragma unroll
-            for (int i = 0; i < G::TM; ++i)
-#pragma unroll
-                for (int j = 0; j < G::TN; ++j) acc[i][j] = mfma_32x32x16(af[s & 1][i], bf[s & 1][j], acc[i][j]);
+            mfmas((NS - 1) & 1);
+            if (kt + 1 < KT) {
+                __builtin_amdgcn_sched_barrier(0);
+                // tile kt+1 has landed (this wave's DMA), then every wave's has and
+                // every wave is done reading stage st, which takes tile kt+STAGES.
+                wait_stages<G::LOADS, STAGES>(min(STAGES - 2, KT - 2 - kt));
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                if (kt + STAGES < KT) issue(kt + STAGES, st);
+                load_frags((kt + 1) % STAGES, 0, 0);
+            }
         }
     }
 
@@ -221,23 +276,39 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                 }
             }
         __syncthreads();
-        constexpr int CPR = BN / 8;  // 8-column chunks per row
-        for (int q = tid; q < BM * CPR; q += G::NT) {
-            const int rr = q / CPR, c8 = (q - rr * CPR) * 8;
-            const int row = m0 + rr, col = n0 + c8;
-            if (row >= p.M || col >= p.N) continue;
+        // Each thread owns one 8-column chunk of the tile for all its rows, so
+        // the bias is fetched once; rows step by NT / CPR.
+        constexpr int CPR = BN / 8;
+        static_assert(G::NT % CPR == 0, "epilogue chunk mapping");
+        const int c8 = (tid % CPR) * 8;
+        const int col = n0 + c8;
+        const int nc = min(8, p.N - col);
+        if (nc <= 0) return;
+        const bool vec8 = p.vec && nc == 8;
+        float bv[8];
+        if (p.bias && vec8) {
+            const float4 b0 = *reinterpret_cast<const float4 *>(p.bias + col);
+            const float4 b1 = *reinterpret_cast<const float4 *>(p.bias + col + 4);
+            bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
+            bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bv[e] = (p.bias && e < nc) ? p.bias[col + e] : 0.0f;
+        }
+        for (int rr = tid / CPR; rr < BM; rr += G::NT / CPR) {
+            const int row = m0 + rr;
+            if (row >= p.M) break;
             const float4 v0 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8]);
             const float4 v1 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8 + 4]);
-            float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            const int nc = min(8, p.N - col);
-            if (MODE == kGemmStore) {
+            float v[8] = {v0.x + bv[0], v0.y + bv[1], v0.z + bv[2], v0.w + bv[3],
+                          v1.x + bv[4], v1.y + bv[5], v1.z + bv[6], v1.w + bv[7]};
+            if constexpr (MODE == kGemmStore) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    if (p.bias && e < nc) v[e] += p.bias[col + e];
-                    if (p.act == kActSilu) v[e] = silu_f(v[e]);
-                    else if (p.act == kActGelu) v[e] = gelu_tanh_f(v[e]);
+                    if constexpr (ACT == kActSilu) v[e] = silu_f(v[e]);
+                    if constexpr (ACT == kActGelu) v[e] = gelu_tanh_f(v[e]);
                 }
-                if (nc == 8 && p.vec) {
+                if (vec8) {
                     if (p.out16) {
                         f16x8 h;
 #pragma unroll
@@ -257,21 +328,36 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                 }
             } else {  // kGemmResidual: x += gate * (acc + bias)
                 const int b = row / p.rows_per_batch;
-                const float * ga = p.gate_a ? p.gate_a + (int64_t)b * p.gate_stride + col : nullptr;
-                const float * gt = p.gate_t ? p.gate_t + col : nullptr;
-                float * xr = p.out32 + (int64_t)row * p.ldo32 + col;
-                if (nc == 8 && p.vec) {
-                    float x[8], g[8];
-                    const float4 x0 = *reinterpret_cast<const float4 *>(xr);
-                    const float4 x1 = *reinterpret_cast<const float4 *>(xr + 4);
-                    x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
-                    x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+                float g[8];
+                if (p.gate_a && vec8) {
+                    const float * ga = p.gate_a + (int64_t)b * p.gate_stride + col;
+                    const float4 g0 = *reinterpret_cast<const float4 *>(ga);
+                    const float4 g1 = *reinterpret_cast<const float4 *>(ga + 4);
+                    g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
+                    g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+                    if (p.gate_t) {
+                        const float4 t0 = *reinterpret_cast<const float4 *>(p.gate_t + col);
+                        const float4 t1 = *reinterpret_cast<const float4 *>(p.gate_t + col + 4);
+                        g[0] += t0.x; g[1] += t0.y; g[2] += t0.z; g[3] += t0.w;
+                        g[4] += t1.x; g[5] += t1.y; g[6] += t1.z; g[7] += t1.w;
+                    }
+                } else {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        g[e] = ga ? ga[e] + (gt ? gt[e] : 0.0f) : 1.0f;
-                        const float y = v[e] + (p.bias ? p.bias[col + e] : 0.0f);
-                        x[e] = x[e] + g[e] * y;
+                        g[e] = 1.0f;
+                        if (p.gate_a && e < nc) {
+                            g[e] = p.gate_a[(int64_t)b * p.gate_stride + col + e];
+                            if (p.gate_t) g[e] += p.gate_t[col + e];
+                        }
                     }
+                }
+                float * xr = p.out32 + (int64_t)row * p.ldo32 + col;
+                if (vec8) {
+                    const float4 x0 = *reinterpret_cast<const float4 *>(xr);
+                    const float4 x1 = *reinterpret_cast<const float4 *>(xr + 4);
+                    float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] = x[e] + g[e] * v[e];
                     *reinterpret_cast<float4 *>(xr) = make_float4(x[0], x[1], x[2], x[3]);
                     *reinterpret_cast<float4 *>(xr + 4) = make_float4(x[4], x[5], x[6], x[7]);
                     if (p.out16) {
@@ -282,9 +368,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                     }
                 } else {
                     for (int e = 0; e < nc; ++e) {
-                        const float g = ga ? ga[e] + (gt ? gt[e] : 0.0f) : 1.0f;
-                        const float y = v[e] + (p.bias ? p.bias[col + e] : 0.0f);
-                        const float nx = xr[e] + g * y;
+                        const float nx = xr[e] + g[e] * v[e];
                         xr[e] = nx;
                         if (p.out16) reinterpret_cast<f16 *>(p.out16)[(int64_t)row * p.ldo16 + col + e] = (f16)nx;
                     }
@@ -298,22 +382,25 @@ bool set_lds_limit(const void * k, size_t lds) {
     return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int MODE>
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, int SCHED, int ACT>
 hipError_t launch_mode(const GemmParams & p, int tiles, hipStream_t s) {
     using G = Cfg<BM, BN, WM, WN, STAGES>;
-    static const bool attr = set_lds_limit(reinterpret_cast<const void *>(&gemm_kernel<BM, BN, WM, WN, STAGES, MODE>),
-                                           G::LDS_BYTES);
+    static const bool attr = set_lds_limit(
+        reinterpret_cast<const void *>(&gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT>), G::LDS_BYTES);
     (void)attr;
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, STAGES, MODE>), dim3(tiles), dim3(G::NT), G::LDS_BYTES, s, p);
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT>), dim3(tiles), dim3(G::NT),
+                       G::LDS_BYTES, s, p);
     return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES>
+template <int BM, int BN, int WM, int WN, int STAGES, int SCHED = 0>
 hipError_t launch(const GemmParams & p, hipStream_t s) {
     const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    if (p.mode == kGemmResidual) return launch_mode<BM, BN, WM, WN, STAGES, kGemmResidual>(p, tiles, s);
-    if (p.mode == kGemmVT) return launch_mode<BM, BN, WM, WN, STAGES, kGemmVT>(p, tiles, s);
-    return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore>(p, tiles, s);
+    if (p.mode == kGemmResidual) return launch_mode<BM, BN, WM, WN, STAGES, kGemmResidual, SCHED, kActNone>(p, tiles, s);
+    if (p.mode == kGemmVT) return launch_mode<BM, BN, WM, WN, STAGES, kGemmVT, SCHED, kActNone>(p, tiles, s);
+    if (p.act == kActSilu) return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActSilu>(p, tiles, s);
+    if (p.act == kActGelu) return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActGelu>(p, tiles, s);
+    return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActNone>(p, tiles, s);
 }
 
 }  // namespace gemm_detail
@@ -335,34 +422,41 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     bool vec = true;
     if (p.out16) vec = vec && p.ldo16 % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out16) & 15) == 0;
     if (p.out32) vec = vec && p.ldo32 % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out32) & 15) == 0;
-    if (p.gate_a) vec = vec && p.gate_stride % 4 == 0;
+    if (p.gate_a) vec = vec && p.gate_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(p.gate_a) & 15) == 0;
+    if (p.gate_t) vec = vec && (reinterpret_cast<uintptr_t>(p.gate_t) & 15) == 0;
+    if (p.bias) vec = vec && (reinterpret_cast<uintptr_t>(p.bias) & 15) == 0;
     p.vec = vec ? 1 : 0;
     static const int forced = [] {
         const char * e = std::getenv("SANA_GEMM_VARIANT");
         return e ? std::atoi(e) : -1;
     }();
     switch (forced) {
-        case 0: return launch<128, 128, 2, 2, 4>(p, s);
-        case 1: return launch<128, 128, 2, 2, 3>(p, s);
-        case 2: return launch<128, 128, 2, 2, 2>(p, s);
-        case 3: return launch<128, 64, 2, 2, 4>(p, s);
-        case 4: return launch<64, 64, 2, 2, 4>(p, s);
-        case 5: return launch<256, 128, 2, 2, 3>(p, s);
-        case 6: return launch<128, 256, 2, 2, 3>(p, s);
-        case 7: return launch<64, 128, 2, 2, 4>(p, s);
-        case 8: return launch<128, 64, 2, 2, 2>(p, s);
-        case 9: return launch<64, 64, 2, 2, 2>(p, s);
-        case 10: return launch<256, 128, 2, 2, 2>(p, s);
-        case 11: return launch<128, 128, 1, 4, 3>(p, s);
+        case 0: return launch<128, 128, 2, 2, 2, 0>(p, s);
+        case 1: return launch<128, 128, 2, 2, 2, 1>(p, s);
+        case 2: return launch<128, 128, 2, 2, 2, 2>(p, s);
+        case 3: return launch<128, 128, 2, 2, 3, 0>(p, s);
+        case 4: return launch<128, 128, 2, 2, 3, 1>(p, s);
+        case 5: return launch<128, 128, 2, 2, 3, 2>(p, s);
+        case 6: return launch<128, 64, 2, 2, 2, 0>(p, s);
+        case 7: return launch<128, 64, 2, 2, 2, 1>(p, s);
+        case 8: return launch<128, 64, 2, 2, 3, 1>(p, s);
+        case 9: return launch<64, 64, 2, 2, 2, 0>(p, s);
+        case 10: return launch<64, 64, 2, 2, 2, 1>(p, s);
+        case 11: return launch<64, 64, 2, 2, 4, 1>(p, s);
+        case 12: return launch<256, 128, 2, 2, 3, 1>(p, s);
+        case 13: return launch<256, 128, 2, 2, 3, 2>(p, s);
+        case 14: return launch<128, 256, 2, 2, 3, 1>(p, s);
+        case 15: return launch<128, 128, 2, 2, 4, 1>(p, s);
+        case 16: return launch<128, 128, 2, 2, 4, 2>(p, s);
+        case 17: return launch<128, 64, 2, 2, 4, 1>(p, s);
         default: break;
     }
-    // Tile choice from measured sweeps on MI355X: small grids (<= 160 tiles of
-    // 128x128) need 64x64 tiles to occupy the 256 CUs; otherwise two-stage
-    // 128-row tiles keep two workgroups resident per CU.
+    // Tile choice from measured sweeps on MI355X: grids of <= 160 128x128
+    // tiles use 64x64 tiles to occupy the 256 CUs; otherwise 128x128 tiles with
+    // two stages keep two workgroups resident per CU.
     const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
-    if (t128 <= 160) return launch<64, 64, 2, 2, 2>(p, s);
-    if (p.K >= 2048 || (t128 >= 300 && t128 <= 500) || t128 >= 2000) return launch<128, 128, 2, 2, 2>(p, s);
-    return launch<128, 64, 2, 2, 2>(p, s);
+    if (t128 <= 160) return launch<64, 64, 2, 2, 2, 1>(p, s);
+    return launch<128, 128, 2, 2, 2, 1>(p, s);
 }
 
 }  // namespace sana

@@ -78,9 +78,10 @@ hipError_t patch_embed(const float * latent, int Bl, int B, int Cl, int S, const
                        float * out, int C, hipStream_t s);
 
 // Final layer: LN(eps, no affine) + modulate(shift = emb + T[0], scale = emb + T[1])
-// + proj (Wt [C, Cl] fp32, bias [Cl]) stored NCHW [B, Cl, S].
+// into y [B*S, C] fp32 (workspace), then proj (Wt [C, Cl] fp32, bias [Cl],
+// Cl <= 32) stored NCHW [B, Cl, S].
 hipError_t final_layer(const float * x, const float * emb, const float * table, const float * Wt, const float * bias,
-                       float * out, int B, int S, int C, int Cl, float eps, hipStream_t s);
+                       float * y, float * out, int B, int S, int C, int Cl, float eps, hipStream_t s);
 
 // ReLU linear attention.  q/k/v fp16 token-major with row stride ld (head h at
 // columns h*D..), out fp16 with row stride ldo.  Workspace: partial states.

@@ -205,141 +205,184 @@ __global__ void sinusoid_kernel(const float * __restrict__ t, const float * __re
 __global__ __launch_bounds__(256) void gemv_kernel(const float * __restrict__ in, const float * __restrict__ W,
                                                    const float * __restrict__ bias, float * __restrict__ out, int B,
                                                    int K, int N, int act_in) {
-    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    constexpr int kRows = 4;  // outputs per wave: their weight rows are streamed together
+    const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kRows;
     const int lane = threadIdx.x & 63;
-    if (n >= N) return;
-    const float4 * wr = reinterpret_cast<const float4 *>(W + (int64_t)n * K);
+    if (n0 >= N) return;
     const int k4n = K >> 2;
-    for (int b0 = 0; b0 < B; b0 += 8) {
-        float acc[8];
+    for (int b0 = 0; b0 < B; b0 += 2) {
+        float acc[kRows][2];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+        for (int r = 0; r < kRows; ++r) acc[r][0] = acc[r][1] = 0.0f;
         for (int k4 = lane; k4 < k4n; k4 += 64) {
-            const float4 w = wr[k4];
+            float4 a[2];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                if (b0 + j < B) {
-                    float4 a = reinterpret_cast<const float4 *>(in + (int64_t)(b0 + j) * K)[k4];
-                    if (act_in == 1) {
-                        a.x = silu_f(a.x); a.y = silu_f(a.y); a.z = silu_f(a.z); a.w = silu_f(a.w);
-                    }
-                    acc[j] += (a.x * w.x + a.y * w.y) + (a.z * w.z + a.w * w.w);
+            for (int j = 0; j < 2; ++j) {
+                a[j] = b0 + j < B ? reinterpret_cast<const float4 *>(in + (int64_t)(b0 + j) * K)[k4]
+                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (act_in == 1) {
+                    a[j].x = silu_f(a[j].x); a[j].y = silu_f(a[j].y); a[j].z = silu_f(a[j].z); a[j].w = silu_f(a[j].w);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) {
+                if (n0 + r < N) {
+                    const float4 w = reinterpret_cast<const float4 *>(W + (int64_t)(n0 + r) * K)[k4];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[r][j] += (a[j].x * w.x + a[j].y * w.y) + (a[j].z * w.z + a[j].w * w.w);
                 }
             }
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float r = wave_sum(acc[j]);
-            if (lane == 0 && b0 + j < B) out[(int64_t)(b0 + j) * N + n] = r + (bias ? bias[n] : 0.0f);
-        }
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float v = wave_sum(acc[r][j]);
+                if (lane == 0 && n0 + r < N && b0 + j < B) out[(int64_t)(b0 + j) * N + n0 + r] = v + (bias ? bias[n0 + r] : 0.0f);
+            }
     }
 }
 
 // conv2d_1x1 patch embed (src/common_ops.cpp:322-405) writing token-major
-// [B, S, C]; weight transposed to [Cl, C] on upload so reads coalesce.  A
-// block handles 8 tokens: their Cl input channels are staged in LDS and each
-// thread produces output channels c = tid, tid + 256, ... for the 8 tokens
-// (bias first, then input channels in order, as the reference accumulates).
-constexpr int kPatchTok = 8;
+// [B, S, C] with v_mfma_f32_32x32x2_f32 (fp32 products, fp32 accumulation):
+// out[s][c] = bias[c] + sum_ic lat[ic][s] * Wt[ic][c], weight transposed to
+// [Cl, C] on upload.  One wave per 32 tokens x 32 channels; the A operand
+// (lane: token l%32, channel pair l/32) and the B operand (lane: channel
+// pair l/32, output l%32) are both contiguous across lanes.
 __global__ __launch_bounds__(256) void patch_embed_kernel(const float * __restrict__ latent, int Bl, int Cl, int S,
                                                           const float * __restrict__ Wt,
                                                           const float * __restrict__ bias, float * __restrict__ out,
                                                           int C) {
-    extern __shared__ float lat_s[];  // [Cl][kPatchTok]
-    const int s0 = blockIdx.x * kPatchTok;
-    const int b = blockIdx.y;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int c0 = (blockIdx.x * 4 + w) * 32;
+    const int s0 = blockIdx.y * 32;
+    const int b = blockIdx.z;
+    if (c0 >= C) return;
     const float * lat = latent + (int64_t)(b % Bl) * Cl * S;
-    for (int i = threadIdx.x; i < Cl * kPatchTok; i += blockDim.x) {
-        const int ic = i / kPatchTok, t = i - ic * kPatchTok;
-        lat_s[i] = (s0 + t < S) ? lat[(int64_t)ic * S + s0 + t] : 0.0f;
+    const int s = s0 + (lane & 31), c = c0 + (lane & 31), kh = lane >> 5;
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    for (int ic = 0; ic < Cl; ic += 2) {
+        const int k = ic + kh;
+        const float a = (k < Cl && s < S) ? lat[(int64_t)k * S + s] : 0.0f;
+        const float bw = (k < Cl && c < C) ? Wt[(int64_t)k * C + c] : 0.0f;
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bw, acc, 0, 0, 0);
     }
-    __syncthreads();
-    for (int c = threadIdx.x; c < C; c += blockDim.x) {
-        float acc[kPatchTok];
-        const float bv = bias ? bias[c] : 0.0f;
+    if (c >= C) return;
+    const float bv = bias ? bias[c] : 0.0f;
 #pragma unroll
-        for (int t = 0; t < kPatchTok; ++t) acc[t] = bv;
-#pragma unroll 8
-        for (int ic = 0; ic < Cl; ++ic) {
-            const float w = Wt[(int64_t)ic * C + c];
-#pragma unroll
-            for (int t = 0; t < kPatchTok; ++t) acc[t] += lat_s[ic * kPatchTok + t] * w;
-        }
-#pragma unroll
-        for (int t = 0; t < kPatchTok; ++t)
-            if (s0 + t < S) out[((int64_t)b * S + s0 + t) * C + c] = acc[t];
+    for (int i = 0; i < 16; ++i) {
+        const int row = s0 + 8 * (i >> 2) + 4 * kh + (i & 3);
+        if (row < S) out[((int64_t)b * S + row) * C + c] = acc[i] + bv;
     }
 }
 
-// Final layer (src/transformer.cpp:668-681): LN(eps, no affine), modulate with
-// shift = emb + T[0], scale = emb + T[1] (compute_final_modulation, :126-163),
-// proj_out C -> Cl (+bias), stored NCHW [B, Cl, S] (tokens_to_grid_4d).  A
-// block handles kFinalRows rows: each wave normalises rows into LDS, then
-// thread (row, o) reduces over C with Wt [C, Cl] (o contiguous).
-constexpr int kFinalRows = 8;
-__global__ __launch_bounds__(256) void final_layer_kernel(const float * __restrict__ x, const float * __restrict__ emb,
-                                                          const float * __restrict__ T, const float * __restrict__ Wt,
-                                                          const float * __restrict__ bias, float * __restrict__ out,
-                                                          int B, int S, int C, int Cl, float eps) {
-    extern __shared__ float xs[];  // [kFinalRows][C]
+// Final layer (src/transformer.cpp:668-681), first half: LN(eps, no affine)
+// and modulate with shift = emb + T[0], scale = emb + T[1]
+// (compute_final_modulation, :126-163), fp32 rows out.  One wave per row.
+__global__ __launch_bounds__(256) void final_norm_kernel(const float * __restrict__ x, const float * __restrict__ emb,
+                                                         const float * __restrict__ T, float * __restrict__ y, int B,
+                                                         int S, int C, float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= B * S) return;
+    const int b = row / S;
+    const float * xr = x + (int64_t)row * C;
+    float v[kMaxPerLane];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+        const int c = lane + 64 * i;
+        v[i] = c < C ? xr[c] : 0.0f;
+        sum += v[i];
+    }
+    const float mean = wave_sum(sum) / (float)C;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+        const int c = lane + 64 * i;
+        if (c < C) {
+            const float d = v[i] - mean;
+            q += d * d;
+        }
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(q) / (float)C + eps);
+    const float * e = emb + (int64_t)b * C;
+    float * yr = y + (int64_t)row * C;
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+        const int c = lane + 64 * i;
+        if (c < C) {
+            const float sh = e[c] + T[c], sc = e[c] + T[C + c];
+            yr[c] = ((v[i] - mean) * inv) * (1.0f + sc) + sh;
+        }
+    }
+}
+
+// Final layer, second half: proj_out C -> Cl (+bias), stored NCHW [B, Cl, S]
+// (tokens_to_grid_4d), on v_mfma_f32_32x32x2_f32 (fp32 products and sums).
+// A workgroup covers 32 rows; its 4 waves split C into quarters and their
+// 32x32 partial tiles are summed in LDS in fixed order.  Lane (row l%32,
+// half h = l/32) loads 4 consecutive channels c0 + 4h .. c0 + 4h + 3 of its row
+// with one 16-byte load and feeds them to 4 MFMAs; the B operand supplies the
+// same channel order (the reduction order over C is permuted, not its terms).
+__global__ __launch_bounds__(256) void proj_out_kernel(const float * __restrict__ y, const float * __restrict__ Wt,
+                                                       const float * __restrict__ bias, float * __restrict__ out,
+                                                       int B, int S, int C, int Cl) {
+    __shared__ float part[4][32][33];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int r0 = blockIdx.x * kFinalRows;
-    for (int rr = w; rr < kFinalRows; rr += 4) {
-        const int row = r0 + rr;
-        float * dst = xs + rr * C;
-        if (row >= B * S) {
-            for (int c = lane; c < C; c += 64) dst[c] = 0.0f;
-            continue;
-        }
-        const int b = row / S;
-        const float * xr = x + (int64_t)row * C;
-        float v[kMaxPerLane];
-        float sum = 0.0f;
+    const int r0 = blockIdx.x * 32;
+    const int rows = B * S;
+    const int rr = min(r0 + (lane & 31), rows - 1);
+    const int h = lane >> 5, n = lane & 31;
+    const int q = C / 4;  // channels per wave (C % 128 == 0)
+    const float * yr = y + (int64_t)rr * C;
+    f32x16 acc;
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
-            const int c = lane + 64 * i;
-            v[i] = c < C ? xr[c] : 0.0f;
-            sum += v[i];
-        }
-        const float mean = wave_sum(sum) / (float)C;
-        float q = 0.0f;
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    // 32 channels per iteration: all loads of the iteration are issued before its 16 MFMAs
+    for (int c0 = w * q; c0 < (w + 1) * q; c0 += 32) {
+        float av[4][4], bw[4][4];
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
-            const int c = lane + 64 * i;
-            if (c < C) {
-                const float d = v[i] - mean;
-                q += d * d;
-            }
-        }
-        const float inv = 1.0f / sqrtf(wave_sum(q) / (float)C + eps);
-        const float * e = emb + (int64_t)b * C;
+        for (int u = 0; u < 4; ++u) {
+            const float4 a = *reinterpret_cast<const float4 *>(yr + c0 + 8 * u + 4 * h);
+            av[u][0] = a.x; av[u][1] = a.y; av[u][2] = a.z; av[u][3] = a.w;
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
-            const int c = lane + 64 * i;
-            if (c < C) {
-                const float sh = e[c] + T[c], sc = e[c] + T[C + c];
-                dst[c] = ((v[i] - mean) * inv) * (1.0f + sc) + sh;
-            }
+            for (int e = 0; e < 4; ++e) bw[u][e] = n < Cl ? Wt[(int64_t)(c0 + 8 * u + 4 * h + e) * Cl + n] : 0.0f;
         }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u][e], bw[u][e], acc, 0, 0, 0);
     }
+    // lane holds output column n, rows 8*(i/4) + 4*h + i%4
+#pragma unroll
+    for (int i = 0; i < 16; ++i) part[w][8 * (i >> 2) + 4 * h + (i & 3)][n] = acc[i];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < kFinalRows * Cl; idx += blockDim.x) {
-        const int rr = idx / Cl, o = idx - rr * Cl;
-        const int row = r0 + rr;
-        if (row >= B * S) continue;
-        const float * xv = xs + rr * C;
-        // 8 independent partial sums so the Wt loads of 8 channels are in flight together
-        float pp[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        int c = 0;
-        for (; c + 8 <= C; c += 8) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) pp[u] += xv[c + u] * Wt[(int64_t)(c + u) * Cl + o];
-        }
-        for (; c < C; ++c) pp[0] += xv[c] * Wt[(int64_t)c * Cl + o];
-        const float p = ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
+    for (int idx = threadIdx.x; idx < 32 * 32; idx += 256) {
+        const int r = idx >> 5, o = idx & 31;
+        const int row = r0 + r;
+        if (row >= rows || o >= Cl) continue;
+        const float v = ((part[0][r][o] + part[1][r][o]) + (part[2][r][o] + part[3][r][o])) + (bias ? bias[o] : 0.0f);
         const int b = row / S, sidx = row - b * S;
-        out[((int64_t)b * Cl + o) * S + sidx] = p + (bias ? bias[o] : 0.0f);
+        out[((int64_t)b * Cl + o) * S + sidx] = v;
     }
+}
+
+// Plain fp32 proj_out for hidden sizes that are not a multiple of 32.
+__global__ __launch_bounds__(256) void proj_out_scalar_kernel(const float * __restrict__ y,
+                                                              const float * __restrict__ Wt,
+                                                              const float * __restrict__ bias,
+                                                              float * __restrict__ out, int B, int S, int C, int Cl) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= B * S * Cl) return;
+    const int row = idx / Cl, o = idx - row * Cl;
+    float p = 0.0f;
+    for (int c = 0; c < C; ++c) p += y[(int64_t)row * C + c] * Wt[(int64_t)c * Cl + o];
+    const int b = row / S, sidx = row - b * S;
+    out[((int64_t)b * Cl + o) * S + sidx] = p + (bias ? bias[o] : 0.0f);
 }
 
 }  // namespace
@@ -400,24 +443,31 @@ hipError_t gemv_f32(const float * in, const float * W, const float * bias, float
     if (B <= 0 || K <= 0 || N <= 0 || K % 4 ||
         ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemv_kernel, dim3((N + 3) / 4), dim3(256), 0, s, in, W, bias, out, B, K, N, act_in);
+    hipLaunchKernelGGL(gemv_kernel, dim3((N + 15) / 16), dim3(256), 0, s, in, W, bias, out, B, K, N, act_in);
     return hipGetLastError();
 }
 
 hipError_t patch_embed(const float * latent, int Bl, int B, int Cl, int S, const float * Wt, const float * bias,
                        float * out, int C, hipStream_t s) {
-    if (Bl <= 0 || B <= 0 || Cl <= 0 || Cl > 1024 || S <= 0 || C <= 0 || B > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(patch_embed_kernel, dim3((S + kPatchTok - 1) / kPatchTok, B), dim3(256),
-                       sizeof(float) * Cl * kPatchTok, s, latent, Bl, Cl, S, Wt, bias, out, C);
+    if (Bl <= 0 || B <= 0 || Cl <= 0 || S <= 0 || C <= 0 || B > 65535 || (S + 31) / 32 > 65535)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(patch_embed_kernel, dim3((C + 127) / 128, (S + 31) / 32, B), dim3(256), 0, s, latent, Bl, Cl, S,
+                       Wt, bias, out, C);
     return hipGetLastError();
 }
 
 hipError_t final_layer(const float * x, const float * emb, const float * table, const float * Wt, const float * bias,
-                       float * out, int B, int S, int C, int Cl, float eps, hipStream_t s) {
-    if (B <= 0 || S <= 0 || C <= 0 || C > 64 * kMaxPerLane || Cl <= 0) return hipErrorInvalidValue;
+                       float * y, float * out, int B, int S, int C, int Cl, float eps, hipStream_t s) {
+    if (B <= 0 || S <= 0 || C <= 0 || C > 64 * kMaxPerLane || Cl <= 0 || Cl > 32 || !y ||
+        (reinterpret_cast<uintptr_t>(y) & 15))
+        return hipErrorInvalidValue;
     const int rows = B * S;
-    hipLaunchKernelGGL(final_layer_kernel, dim3((rows + kFinalRows - 1) / kFinalRows), dim3(256),
-                       sizeof(float) * kFinalRows * C, s, x, emb, table, Wt, bias, out, B, S, C, Cl, eps);
+    hipLaunchKernelGGL(final_norm_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, emb, table, y, B, S, C, eps);
+    if (C % 128 == 0)
+        hipLaunchKernelGGL(proj_out_kernel, dim3((rows + 31) / 32), dim3(256), 0, s, y, Wt, bias, out, B, S, C, Cl);
+    else
+        hipLaunchKernelGGL(proj_out_scalar_kernel, dim3((rows * Cl + 255) / 256), dim3(256), 0, s, y, Wt, bias, out, B,
+                           S, C, Cl);
     return hipGetLastError();
 }
 

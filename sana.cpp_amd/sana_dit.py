@@ -49,6 +49,10 @@ PROTOTYPES = {
     "sana_dit_forward_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp, _vp]),
     "sana_dit_step_device": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp, _vp]),
     "sana_dit_block_forward": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "sana_dit_run_blocks": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp]),
+    "sana_dit_denoise_loop": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, ctypes.c_float, _vp]),
+    "sana_dit_denoise_loop_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, ctypes.c_float, _vp,
+                                                    _vp]),
     "sana_dit_time_embed": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "sana_dit_time_gemm": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _fp, ctypes.POINTER(ctypes.c_double)]),
     "sana_gguf_num_tensors": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_i64)]),
@@ -186,6 +190,29 @@ class Dit:
         outs = [np.empty_like(x) for _ in range(3)]
         check(lib().sana_dit_block_forward(self.h, block, ptr(x), ptr(t_mod), B, N, *[ptr(o) for o in outs]))
         return outs
+
+    def run_blocks(self, begin, end, x, t_mod):
+        x = _f32(x)
+        t_mod = _f32(t_mod)
+        B, N, C = x.shape
+        out = np.empty_like(x)
+        check(lib().sana_dit_run_blocks(self.h, begin, end, ptr(x), ptr(t_mod), B, N, ptr(out)))
+        return out
+
+    def denoise_loop(self, latent, timesteps, sigmas, guidance):
+        latent = _f32(latent)
+        ts, sg = _f32(timesteps), _f32(sigmas)
+        Bl, Cl, H, W = latent.shape
+        out = np.empty_like(latent)
+        check(lib().sana_dit_denoise_loop(self.h, ptr(latent), Bl, H, W, ptr(ts), ptr(sg), ts.size, float(guidance),
+                                          ptr(out)))
+        return out
+
+    def denoise_loop_device(self, d_latent, shape, timesteps, sigmas, guidance, d_out, stream=None):
+        ts, sg = _f32(timesteps), _f32(sigmas)
+        Bl, Cl, H, W = shape
+        check(lib().sana_dit_denoise_loop_device(self.h, ptr(d_latent), Bl, H, W, ptr(ts), ptr(sg), ts.size,
+                                                 float(guidance), ptr(d_out), stream))
 
     def time_embed(self, t):
         t = _f32(np.atleast_1d(t))

@@ -1,0 +1,144 @@
+"""Full-model parity of the HIP path against the reference's own CPU outputs.
+
+The golden fixtures (tests/golden/*.npz) hold the outputs of the reference's
+src/*.cpp compiled from source (tests/golden/make_golden.py) on the seeded
+synthetic Sana-0.6B model of oracle/model_spec.h; the oracle regenerates the
+identical weights bit for bit (tests/test_oracle_golden.py pins that), and
+they are uploaded here through the C ABI.
+
+Tolerances (relative L2): 2e-3 per forward, 1e-2 on the final latent of the
+20-step DPM-Solver++ loop.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL_FORWARD = 2e-3
+TOL_LOOP = 1e-2
+
+
+def golden(name):
+    return np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False)
+
+
+@pytest.fixture(scope="module")
+def full_model():
+    import sana_dit
+    print("generating the seeded 28-block weights on the host ...", flush=True)
+    m = O.Model(layers=28, self_heads=36, cross_heads=16)
+    d = sana_dit.Dit(layers=28, self_heads=36, cross_heads=16)
+    for name, shape in sana_dit.manifest(28).items():
+        d.set_weight(name, m.get(name, shape))
+    d.check_weights()
+    yield m, d
+    d.close()
+
+
+@pytest.mark.parametrize("case,masked", [("cfg2", False), ("cfg2_mask", True)])
+def test_forward_1024px_vs_reference(full_model, case, masked):
+    m, d = full_model
+    fx = golden(case)
+    latent = O.randn((1, 32, 32, 32), 42)
+    caption = O.randn((2, 300, 2304), 43)
+    bias = O.mask_bias(300, 1, 40) if masked else None
+    d.set_context(caption, projected=False, bias=bias)
+    ctx = d.get_context((2, 300, 1152))
+    stride = int(fx["context__stride"])
+    ctx_err = rel_l2(ctx.reshape(-1)[::stride], fx["context__sub"])
+    got = d.forward(latent, 999.0)
+    err = rel_l2(got, fx["noise_pred"])
+    guided = got[:1] + np.float32(4.5) * (got[1:] - got[:1])
+    gerr = rel_l2(guided, fx["guided"])
+    print(f"{case}: context rel_l2 {ctx_err:.2e}, noise_pred rel_l2 {err:.2e}, guided rel_l2 {gerr:.2e}")
+    assert ctx_err < 1e-3
+    assert err < TOL_FORWARD
+    assert gerr < TOL_FORWARD
+
+
+def test_forward_deterministic(full_model):
+    m, d = full_model
+    latent = O.randn((1, 32, 32, 32), 42)
+    caption = O.randn((2, 300, 2304), 43)
+    d.set_context(caption, projected=False)
+    a = d.forward(latent, 999.0)
+    b = d.forward(latent, 999.0)
+    assert np.array_equal(a, b)
+
+
+def test_denoise_loop_1024px_vs_reference(full_model):
+    path = os.path.join(GOLDEN, "cfg3.npz")
+    if not os.path.exists(path):
+        pytest.skip("cfg3 golden not generated")
+    m, d = full_model
+    fx = golden("cfg3")
+    latent = O.randn((1, 32, 32, 32), 42)
+    caption = O.randn((2, 300, 2304), 43)
+    d.set_context(caption, projected=False)
+    ts, sg = O.scheduler_timesteps(20)
+    fin = d.denoise_loop(latent, ts, sg, 4.5)
+    err = rel_l2(fin, fx["final_latent"])
+    print(f"cfg3: final latent rel_l2 {err:.2e}")
+    assert err < TOL_LOOP
+
+
+SMALL = dict(layers=2, hidden=128, ffn=256, caption=96, latent=8, self_heads=4, cross_heads=2)
+
+
+@pytest.fixture(scope="module")
+def small_model():
+    import sana_dit
+    m = O.Model(**SMALL)
+    d = sana_dit.Dit(layers=2, hidden=128, ffn=256, caption_dim=96, latent_channels=8, self_heads=4, cross_heads=2)
+    for name, shape in sana_dit.manifest(2, 128, 256, 96, 8).items():
+        d.set_weight(name, m.get(name, shape))
+    d.check_weights()
+    yield m, d
+    d.close()
+
+
+def test_small_loop_vs_oracle(small_model):
+    m, d = small_model
+    latent = O.randn((1, 8, 8, 8), 42)
+    caption = O.randn((2, 16, 96), 43)
+    ref = m.loop(latent, caption, 6, 4.5)
+    d.set_context(caption, projected=False)
+    ts, sg = O.scheduler_timesteps(6)
+    got = d.denoise_loop(latent, ts, sg, 4.5)
+    err = rel_l2(got, ref)
+    print(f"small loop rel_l2 {err:.2e}")
+    assert err < TOL_LOOP
+
+
+def test_small_run_blocks_vs_oracle(small_model):
+    m, d = small_model
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((2, 64, 128)).astype(np.float32)
+    ctx = rng.standard_normal((2, 16, 128)).astype(np.float32)
+    emb, tmod = m.time(np.array([500.0, 500.0], np.float32))
+    ref = x
+    for i in range(2):
+        ref = m.block(i, ref, ctx, tmod)[2]
+    d.set_context(ctx, projected=True)
+    got = d.run_blocks(0, 2, x, tmod)
+    assert rel_l2(got, ref) < TOL_FORWARD
+
+
+def test_small_forward_masked_vs_oracle(small_model):
+    m, d = small_model
+    latent = O.randn((1, 8, 8, 8), 5)
+    caption = O.randn((2, 16, 96), 6)
+    bias = np.full((2, 16), -10000.0, np.float32)
+    bias[0, :3] = 0.0
+    bias[1, :11] = 0.0
+    ctx = m.project_caption(caption)
+    ref = m.forward(latent, ctx, 733.0, bias)
+    d.set_context(caption, projected=False, bias=bias)
+    got = d.forward(latent, 733.0)
+    assert rel_l2(got, ref) < TOL_FORWARD
