@@ -129,6 +129,11 @@ int sana_dit_denoise_loop(sana_dit * ctx, const float * latent, int64_t Bl, int6
 int sana_dit_denoise_loop_device(sana_dit * ctx, const float * d_latent, int64_t Bl, int64_t H, int64_t W,
                                  const float * timesteps, const float * sigmas, int64_t steps, float guidance,
                                  float * d_final_latent, void * stream);
+/* The converted model outputs (x0 = sample - sigma * guided prediction) of the
+ * last two steps of the last denoise loop on this context, [Bl, Cl, H, W]
+ * each: the previous_model_outputs a host scheduler state holds after the loop
+ * (src/scheduler.cpp:286-290).  x0_prev is left untouched after a one-step loop. */
+int sana_dit_loop_model_outputs(sana_dit * ctx, float * x0_prev, float * x0_last);
 /* Time MLP of the forward (src/transformer.cpp:638-656): B timesteps ->
  * embedded [B, C] (pre-SiLU) and t_mod [B, 6C]. */
 int sana_dit_time_embed(sana_dit * ctx, const float * t, int64_t B, float * embedded, float * t_mod);

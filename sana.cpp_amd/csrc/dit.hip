@@ -160,6 +160,7 @@ struct sana_dit {
              GraphEntry>
         graphs;
     int64_t last_M = 0, last_B = 0, last_N = 0;
+    int64_t loop_steps = 0, loop_n = 0;  // shape of the last denoise loop (its converted outputs stay in loop_x0)
 
     ~sana_dit() {
         for (auto & kv : graphs)
@@ -978,6 +979,8 @@ float * enqueue_loop(sana_dit * c, const float * d_latent, int64_t Bl, int64_t H
                            guidance, s0_v, ca, cb, cc, inv_r0, first ? 0 : 1);
         hip_check(hipGetLastError(), "cfg_dpm");
     }
+    c->loop_steps = steps;
+    c->loop_n = n;
     return c->loop_lat[steps & 1].as<float>();
 }
 
@@ -1024,6 +1027,21 @@ int sana_dit_denoise_loop(sana_dit * c, const float * latent, int64_t Bl, int64_
         float * res = enqueue_loop(c, c->lat_in.as<float>(), Bl, Hh, Ww, timesteps, sigmas, steps, guidance, c->stream);
         hip_check(hipMemcpyAsync(final_latent, res, (size_t)n * 4, hipMemcpyDeviceToHost, c->stream), "final");
         hip_check(hipStreamSynchronize(c->stream), "denoise_loop");
+    });
+}
+
+int sana_dit_loop_model_outputs(sana_dit * c, float * x0_prev, float * x0_last) {
+    if (!c || !x0_last) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    if (c->loop_steps <= 0) return set_err(SANA_ERR_STATE, "no denoise loop has run");
+    return guarded([&] {
+        const int64_t st = c->loop_steps;
+        const size_t bytes = (size_t)c->loop_n * 4;
+        // step i writes its converted output to loop_x0[(i + 1) & 1]
+        hip_check(hipMemcpyAsync(x0_last, c->loop_x0[st & 1].p, bytes, hipMemcpyDeviceToHost, c->stream), "x0");
+        if (x0_prev && st >= 2)
+            hip_check(hipMemcpyAsync(x0_prev, c->loop_x0[(st - 1) & 1].p, bytes, hipMemcpyDeviceToHost, c->stream),
+                      "x0");
+        hip_check(hipStreamSynchronize(c->stream), "loop_model_outputs");
     });
 }
 

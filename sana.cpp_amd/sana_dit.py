@@ -53,6 +53,7 @@ PROTOTYPES = {
     "sana_dit_denoise_loop": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, ctypes.c_float, _vp]),
     "sana_dit_denoise_loop_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, ctypes.c_float, _vp,
                                                     _vp]),
+    "sana_dit_loop_model_outputs": (ctypes.c_int, [_vp, _vp, _vp]),
     "sana_dit_time_embed": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "sana_dit_time_gemm": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _fp, ctypes.POINTER(ctypes.c_double)]),
     "sana_gguf_num_tensors": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_i64)]),

@@ -33,7 +33,13 @@ def test_binding_covers_every_declared_symbol():
 
 
 def test_last_error_is_empty_string_initially():
-    assert sana_dit.lib().sana_dit_last_error() in (b"",)
+    # a fresh process: other tests in this one may have left a message
+    import subprocess
+    import sys
+    code = ("import ctypes, sys; sys.path.insert(0, %r); import sana_dit; "
+            "print(repr(sana_dit.lib().sana_dit_last_error()))" % os.path.join(ROOT, "sana.cpp_amd"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, check=True).stdout
+    assert out.strip() == "b''"
 
 
 def test_create_rejects_bad_config_without_gpu():
