@@ -1036,11 +1036,11 @@ int sana_dit_loop_model_outputs(sana_dit * c, float * x0_prev, float * x0_last) 
     return guarded([&] {
         const int64_t st = c->loop_steps;
         const size_t bytes = (size_t)c->loop_n * 4;
-        // step i writes its converted output to loop_x0[(i + 1) & 1]
-        hip_check(hipMemcpyAsync(x0_last, c->loop_x0[st & 1].p, bytes, hipMemcpyDeviceToHost, c->stream), "x0");
+        // step i writes its converted output to loop_x0[i & 1] (cfg_dpm_kernel's x0_out)
+        hip_check(hipMemcpyAsync(x0_last, c->loop_x0[(st - 1) & 1].p, bytes, hipMemcpyDeviceToHost, c->stream),
+                  "x0");
         if (x0_prev && st >= 2)
-            hip_check(hipMemcpyAsync(x0_prev, c->loop_x0[(st - 1) & 1].p, bytes, hipMemcpyDeviceToHost, c->stream),
-                      "x0");
+            hip_check(hipMemcpyAsync(x0_prev, c->loop_x0[st & 1].p, bytes, hipMemcpyDeviceToHost, c->stream), "x0");
         hip_check(hipStreamSynchronize(c->stream), "loop_model_outputs");
     });
 }

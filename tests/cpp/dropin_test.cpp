@@ -444,8 +444,9 @@ void gpu_small_model_tests() {
             run_full_denoising_step_with_cfg(latent, ctx, 4.5f, done, cfg, w);
         },
         "step past the schedule");
-    throws<std::invalid_argument>([&] { run_full_denoising_step_with_cfg(latent, x, 4.5f, st, cfg, w); },
-                                  "context batch != 2 x latent batch");
+    throws<std::invalid_argument>(
+        [&] { run_full_denoising_step_with_cfg(latent, Tensor({3, L, C}), 4.5f, st, cfg, w); },
+        "context batch != 2 x latent batch");
 
     // whole loop: the fused device loop and the per-step path, against the oracle loop
     std::vector<float> ref(latent.numel());
@@ -462,9 +463,9 @@ void gpu_small_model_tests() {
               s_fused.previous_model_outputs.size() == 2,
           "scheduler state after the device loop");
     if (s_fused.previous_model_outputs.size() == 2 && s_steps.previous_model_outputs.size() == 2) {
-        close_l2(s_fused.previous_model_outputs[0].data(), s_steps.previous_model_outputs[0].data(), 1e-2,
+        close_l2(s_fused.previous_model_outputs[0].data(), s_steps.previous_model_outputs[0].data(), 2e-3,
                  "loop model output n-2");
-        close_l2(s_fused.previous_model_outputs[1].data(), s_steps.previous_model_outputs[1].data(), 1e-2,
+        close_l2(s_fused.previous_model_outputs[1].data(), s_steps.previous_model_outputs[1].data(), 2e-3,
                  "loop model output n-1");
     }
     // a loop resumed mid-schedule takes the per-step path
