@@ -15,15 +15,23 @@ the context kept resident (sana_dit_forward_device) is reported beside it.
 Prints ONE JSON line (rank 0, N = 1 only):
   value / ms_per_step      ms per step (lower is better)
   roofline                 the dominant kernel (Mix-FFN inverted 1x1 GEMM,
-                           2048 x 5760 x 1152) timed with HIP events on its
-                           own stream, against the dense fp16 MFMA peak
+                           2048 x 5760 x 1152) timed with HIP events on the
+                           stream it is launched on, against the dense fp16
+                           MFMA peak; `traffic` is its HBM bytes per launch
+                           from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+                           summarised in profiles/ (null when absent)
   cpu_baseline             the reference's own CPU block_forward (compiled
                            from source into oracle/_ref, 1 thread) on one
-                           block of the same workload, x28
+                           block of the same workload, median of 6, x28
+
+--pmc-calib adds, before the timed region, three launches of a plain copy
+kernel over 256 MiB (torch.neg: 256 MiB read + 256 MiB written), the known
+size the HBM counters are scaled by.
 """
 import argparse
 import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -34,6 +42,11 @@ sys.path.insert(0, os.path.join(ROOT, "sana.cpp_amd"))
 
 PEAK_MFMA_TFLOPS = 2516.6   # MI355X dense fp16/bf16
 PEAK_HBM_GBS = 8000.0
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_inverted_gemm_1024px_hbm_traffic.md")
+CPU_REPS = 6
+# operands and output of the Mix-FFN inverted GEMM, fp16: A 2048x1152, W 5760x1152, out 2048x5760, bias fp32
+GEMM_BYTES = 2 * (2048 * 1152 + 5760 * 1152 + 2048 * 5760) + 4 * 5760
 
 DIMS = dict(layers=28, hidden=1152, ffn=5760, caption_dim=2304, latent_channels=32, self_heads=36, cross_heads=16)
 SIDE = 32          # 1024 px / 32 (DC-AE f32 latent)
@@ -66,7 +79,8 @@ def cpu_baseline():
     exe = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
     B = 2
     if os.path.exists(exe):
-        cmd = [exe, "time-block", str(DIMS["self_heads"]), str(DIMS["cross_heads"]), str(B), str(SIDE), "1"]
+        cmd = [exe, "time-block", str(DIMS["self_heads"]), str(DIMS["cross_heads"]), str(B), str(SIDE),
+               str(CPU_REPS)]
         if shutil.which("taskset"):
             cmd = ["taskset", "-c", "0"] + cmd
         t0 = time.time()
@@ -94,10 +108,21 @@ def cpu_baseline():
     ms = block_ms * DIMS["layers"]
     return {"value": round(ms, 1), "unit": "ms/step", "cores": 1, "kind": kind,
             "sample": (f"one DiT block (block_forward: self linear attention, cross attention incl. its K/V "
-                       f"projections, Mix-FFN) at B=2, N=1024, L=300, 36x32/16x72 heads, 1 rep on 1 thread "
-                       f"({block_ms:.0f} ms), x28 blocks; patch/time/final layers (<0.1% of FLOPs) untimed; "
-                       f"{wall:.1f} s wall"),
+                       f"projections, Mix-FFN) at B=2, N=1024, L=300, 36x32/16x72 heads, median of "
+                       f"{CPU_REPS if kind == 'reference' else 1} reps on 1 thread ({block_ms:.0f} ms), x28 blocks; "
+                       f"patch/time/final layers (<0.1% of FLOPs) untimed; {wall:.1f} s wall"),
             "host_nproc": os.cpu_count()}
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (None when it is absent)."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9]+)", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def main():
@@ -106,6 +131,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-calib", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for {args.gpus}); "
@@ -143,6 +169,15 @@ def main():
 
     def fwd():
         d.forward_device(latent, shape, TIMESTEP, out, sp)
+
+    if args.pmc_calib:
+        src = torch.ones(64 << 20, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     torch.cuda.synchronize()
     for _ in range(args.warmup):
@@ -204,10 +239,11 @@ def main():
         "step_gflop": round(step_flops / 1e9, 2),
         "forward_gflop_context_resident": round(fwd_flops / 1e9, 2),
         "gemms": per_gemm,
-        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<256,128,store> Mix-FFN inverted 2048x5760x1152 +bias+SiLU",
+        "roofline": {"bound": "mfma",
+                     "kernel": "gemm_kernel (128x128 tile, bias+SiLU epilogue): Mix-FFN inverted 2048x5760x1152",
                      "achieved": round(gemm_tflops, 1), "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tflops / PEAK_MFMA_TFLOPS, 4), "traffic": None,
-                     "avg_us": round(gemm_ms * 1e3, 2)},
+                     "frac": round(gemm_tflops / PEAK_MFMA_TFLOPS, 4), "traffic": measured_traffic(),
+                     "algorithmic_bytes": GEMM_BYTES, "avg_us": round(gemm_ms * 1e3, 2)},
         "cpu_baseline": cpu,
     }
     d.close()

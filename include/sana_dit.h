@@ -137,9 +137,11 @@ int sana_dit_loop_model_outputs(sana_dit * ctx, float * x0_prev, float * x0_last
 /* Time MLP of the forward (src/transformer.cpp:638-656): B timesteps ->
  * embedded [B, C] (pre-SiLU) and t_mod [B, 6C]. */
 int sana_dit_time_embed(sana_dit * ctx, const float * t, int64_t B, float * embedded, float * t_mod);
-/* Average duration (ms) over `iters` eager launches of one GEMM of block 0 at
- * the token count of the last forward: which = 0 QKV, 1 attn out, 2 cross q,
- * 3 cross out, 4 FFN inverted, 5 FFN point.  Also returns its FLOPs. */
+/* Average duration (ms) over `iters` eager launches of one GEMM of the blocks
+ * at the token count of the last forward (launch i uses block i mod layers, so
+ * weights stream from HBM as in the forward): which = 0 QKV, 1 attn out,
+ * 2 cross q, 3 cross out, 4 FFN inverted, 5 FFN point.  Also returns its
+ * FLOPs.  Overwrites the forward's activation buffers. */
 int sana_dit_time_gemm(sana_dit * ctx, int which, int iters, float * avg_ms, double * flops);
 
 /* GGUF index inspection (no GPU needed): number of tensors, and the name,
@@ -172,6 +174,44 @@ int sana_hip_cross_attention(const void * q, int64_t ldq, const void * k, int64_
                              int64_t L, int64_t H, int64_t D, void * stream);
 int sana_hip_dwconv_glu(const void * x, int64_t ldx, const float * w_tapmajor, const float * bias, void * out,
                         int64_t ldo, int64_t B, int64_t H, int64_t W, int64_t F, void * stream);
+
+/* ---- fp32 op launchers on device pointers: the op-level API of the drop-in
+ * (src/common_ops.h:5-49, src/transformer_ops.h:5-50).  fp32 in, fp32 out, in
+ * the reference's layouts; asynchronous on `stream`. ---- */
+#define SANA_OP_SILU 0
+#define SANA_OP_GELU_TANH 1
+#define SANA_OP_RELU 2
+/* C[z] (+)= A[z] . op(B[z]) + bias for z < batch (gemm_row_major,
+ * src/common_ops.cpp:13-65, and its batched uses).  A [M, K] (lda), B [K, N]
+ * (ldb) or, with b_transposed, [N, K]; bias_mode 1: bias[N] per column,
+ * 2: bias[M] per row; accumulate = 1 adds into C (gemm_accumulate_row_major). */
+int sana_op_gemm_f32(const float * A, int64_t lda, int64_t strideA, const float * B, int64_t ldb, int64_t strideB,
+                     int b_transposed, const float * bias, int bias_mode, float * C, int64_t ldc, int64_t strideC,
+                     int64_t M, int64_t N, int64_t K, int64_t batch, int accumulate, void * stream);
+/* y = op(x) elementwise: SANA_OP_SILU, SANA_OP_GELU_TANH, SANA_OP_RELU. */
+int sana_op_unary_f32(const float * x, float * y, int64_t n, int op, void * stream);
+/* Row softmax of x * scale (+ bias[(row / bias_div) * cols + col]) (softmax_lastdim_4d
+ * and attention_4d, src/transformer_ops.cpp:280-392). */
+int sana_op_softmax_f32(const float * x, float * y, int64_t rows, int64_t cols, float scale, const float * bias,
+                        int64_t bias_div, void * stream);
+/* RMSNorm over rows (rms_norm_3d_lastdim, src/tensor.cpp:276-316); w may be NULL. */
+int sana_op_rms_norm_f32(const float * x, const float * w, float * y, int64_t rows, int64_t cols, float eps,
+                         void * stream);
+/* Depthwise ksize x ksize (3 or 5) convolution, zero padding, NCHW
+ * (depthwise_conv2d_3x3 / _5x5, src/common_ops.cpp:483-572, :576-718); bias may be NULL. */
+int sana_op_dwconv_f32(const float * x, const float * w, const float * bias, float * y, int64_t B, int64_t C,
+                       int64_t H, int64_t W, int64_t ksize, void * stream);
+/* GLU of the split channels of x [B, 2F, S]: y = data * silu(gate) (glumb_conv,
+ * src/common_ops.cpp:744-756). */
+int sana_op_glu_f32(const float * x, float * y, int64_t B, int64_t F, int64_t S, void * stream);
+/* linear_attention_4d (src/transformer_ops.cpp:402-543) on [BH, N, D] q / k / v;
+ * state is a workspace of BH * (D + 1) * D floats. */
+int sana_op_linear_attention_f32(const float * q, const float * k, const float * v, float * out, int64_t BH,
+                                 int64_t Nq, int64_t Nk, int64_t D, float * state, void * stream);
+/* split = 1: [B, N, H*D] -> [B, H, N, D] (split_heads_3d); split = 0: the
+ * inverse (merge_heads_4d), src/transformer_ops.cpp:83-171. */
+int sana_op_heads_f32(const float * x, float * y, int64_t B, int64_t N, int64_t H, int64_t D, int split,
+                      void * stream);
 
 #ifdef __cplusplus
 }

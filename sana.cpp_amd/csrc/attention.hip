@@ -369,8 +369,17 @@ __global__ __launch_bounds__(256) void xattn_kernel(const f16 * __restrict__ q, 
 // fp16 then feeds O^T = V^T . P^T directly from registers as the B operand; the
 // key order inside each 16-key MFMA step is permuted identically in both
 // operands (lane half h supplies keys 4h..4h+3 and 8+4h..8+4h+3), which leaves
-// the sum over keys unchanged.  Keys >= L get probability exactly 0.
+// the sum over keys unchanged.
+//
+// With 1024 queries per (b, h) there are only four waves per CU, so the
+// kernel is latency-bound and written for instruction-level parallelism: the
+// query fragments and all staging loads are issued before the first wait,
+// key masking is branch-free (keys >= L carry a -inf bias in LDS, so their
+// probability is exactly 0), the exponent is one v_exp_f32 on log2-scaled
+// scores, and the P.V product keeps one accumulator per 32-dim tile so the
+// MFMA chains are independent.
 constexpr int kXaQ = 128;  // queries per workgroup
+constexpr float kLog2e = 1.4426950408889634f;
 template <int LT>
 __global__ __launch_bounds__(256) void xattn_fast_kernel(const f16 * __restrict__ q, int64_t ldq,
                                                          const f16 * __restrict__ k, int64_t ldk,
@@ -380,78 +389,98 @@ __global__ __launch_bounds__(256) void xattn_fast_kernel(const f16 * __restrict_
     constexpr int LP = LT * 32;
     constexpr int KROW = 96 + 8;    // halves per K row (d padded, 208 B rows)
     constexpr int VROW = LP + 8;    // halves per V^T row
+    constexpr int KCH = KROW / 8;   // 16-byte chunks per staged K row
+    constexpr int VCH = VROW / 8;
+    constexpr int KN = (LP * KCH + 255) / 256;  // K chunks per thread
+    constexpr int VN = (96 * VCH + 255) / 256;  // V^T chunks per thread
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     f16 * Ks = reinterpret_cast<f16 *>(smem);                       // [LP][KROW]
     f16 * Vs = Ks + LP * KROW;                                       // [96][VROW]
-    float * bs = reinterpret_cast<float *>(Vs + 96 * VROW);          // [LP]
+    float * bs = reinterpret_cast<float *>(Vs + 96 * VROW);          // [LP], log2-scaled bias, -inf past L
     const int h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int KS = (D + 15) / 16;   // 16-deep steps over head dims
-    const int DT = (D + 31) / 32;   // 32-wide output dim tiles
-    // stage K rows (zero past D and past L), V^T rows (zero past D; keys past L are zero in vt), bias
-    const f16 * kb = k + (int64_t)b * L * ldk + (int64_t)h * D;
-    for (int idx = tid; idx < LP * (KROW / 8); idx += 256) {
-        const int key = idx / (KROW / 8), c8 = (idx - key * (KROW / 8)) * 8;
-        f16x8 v8;
-        if (key < L && c8 < D) {
-            v8 = *reinterpret_cast<const f16x8 *>(kb + (int64_t)key * ldk + c8);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v8[e] = (f16)0.0f;
-        }
-        *reinterpret_cast<f16x8 *>(Ks + key * KROW + c8) = v8;
-    }
-    const f16 * vb = vt + ((int64_t)b * H * D + (int64_t)h * D) * ldvt;
-    for (int idx = tid; idx < 96 * (VROW / 8); idx += 256) {
-        const int dim = idx / (VROW / 8), c8 = (idx - dim * (VROW / 8)) * 8;
-        f16x8 v8;
-        if (dim < D && c8 < LP) {
-            v8 = *reinterpret_cast<const f16x8 *>(vb + (int64_t)dim * ldvt + c8);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v8[e] = (f16)0.0f;
-        }
-        *reinterpret_cast<f16x8 *>(Vs + dim * VROW + c8) = v8;
-    }
-    for (int key = tid; key < LP; key += 256) bs[key] = (key < L && bias) ? bias[(int64_t)b * L + key] : 0.0f;
-    __syncthreads();
-
-    const int q0 = blockIdx.x * kXaQ + w * 32;
-    if (q0 >= N) return;
     const int hh = lane >> 5;
+    const int KS = (D + 15) / 16;   // 16-deep steps over head dims (<= 6)
+    const int DT = (D + 31) / 32;   // 32-wide output dim tiles (<= 3)
+    const int q0 = blockIdx.x * kXaQ + w * 32;
+
+    // query fragments of this lane's column (issued first; independent of LDS)
     const int qcol = min(q0 + (lane & 31), N - 1);
     const f16 * qr = q + ((int64_t)b * N + qcol) * ldq + (int64_t)h * D;
+    f16x8 qf[6];
+#pragma unroll
+    for (int ks = 0; ks < 6; ++ks) {
+        const int d0 = ks * 16 + 8 * hh;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[ks][e] = (f16)0.0f;
+        if (ks < KS && d0 + 8 <= D) qf[ks] = *reinterpret_cast<const f16x8 *>(qr + d0);
+    }
 
-    // S^T[key][q]: tile t holds keys 32t + 8*(i/4) + 4*hh + i%4 for the lane's query.
+    // stage K rows (zero past D and past L) and V^T rows (zero past D; keys
+    // past L are zero in vt): all loads in flight before the LDS stores
+    const f16 * kb = k + (int64_t)b * L * ldk + (int64_t)h * D;
+    const f16 * vb = vt + ((int64_t)b * H * D + (int64_t)h * D) * ldvt;
+    f16x8 kreg[KN], vreg[VN];
+#pragma unroll
+    for (int j = 0; j < KN; ++j) {
+        const int idx = tid + 256 * j;
+        const int key = idx / KCH, c8 = (idx - key * KCH) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kreg[j][e] = (f16)0.0f;
+        if (idx < LP * KCH && key < L && c8 < D) kreg[j] = *reinterpret_cast<const f16x8 *>(kb + (int64_t)key * ldk + c8);
+    }
+#pragma unroll
+    for (int j = 0; j < VN; ++j) {
+        const int idx = tid + 256 * j;
+        const int dim = idx / VCH, c8 = (idx - dim * VCH) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vreg[j][e] = (f16)0.0f;
+        if (idx < 96 * VCH && dim < D && c8 < LP) vreg[j] = *reinterpret_cast<const f16x8 *>(vb + (int64_t)dim * ldvt + c8);
+    }
+    for (int key = tid; key < LP; key += 256)
+        bs[key] = key < L ? (bias ? bias[(int64_t)b * L + key] * kLog2e : 0.0f) : -INFINITY;
+#pragma unroll
+    for (int j = 0; j < KN; ++j) {
+        const int idx = tid + 256 * j;
+        if (idx < LP * KCH) *reinterpret_cast<f16x8 *>(Ks + idx * 8) = kreg[j];
+    }
+#pragma unroll
+    for (int j = 0; j < VN; ++j) {
+        const int idx = tid + 256 * j;
+        if (idx < 96 * VCH) *reinterpret_cast<f16x8 *>(Vs + idx * 8) = vreg[j];
+    }
+    __syncthreads();
+    if (q0 >= N) return;
+
+    // S^T[key][q] (log2-scaled): tile t holds keys 32t + 8*(i/4) + 4*hh + i%4 for the lane's query.
     f32x16 st[LT];
 #pragma unroll
     for (int t = 0; t < LT; ++t)
 #pragma unroll
         for (int i = 0; i < 16; ++i) st[t][i] = 0.0f;
-    for (int ks = 0; ks < KS; ++ks) {
-        const int d0 = ks * 16 + 8 * hh;
-        f16x8 qf;
-        if (d0 + 8 <= D) {
-            qf = *reinterpret_cast<const f16x8 *>(qr + d0);
-        } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qf[e] = (f16)0.0f;
-        }
+    for (int ks = 0; ks < 6; ++ks) {
+        if (ks >= KS) break;
+        const int d0 = ks * 16 + 8 * hh;
 #pragma unroll
         for (int t = 0; t < LT; ++t) {
             const f16x8 kf = *reinterpret_cast<const f16x8 *>(Ks + (t * 32 + (lane & 31)) * KROW + d0);
-            st[t] = mfma_32x32x16(kf, qf, st[t]);
+            st[t] = mfma_32x32x16(kf, qf[ks], st[t]);
         }
     }
+    const float scale2 = scale * kLog2e;
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < LT; ++t)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int key = t * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-            const float sv = key < L ? st[t][i] * scale + bs[key] : -INFINITY;
-            st[t][i] = sv;
-            mx = fmaxf(mx, sv);
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bs + t * 32 + 8 * i4 + 4 * hh);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float sv = st[t][4 * i4 + u] * scale2 + b4[u];
+                st[t][4 * i4 + u] = sv;
+                mx = fmaxf(mx, sv);
+            }
         }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     float sum = 0.0f;
@@ -460,25 +489,29 @@ __global__ __launch_bounds__(256) void xattn_fast_kernel(const f16 * __restrict_
     for (int t = 0; t < LT; ++t)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int key = t * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-            const float e = key < L ? expf(st[t][i] - mx) : 0.0f;
+            const float e = __builtin_amdgcn_exp2f(st[t][i] - mx);
             sum += e;
             pf[t][i >> 3][i & 7] = (f16)e;
         }
     sum += __shfl_xor(sum, 32, 64);
     const float rs = 1.0f / sum;
 
-    // O^T[dim][q] = V^T . P^T; A lane (dim, hh) supplies keys 16s + 4hh + {0..3} and 16s + 8 + 4hh + {0..3}.
-    for (int dt = 0; dt < DT; ++dt) {
-        f32x16 o;
+    // O^T[dim][q] = V^T . P^T, one accumulator per 32-dim tile; A lane (dim, hh)
+    // supplies keys 16s + 4hh + {0..3} and 16s + 8 + 4hh + {0..3}.
+    f32x16 o[3];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[i] = 0.0f;
-        const f16 * vrow = Vs + (dt * 32 + (lane & 31)) * VROW;
+    for (int dt = 0; dt < 3; ++dt)
 #pragma unroll
-        for (int t = 0; t < LT; ++t)
+        for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                const int kbase = t * 32 + 16 * s2 + 4 * hh;
+    for (int t = 0; t < LT; ++t)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int kbase = t * 32 + 16 * s2 + 4 * hh;
+#pragma unroll
+            for (int dt = 0; dt < 3; ++dt) {
+                if (dt >= DT) break;
+                const f16 * vrow = Vs + (dt * 32 + (lane & 31)) * VROW;
                 const f16x4 lo4 = *reinterpret_cast<const f16x4 *>(vrow + kbase);
                 const f16x4 hi4 = *reinterpret_cast<const f16x4 *>(vrow + kbase + 8);
                 f16x8 af;
@@ -487,16 +520,26 @@ __global__ __launch_bounds__(256) void xattn_fast_kernel(const f16 * __restrict_
                     af[e] = lo4[e];
                     af[4 + e] = hi4[e];
                 }
-                o = mfma_32x32x16(af, pf[t][s2], o);
+                o[dt] = mfma_32x32x16(af, pf[t][s2], o[dt]);
             }
-        // lane holds query column (lane & 31), dims dt*32 + 8*(i/4) + 4*hh + i%4
-        const int qq = q0 + (lane & 31);
-        if (qq < N) {
-            f16 * orow = out + ((int64_t)b * N + qq) * ldo + (int64_t)h * D;
+        }
+    // lane holds query column (lane & 31), dims dt*32 + 8*(i/4) + 4*hh + i%4:
+    // four consecutive dims per 8-byte store (D % 8 == 0, rows 16-byte aligned)
+    const int qq = q0 + (lane & 31);
+    if (qq < N) {
+        f16 * orow = out + ((int64_t)b * N + qq) * ldo + (int64_t)h * D;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int dim = dt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-                if (dim < D) orow[dim] = (f16)(o[i] * rs);
+        for (int dt = 0; dt < 3; ++dt) {
+            if (dt >= DT) break;
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const int dim = dt * 32 + 8 * i4 + 4 * hh;
+                if (dim < D) {
+                    f16x4 v4;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) v4[u] = (f16)(o[dt][4 * i4 + u] * rs);
+                    *reinterpret_cast<f16x4 *>(orow + dim) = v4;
+                }
             }
         }
     }
@@ -606,7 +649,8 @@ hipError_t cross_attention(const half_t * q, int64_t ldq, const half_t * k, int6
     f16 * oo = reinterpret_cast<f16 *>(out);
     // fast path: LDS-staged head, transposed scores (ldvt >= the 32-padded key count)
     const int lt32 = (L + 31) / 32;
-    if (vec && D <= 96 && lt32 <= 10 && ldvt >= (int64_t)lt32 * 32) {
+    const bool out_vec = ldo % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;  // 8-byte output stores
+    if (vec && out_vec && D <= 96 && lt32 <= 10 && ldvt >= (int64_t)lt32 * 32) {
         if (lt32 <= 2) return launch_xattn_fast<2>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
         if (lt32 <= 4) return launch_xattn_fast<4>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
         return launch_xattn_fast<10>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);

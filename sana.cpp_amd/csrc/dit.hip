@@ -1068,10 +1068,12 @@ int sana_dit_time_gemm(sana_dit * c, int which, int iters, float * avg_ms, doubl
     if (c->last_M <= 0) return set_err(SANA_ERR_STATE, "run a forward first");
     if (which < 0 || which > 5) return set_err(SANA_ERR_INVALID_ARGUMENT, "which must be 0..5");
     return guarded([&] {
-        BlockDev & w = *c->blocks[0];
         const int64_t M = c->last_M, C = c->C, N = c->last_N;
         // Scratch outputs: the dedicated buffers of each GEMM in the forward.
-        auto run = [&]() {
+        // Launch i uses block i's weights, cycling as the forward does, so the
+        // weights stream from HBM instead of staying in cache.
+        auto run = [&](int i) {
+            BlockDev & w = *c->blocks[i % c->L_];
             switch (which) {
                 case 0:
                     gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp, nullptr,
@@ -1102,12 +1104,12 @@ int sana_dit_time_gemm(sana_dit * c, int which, int iters, float * avg_ms, doubl
         };
         const double f[6] = {2.0 * M * 3 * C * C, 2.0 * M * C * C, 2.0 * M * C * C, 2.0 * M * C * C,
                              2.0 * M * c->E * C, 2.0 * M * C * c->F};
-        run();  // warm
+        run(c->L_ - 1);  // warm
         hipEvent_t e0, e1;
         hip_check(hipEventCreate(&e0), "event");
         hip_check(hipEventCreate(&e1), "event");
         hip_check(hipEventRecord(e0, c->stream), "record");
-        for (int i = 0; i < iters; ++i) run();
+        for (int i = 0; i < iters; ++i) run(i);
         hip_check(hipEventRecord(e1, c->stream), "record");
         hip_check(hipEventSynchronize(e1), "sync");
         float ms = 0.0f;

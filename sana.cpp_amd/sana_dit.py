@@ -71,6 +71,15 @@ PROTOTYPES = {
     "sana_hip_cross_attention": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
                                                 _i64, _i64, _vp]),
     "sana_hip_dwconv_glu": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "sana_op_gemm_f32": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, ctypes.c_int, _vp, _i64,
+                                        _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
+    "sana_op_unary_f32": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_int, _vp]),
+    "sana_op_softmax_f32": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.c_float, _vp, _i64, _vp]),
+    "sana_op_rms_norm_f32": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
+    "sana_op_dwconv_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "sana_op_glu_f32": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp]),
+    "sana_op_linear_attention_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "sana_op_heads_f32": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
 }
 
 _lib = None

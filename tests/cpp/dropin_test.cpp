@@ -6,6 +6,9 @@
 //
 //   dropin_test cpu          host-only checks; touches no GPU
 //   dropin_test gpu          block known answers and small-model parity on the GPU
+//   dropin_test ops          the op-level API (common_ops.h, transformer_ops.h) on the
+//                            GPU: the reference's known answers and exception types,
+//                            and random shapes against the oracle
 //   dropin_test gguf FILE [run]
 //                            weights_io + loaders on FILE (a GGUF of the seeded
 //                            small model) against the oracle's tensors; with
@@ -16,6 +19,7 @@
 //                            Sana-0.6B model (28 blocks, 36/16 heads, guidance
 //                            4.5): CAPTION [2,300,2304] and LATENT [1,32,32,32]
 //                            raw fp32 in, final latent raw fp32 out
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -26,11 +30,13 @@
 #include <string>
 #include <vector>
 
+#include "common_ops.h"
 #include "oracle.h"
 #include "scheduler.h"
 #include "tensor.h"
 #include "torch_rng.h"
 #include "transformer.h"
+#include "transformer_ops.h"
 #include "weights_io.h"
 
 namespace {
@@ -475,6 +481,202 @@ void gpu_small_model_tests() {
     close_l2(mid.data(), ref, 1e-2, "loop resumed after one step");
 }
 
+// ---------------------------------------------------------------- op-level API
+
+void ops_kat_tests() {
+    // tests/test_transformer.cpp:74-300 and tests/test_tensor.cpp:180-313 known answers
+    const Tensor lin_in = filled({2, 3}, {1, 2, 3, 4, 5, 6});
+    const Tensor lin_w = filled({3, 2}, {7, 8, 9, 10, 11, 12});
+    const Tensor lin_b = t1({1, -2});
+    const Tensor lo = linear_2d(lin_in, lin_w, &lin_b);
+    check(lo.shape() == std::vector<size_t>({2, 2}) && lo.at(0) == 59.0f && lo.at(1) == 62.0f && lo.at(2) == 140.0f &&
+              lo.at(3) == 152.0f,
+          "linear_2d");
+    const Tensor eye = eye2(), zb = t1({0, 0});
+    const Tensor mo = mlp_2d(filled({1, 2}, {1, -1}), eye, &zb, filled({2, 1}, {1, 1}), nullptr);
+    near(mo.at(0), 0.4621172f, 1e-5f, "mlp_2d");
+    const Tensor seq_in = filled({1, 2, 3}, {1, 2, 3, 4, 5, 6});
+    const Tensor so = linear_3d_lastdim(seq_in, lin_w, &lin_b);
+    check(so.shape() == std::vector<size_t>({1, 2, 2}) && so.at(0) == 59.0f && so.at(3) == 152.0f,
+          "linear_3d_lastdim");
+    const Tensor heads_in = filled({1, 2, 4}, {1, 2, 3, 4, 5, 6, 7, 8});
+    const Tensor ho = split_heads_3d(heads_in, 2);
+    check(ho.shape() == std::vector<size_t>({1, 2, 2, 2}) && ho.at({0, 1, 0, 0}) == 3.0f &&
+              ho.at({0, 0, 1, 0}) == 5.0f && ho.at({0, 1, 1, 1}) == 8.0f,
+          "split_heads_3d");
+    check(merge_heads_4d(ho).data() == heads_in.data(), "merge_heads_4d");
+    const Tensor q = filled({1, 1, 2, 2}, {1, 0, 0, 1}), k = filled({1, 1, 2, 2}, {1, 2, 3, 4});
+    const Tensor sc = attention_scores_4d(q, k);
+    check(sc.at(0) == 1.0f && sc.at(1) == 3.0f && sc.at(2) == 2.0f && sc.at(3) == 4.0f, "attention_scores_4d");
+    const Tensor w = filled({1, 1, 2, 2}, {1, 0, 0.25f, 0.75f}), v = filled({1, 1, 2, 2}, {10, 20, 30, 40});
+    const Tensor vo = attention_values_4d(w, v);
+    check(vo.at(0) == 10.0f && vo.at(1) == 20.0f && vo.at(2) == 25.0f && vo.at(3) == 35.0f, "attention_values_4d");
+    const Tensor sm = softmax_lastdim_4d(filled({1, 1, 2, 2}, {0, 0, 1, 2}));
+    near(sm.at(0), 0.5f, 1e-6f, "softmax[0]");
+    near(sm.at(2), 0.2689414f, 1e-6f, "softmax[2]");
+    near(sm.at(3), 0.7310586f, 1e-6f, "softmax[3]");
+    const Tensor ao = attention_4d(q, k, v);
+    near(ao.at(0), 26.088594f, 1e-5f, "attention_4d[0]");
+    near(ao.at(3), 36.088594f, 1e-5f, "attention_4d[3]");
+    const Tensor la = linear_attention_4d(q, k, v);
+    near(la.at(0), 25.0f, 1e-5f, "linear_attention_4d[0]");
+    near(la.at(1), 35.0f, 1e-5f, "linear_attention_4d[1]");
+    near(la.at(2), 23.333334f, 1e-5f, "linear_attention_4d[2]");
+    near(la.at(3), 33.333332f, 1e-5f, "linear_attention_4d[3]");
+    const Tensor cap = filled({1, 2, 4}, {1, 2, 3, 4, 5, 6, 7, 8});
+    Tensor c1({4, 2});
+    c1.at({0, 0}) = c1.at({1, 1}) = 1.0f;
+    const Tensor pc = project_caption_context(cap, c1, &zb, eye, &zb, t1({1, 2}));
+    const float want_pc[4] = {0.5590534f, 2.5980382f, 0.9053573f, 2.1728575f};
+    for (int i = 0; i < 4; ++i) near(pc.at(i), want_pc[i], 1e-5f, "project_caption_context " + std::to_string(i));
+    const Tensor bin = filled({1, 2, 2}, {1, 0, 0, 1});
+    const Tensor ab = attention_block_3d(bin, eye, &zb, eye, &zb, eye, &zb, eye, &zb, 1);
+    for (int i = 0; i < 4; ++i) near(ab.at(i), bin.at(i), 1e-5f, "attention_block_3d identity " + std::to_string(i));
+    const Tensor ctx = filled({1, 2, 2}, {2, 0, 0, 3});
+    const Tensor cb = cross_attention_block_3d(bin, ctx, nullptr, eye, &zb, eye, &zb, eye, &zb, eye, &zb, 1);
+    const float want_cb[4] = {1.6088594f, 0.5867110f, 0.2140836f, 2.6788745f};
+    for (int i = 0; i < 4; ++i) near(cb.at(i), want_cb[i], 1e-5f, "cross_attention_block_3d " + std::to_string(i));
+
+    const Tensor conv_in = filled({1, 2, 2, 2}, {1, 2, 3, 4, 10, 20, 30, 40});
+    const Tensor conv_w = filled({3, 2, 1, 1}, {1, 0, 0, 1, 1, 1});
+    const Tensor conv_b = t1({0, 0, -1});
+    const Tensor co = conv2d_1x1(conv_in, conv_w, &conv_b);
+    check(co.shape() == std::vector<size_t>({1, 3, 2, 2}) && co.at({0, 0, 1, 1}) == 4.0f &&
+              co.at({0, 1, 1, 1}) == 40.0f && co.at({0, 2, 0, 1}) == 21.0f && co.at({0, 2, 1, 1}) == 43.0f,
+          "conv2d_1x1");
+    Tensor dw({2, 1, 3, 3});
+    dw.at({0, 0, 1, 1}) = 1.0f;
+    dw.at({1, 0, 1, 1}) = 2.0f;
+    const Tensor dwb = t1({0.5f, -1.0f});
+    const Tensor dwo = depthwise_conv2d_3x3(conv_in, dw, &dwb);
+    check(dwo.at({0, 0, 0, 0}) == 1.5f && dwo.at({0, 0, 1, 1}) == 4.5f && dwo.at({0, 1, 0, 0}) == 19.0f &&
+              dwo.at({0, 1, 1, 1}) == 79.0f,
+          "depthwise_conv2d_3x3");
+    Tensor gi = filled({1, 2, 1, 1}, {1, 2}), gw({4, 2, 1, 1}), gb({4}), gd({4, 1, 3, 3}), gdb({4}), gp({2, 2, 1, 1});
+    gw.at({0, 0, 0, 0}) = gw.at({1, 1, 0, 0}) = gw.at({2, 0, 0, 0}) = gw.at({3, 1, 0, 0}) = 1.0f;
+    for (size_t e = 0; e < 4; ++e) gd.at({e, 0, 1, 1}) = 1.0f;
+    gp.at({0, 0, 0, 0}) = gp.at({1, 1, 0, 0}) = 1.0f;
+    const Tensor go = glumb_conv(gi, gw, &gb, gd, &gdb, gp);
+    const float s1 = 1.0f / (1.0f + std::exp(-1.0f)), s2 = 2.0f / (1.0f + std::exp(-2.0f));
+    near(go.at(0), s1 * (s1 / (1.0f + std::exp(-s1))), 1e-6f, "glumb_conv[0]");
+    near(go.at(1), s2 * (s2 / (1.0f + std::exp(-s2))), 1e-6f, "glumb_conv[1]");
+
+    float C[4];
+    gemm_row_major(lin_in.data().data(), lin_w.data().data(), lin_b.data().data(), C, 2, 3, 2);
+    check(C[0] == 59.0f && C[3] == 152.0f, "gemm_row_major");
+    const Tensor wt = lin_w.transpose_2d();
+    gemm_row_major(lin_in.data().data(), wt.data().data(), nullptr, C, 2, 3, 2, true);
+    check(C[0] == 58.0f && C[3] == 154.0f, "gemm_row_major b_transposed");
+    gemm_accumulate_row_major(lin_in.data().data(), lin_w.data().data(), C, 2, 3, 2);
+    check(C[0] == 116.0f && C[3] == 308.0f, "gemm_accumulate_row_major");
+
+    // exception types (tests/test_transformer.cpp:511-619)
+    const Tensor bad3({2, 3, 4});
+    throws<std::invalid_argument>([&] { linear_2d(bad3, lin_w, &lin_b); }, "linear_2d rank");
+    throws<std::invalid_argument>([&] { mlp_2d(bad3, eye, &zb, eye, &zb); }, "mlp_2d rank");
+    throws<std::invalid_argument>([&] { linear_3d_lastdim(lin_in, lin_w, &lin_b); }, "linear_3d_lastdim rank");
+    throws<std::invalid_argument>([&] { split_heads_3d(seq_in, 2); }, "split_heads_3d divisibility");
+    throws<std::invalid_argument>([&] { merge_heads_4d(heads_in); }, "merge_heads_4d rank");
+    throws<std::invalid_argument>([&] { attention_scores_4d(ho, q); }, "attention_scores_4d heads");
+    throws<std::invalid_argument>([&] { attention_values_4d(sc, ho); }, "attention_values_4d heads");
+    throws<std::invalid_argument>([&] { softmax_lastdim_4d(seq_in); }, "softmax_lastdim_4d rank");
+    throws<std::invalid_argument>([&] { attention_4d(ho, q, v); }, "attention_4d heads");
+    throws<std::invalid_argument>([&] { attention_block_3d(lin_in, eye, &zb, eye, &zb, eye, &zb, eye, &zb, 1); },
+                                  "attention_block_3d rank");
+    throws<std::invalid_argument>([&] { mlp_3d_lastdim(lin_in, eye, &zb, eye, &zb); }, "mlp_3d_lastdim rank");
+    throws<std::invalid_argument>([&] { conv2d_1x1(conv_in, Tensor({3, 3, 1, 1}), nullptr); }, "conv2d_1x1 channels");
+    throws<std::invalid_argument>([&] { depthwise_conv2d_5x5(conv_in, dw, nullptr); }, "depthwise 5x5 shape");
+}
+
+Tensor rnd(std::vector<size_t> shape, uint64_t seed, float scale = 1.0f) {
+    Tensor t(shape);
+    const Tensor r = randn_torch_cpu({std::max<size_t>(t.numel(), 16)}, seed);  // the generator needs >= 16 values
+    std::copy(r.data().begin(), r.data().begin() + static_cast<std::ptrdiff_t>(t.numel()), t.data().begin());
+    t.mul_inplace_scalar(scale);
+    return t;
+}
+
+// [B, C, S] <-> [B, S, C]
+Tensor swap_last(const Tensor & x, size_t B, size_t P, size_t Q) {
+    Tensor y({B, Q, P});
+    for (size_t b = 0; b < B; ++b)
+        for (size_t p = 0; p < P; ++p)
+            for (size_t q = 0; q < Q; ++q) y.data()[(b * Q + q) * P + p] = x.data()[(b * P + p) * Q + q];
+    return y;
+}
+
+void ops_random_tests() {
+    {   // linear_2d vs oracle_linear (weights [out, in] there)
+        const size_t M = 37, K = 70, N = 45;
+        const Tensor x = rnd({M, K}, 1), w = rnd({N, K}, 2, 0.1f), b = rnd({N}, 3, 0.1f);
+        std::vector<float> ref(M * N);
+        oracle_linear(x.data().data(), w.data().data(), b.data().data(), ref.data(), M, K, N);
+        close_l2(linear_2d(x, w.transpose_2d(), &b).data(), ref, 1e-5, "linear_2d random");
+    }
+    {   // attention blocks vs the oracle's
+        const size_t B = 2, N = 33, L = 20, C = 48;
+        const Tensor x = rnd({B, N, C}, 4), cx = rnd({B, L, C}, 5);
+        Tensor wt[4] = {rnd({C, C}, 6, 0.2f), rnd({C, C}, 7, 0.2f), rnd({C, C}, 8, 0.2f), rnd({C, C}, 9, 0.2f)};
+        Tensor bs[4] = {rnd({C}, 10, 0.1f), rnd({C}, 11, 0.1f), rnd({C}, 12, 0.1f), rnd({C}, 13, 0.1f)};
+        Tensor bias({B, 1, L});
+        for (size_t l = 7; l < L; ++l) bias.at({0, 0, l}) = -10000.0f;
+        std::vector<float> ref(B * N * C);
+        oracle_cross_attention_block(x.data().data(), cx.data().data(), bias.data().data(), wt[0].data().data(),
+                                     bs[0].data().data(), wt[1].data().data(), bs[1].data().data(),
+                                     wt[2].data().data(), bs[2].data().data(), wt[3].data().data(),
+                                     bs[3].data().data(), ref.data(), B, N, L, C, 4);
+        const Tensor got = cross_attention_block_3d(x, cx, &bias, wt[0].transpose_2d(), &bs[0], wt[1].transpose_2d(),
+                                                    &bs[1], wt[2].transpose_2d(), &bs[2], wt[3].transpose_2d(),
+                                                    &bs[3], 4);
+        close_l2(got.data(), ref, 1e-5, "cross_attention_block_3d random, masked");
+        oracle_attention_block(x.data().data(), wt[0].data().data(), bs[0].data().data(), wt[1].data().data(),
+                               bs[1].data().data(), wt[2].data().data(), bs[2].data().data(), wt[3].data().data(),
+                               bs[3].data().data(), ref.data(), B, N, C, 3);
+        const Tensor got2 = attention_block_3d(x, wt[0].transpose_2d(), &bs[0], wt[1].transpose_2d(), &bs[1],
+                                               wt[2].transpose_2d(), &bs[2], wt[3].transpose_2d(), &bs[3], 3);
+        close_l2(got2.data(), ref, 1e-5, "attention_block_3d random");
+    }
+    {   // GLUMBConv vs the oracle's (token-major there)
+        const size_t B = 2, H = 5, W = 7, Cin = 16, E = 24, Cout = 16, S = H * W;
+        const Tensor x = rnd({B, Cin, H, W}, 14), iw = rnd({E, Cin, 1, 1}, 15, 0.3f), ib = rnd({E}, 16, 0.1f);
+        const Tensor dw = rnd({E, 1, 3, 3}, 17, 0.3f), db = rnd({E}, 18, 0.1f), pw = rnd({Cout, E / 2, 1, 1}, 19, 0.3f);
+        const Tensor xt = swap_last(x, B, Cin, S);
+        std::vector<float> ref(B * S * Cout);
+        oracle_glumb_conv(xt.data().data(), iw.data().data(), ib.data().data(), dw.data().data(), db.data().data(),
+                          pw.data().data(), ref.data(), B, H, W, Cin, E, Cout);
+        const Tensor got = swap_last(glumb_conv(x, iw, &ib, dw, &db, pw), B, Cout, S);
+        close_l2(got.data(), ref, 1e-5, "glumb_conv random");
+    }
+    {   // caption projection vs the oracle's
+        const size_t rows = 18, Cin = 40, C = 24;
+        const Tensor x = rnd({2, 9, Cin}, 20), w1 = rnd({C, Cin}, 21, 0.2f), b1 = rnd({C}, 22, 0.1f);
+        const Tensor w2 = rnd({C, C}, 23, 0.2f), b2 = rnd({C}, 24, 0.1f), nw = rnd({C}, 25);
+        std::vector<float> ref(rows * C);
+        oracle_caption_projection(x.data().data(), w1.data().data(), b1.data().data(), w2.data().data(),
+                                  b2.data().data(), nw.data().data(), ref.data(), rows, Cin, C);
+        close_l2(project_caption_context(x, w1.transpose_2d(), &b1, w2.transpose_2d(), &b2, nw).data(), ref, 1e-5,
+                 "project_caption_context random");
+    }
+    {   // depthwise 5x5 against direct convolution on the host
+        const size_t B = 2, C = 3, H = 6, W = 9;
+        const Tensor x = rnd({B, C, H, W}, 26), w = rnd({C, 1, 5, 5}, 27), b = rnd({C}, 28);
+        std::vector<float> ref(B * C * H * W);
+        for (size_t p = 0; p < B * C; ++p)
+            for (size_t y = 0; y < H; ++y)
+                for (size_t xx = 0; xx < W; ++xx) {
+                    double acc = 0.0;
+                    for (int ky = 0; ky < 5; ++ky)
+                        for (int kx = 0; kx < 5; ++kx) {
+                            const int iy = int(y) + ky - 2, ix = int(xx) + kx - 2;
+                            if (iy >= 0 && iy < int(H) && ix >= 0 && ix < int(W))
+                                acc += double(x.data()[(p * H + iy) * W + ix]) * w.data()[(p % C) * 25 + ky * 5 + kx];
+                        }
+                    ref[(p * H + y) * W + xx] = float(acc + b.data()[p % C]);
+                }
+        close_l2(depthwise_conv2d_5x5(x, w, &b).data(), ref, 1e-6, "depthwise_conv2d_5x5 random");
+    }
+}
+
 std::vector<float> read_f32(const std::string & path, size_t n) {
     std::vector<float> v(n);
     std::ifstream f(path, std::ios::binary);
@@ -517,12 +719,15 @@ int main(int argc, char ** argv) {
         } else if (mode == "gpu") {
             gpu_kat_tests();
             gpu_small_model_tests();
+        } else if (mode == "ops") {
+            ops_kat_tests();
+            ops_random_tests();
         } else if (mode == "gguf" && argc > 2) {
             gguf_tests(argv[2], argc > 3 && std::string(argv[3]) == "run");
         } else if (mode == "full-loop" && argc > 5) {
             full_loop(argv[2], argv[3], std::strtoul(argv[4], nullptr, 10), argv[5]);
         } else {
-            std::fprintf(stderr, "usage: dropin_test cpu | gpu | gguf FILE [run] | full-loop CAPTION LATENT STEPS OUT\n");
+            std::fprintf(stderr, "usage: dropin_test cpu | gpu | ops | gguf FILE [run] | full-loop CAPTION LATENT STEPS OUT\n");
             return 2;
         }
     } catch (const std::exception & e) {

@@ -131,6 +131,15 @@ def test_dropin_device_paths():
 
 
 @pytest.mark.gpu
+def test_dropin_op_level_api():
+    """common_ops.h / transformer_ops.h on the GPU: the reference's known answers
+    (exact where the reference asserts ==), exception types, and random shapes
+    against the oracle at rel-L2 1e-5 (fp32 throughout)."""
+    res = run_exe("ops", timeout=110)
+    assert res.returncode == 0 and " 0 failures" in res.stdout
+
+
+@pytest.mark.gpu
 def test_dropin_loop_on_gguf_weights(tmp_path):
     path = str(tmp_path / "small.gguf")
     small_gguf(path)
