@@ -231,6 +231,175 @@ __global__ __launch_bounds__(256) void la_apply_kernel(const f16 * __restrict__ 
     }
 }
 
+// la_fused_kernel: the whole linear attention of one (b, h) with head_dim 32
+// in one workgroup of 8 waves, from the kGemmQKV layouts (relu already
+// applied to q and k; K^T and V^T token-contiguous per channel).
+//   1. Wave w sums its token range: S^T[d][r] += relu(K)^T[d][t..t+15] .
+//      V^T[r][t..t+15]^T and ksum[d] += relu(K)^T[d][t..] . 1 on
+//      v_mfma_f32_32x32x16_f16, both operands straight from global memory
+//      (8 consecutive tokens per lane: one 16-byte load).
+//   2. The 8 partial states are summed in LDS in wave order (bit-reproducible)
+//      and stored as an fp16 hi/lo pair, S = hi + lo.
+//   3. Wave w applies it to its tokens transposed, O^T[r][t] = [S | ksum] .
+//      relu(q)^T, so each lane holds four consecutive head dims of one token
+//      (8-byte stores); the denominator is row 0 of the ksum tile.
+// out[t][r] = O^T[r][t] / (den[t] + 1e-15), as src/transformer_ops.cpp:496-537.
+constexpr int kLfWaves = 8;
+constexpr int kLfSrow = 40;  // halves per LDS row of the hi/lo state (80 B rows)
+
+__global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __restrict__ q, int64_t ldq,
+                                                        const f16 * __restrict__ kt, const f16 * __restrict__ vt,
+                                                        f16 * __restrict__ out, int64_t ldo, int N, int H) {
+    __shared__ float part[kLfWaves][33][32];                       // per-wave S^T (rows d) + ksum row
+    __shared__ __attribute__((aligned(16))) f16 sh[2][2][32][kLfSrow];  // [S|ksum tile][hi|lo][row][d]
+    __shared__ __attribute__((aligned(16))) f16 ost[kLfWaves][32][kLfSrow];  // per-wave output staging [token][dim]
+    const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5;
+    const f16 * K = kt + ((int64_t)b * H + h) * 32 * N;  // rows d = 0..31, N tokens each
+    const f16 * V = vt + ((int64_t)b * H + h) * 32 * N;
+    const int span = (N / kLfWaves + 15) / 16 * 16;      // tokens per wave, multiple of 16
+    const int tb = w * span, te = min(N, tb + span);
+
+    // query fragments of the first kQpf apply steps are independent of the
+    // state: issue them before anything else
+    constexpr int kQpf = 4;
+    const f16 * qbase = q + (int64_t)b * N * ldq + (int64_t)h * 32 + 8 * hh;
+    f16x8 qpf[kQpf][2];
+#pragma unroll
+    for (int j = 0; j < kQpf; ++j) {
+        const int tq = min(tb + 32 * j + (lane & 31), N - 1);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) qpf[j][kk] = *reinterpret_cast<const f16x8 *>(qbase + (int64_t)tq * ldq + kk * 16);
+    }
+
+    // 1. partial state: each group's loads (kG steps of 16 tokens) are all
+    // issued before its MFMAs
+    f32x16 s, ks;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = ks[i] = 0.0f;
+    f16x8 ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (f16)1.0f;
+    const f16 * krow = K + (int64_t)(lane & 31) * N + 8 * hh;
+    const f16 * vrow = V + (int64_t)(lane & 31) * N + 8 * hh;
+    constexpr int kG = 8;
+    for (int g0 = tb; g0 < te; g0 += 16 * kG) {
+        f16x8 ka[kG], va[kG];
+#pragma unroll
+        for (int u = 0; u < kG; ++u) {
+            const int t = g0 + 16 * u;
+            if (t < te) {
+                ka[u] = *reinterpret_cast<const f16x8 *>(krow + t);
+                va[u] = *reinterpret_cast<const f16x8 *>(vrow + t);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kG; ++u) {
+            if (g0 + 16 * u < te) {
+                s = mfma_32x32x16(ka[u], va[u], s);
+                ks = mfma_32x32x16(ka[u], ones, ks);
+            }
+        }
+    }
+    // lane holds column r = lane & 31 and rows d = 8*(i/4) + 4*hh + i%4
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int d = 8 * (i >> 2) + 4 * hh + (i & 3);
+        part[w][d][lane & 31] = s[i];
+        if ((lane & 31) == 0) part[w][32][d] = ks[i];
+    }
+    __syncthreads();
+
+    // 2. fixed-order sum of the partials -> hi/lo state tiles.  Tile 0 row r
+    // holds S[r][d]; tile 1 row 0 holds ksum[d], rows 1..31 are zero.
+    for (int e = tid; e < 2 * 32 * 32; e += 64 * kLfWaves) {
+        // consecutive threads take consecutive r: conflict-free reads of part[.][d][r]
+        const int tile = e >> 10, d = (e >> 5) & 31, r = e & 31;
+        float acc = 0.0f;
+        if (tile == 0) {
+            for (int ww = 0; ww < kLfWaves; ++ww) acc += part[ww][d][r];
+        } else if (r == 0) {
+            for (int ww = 0; ww < kLfWaves; ++ww) acc += part[ww][32][d];
+        }
+        // tile 1, r > 0: zero rows
+        const f16 hi = (f16)acc;
+        sh[tile][0][r][d] = hi;
+        sh[tile][1][r][d] = (f16)(acc - (float)hi);
+    }
+    __syncthreads();
+
+    // 3. apply, 32 tokens per step
+    const f16 * srow0 = &sh[0][0][lane & 31][8 * hh];
+    f16x8 sa[2][2][2];  // [tile][hi|lo][k-step]
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+        for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+                sa[tile][hl][kk] = *reinterpret_cast<const f16x8 *>(srow0 + (tile * 2 + hl) * 32 * kLfSrow + kk * 16);
+    // two 32-token steps per iteration: four independent MFMA chains
+    // Output of 32 tokens: staged in this wave's LDS tile [token][dim] (the lane
+    // holds token lane & 31, dims 8*i4 + 4*hh + {0..3}), then written as full
+    // 64-byte token rows, four lanes per token, 16 tokens per store instruction.
+    auto apply_store = [&](int t0, const f32x16 & o, const f32x16 & dn) {
+        // the denominator of token column (lane & 31) is row 0: i = 0 on the hh = 0 lane
+        const float rden = 1.0f / (__shfl(dn[0], lane & 31, 64) + 1e-15f);
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            f16x4 v4;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v4[u] = (f16)(o[4 * i4 + u] * rden);
+            *reinterpret_cast<f16x4 *>(&ost[w][lane & 31][8 * i4 + 4 * hh]) = v4;
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int tl = half * 16 + (lane >> 2), c8 = (lane & 3) * 8;
+            const f16x8 v8 = *reinterpret_cast<const f16x8 *>(&ost[w][tl][c8]);
+            const int t = t0 + tl;
+            if (t < te) *reinterpret_cast<f16x8 *>(out + ((int64_t)b * N + t) * ldo + (int64_t)h * 32 + c8) = v8;
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+    auto load_q = [&](int t0, f16x8 (&qf)[2]) {
+        const int tq = min(t0 + (lane & 31), N - 1);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) qf[kk] = *reinterpret_cast<const f16x8 *>(qbase + (int64_t)tq * ldq + kk * 16);
+    };
+    for (int j = 0, t0 = tb; t0 < te; j += 2, t0 += 64) {
+        f16x8 qa[2], qb[2];
+        if (j + 1 < kQpf) {
+#pragma unroll
+            for (int jj = 0; jj + 1 < kQpf; jj += 2)
+                if (jj == j) {
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk) {
+                        qa[kk] = qpf[jj][kk];
+                        qb[kk] = qpf[jj + 1][kk];
+                    }
+                }
+        } else {
+            load_q(t0, qa);
+            load_q(t0 + 32, qb);
+        }
+        f32x16 oa, da, ob, db;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oa[i] = da[i] = ob[i] = db[i] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl) {
+                oa = mfma_32x32x16(sa[0][hl][kk], qa[kk], oa);
+                ob = mfma_32x32x16(sa[0][hl][kk], qb[kk], ob);
+                da = mfma_32x32x16(sa[1][hl][kk], qa[kk], da);
+                db = mfma_32x32x16(sa[1][hl][kk], qb[kk], db);
+            }
+        apply_store(t0, oa, da);
+        if (t0 + 32 < te) apply_store(t0 + 32, ob, db);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // K4: softmax cross-attention (attention_4d, src/transformer_ops.cpp:348-392:
 // scores * 1/sqrt(D), + bias, softmax over keys, . V) fused per
@@ -577,6 +746,22 @@ int la_chunk_tokens(int N) {
     return (per + kLaSub - 1) / kLaSub * kLaSub;
 }
 }  // namespace
+
+bool linear_attention_fused_ok(int N, int D) { return D == 32 && N > 0 && N % 16 == 0; }
+
+
+hipError_t linear_attention_fused(const half_t * q, int64_t ldq, const half_t * kt, const half_t * vt, half_t * out,
+                                  int64_t ldo, int B, int N, int H, int D, hipStream_t s) {
+    if (!linear_attention_fused_ok(N, D) || B <= 0 || H <= 0 || ldq < (int64_t)H * D || ldo < (int64_t)H * D ||
+        ldq % 8 || ldo % 8 || (int64_t)B * H > 65535 ||
+        ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kt) | reinterpret_cast<uintptr_t>(vt)) & 15) ||
+        (reinterpret_cast<uintptr_t>(out) & 15))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(la_fused_kernel, dim3((unsigned)(B * H)), dim3(64 * kLfWaves), 0, s,
+                       reinterpret_cast<const f16 *>(q), ldq, reinterpret_cast<const f16 *>(kt),
+                       reinterpret_cast<const f16 *>(vt), reinterpret_cast<f16 *>(out), ldo, N, H);
+    return hipGetLastError();
+}
 
 size_t linattn_workspace_floats(int B, int N, int H, int D) {
     const int T = la_chunk_tokens(N);

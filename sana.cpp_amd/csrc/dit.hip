@@ -152,6 +152,7 @@ struct sana_dit {
     DevMem cap32, cap16, caph16, capf32, ctx32, ctx16, kc, vt, bias;
     // forward workspace
     int64_t ws_M = 0, ws_B = 0;
+    DevMem la_kt, la_vt;  // relu(K)^T and V^T per channel, token-contiguous (fused linear attention)
     DevMem x32, fin32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, d_t, tp, e1, emb, tmod, mod_all, lat_in,
         np_out;
     DevMem loop_lat[2], loop_x0[2];  // denoise loop: latent ping-pong and converted-output history
@@ -217,6 +218,33 @@ void expect_shape(const char * name, const int64_t * shape, int ndim, std::vecto
 }
 
 // ---------------------------------------------------------------- forward pieces
+// The fused q | k | v projection of the linear-attention path (kGemmQKV):
+// relu(q) token-major into qkv16 (ld 3C), relu(K)^T and V^T into la_kt / la_vt.
+void gemm_qkv_split(sana_dit * c, BlockDev & w, int64_t B, int64_t N, hipStream_t s) {
+    sana::GemmParams p;
+    p.A = c->xa16.as<half_t>();
+    p.lda = c->Cp;
+    p.W = w.w_qkv.as<half_t>();
+    p.ldw = c->Cp;
+    p.M = (int)(B * N);
+    p.N = (int)(3 * c->C);
+    p.K = (int)c->Cp;
+    p.bias = w.has_qkv_bias ? w.b_qkv.as<float>() : nullptr;
+    p.mode = sana::kGemmQKV;
+    p.out16 = c->qkv16.as<half_t>();
+    p.ldo16 = 3 * c->C;
+    p.kt16 = c->la_kt.as<half_t>();
+    p.vt16 = c->la_vt.as<half_t>();
+    p.qkv_c = (int)c->C;
+    p.qkv_n = (int)N;
+    launch_check(sana::gemm(p, s), "gemm_qkv");
+}
+
+// Whether the self attention runs as kGemmQKV + one fused linear-attention kernel.
+bool fused_linear_attention(const sana_dit * c, int64_t N) {
+    return sana::linear_attention_fused_ok((int)N, (int)c->Ds) && c->C % 8 == 0;
+}
+
 void gemm_store(sana_dit * c, const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N,
                 int64_t K, const float * bias, int act, half_t * o16, int64_t ldo16, float * o32, int64_t ldo32,
                 hipStream_t s) {
@@ -328,6 +356,8 @@ void ensure_forward_buffers(sana_dit * c, int64_t B, int64_t N) {
         c->fin32.ensure((size_t)M * C * 4);
         c->xa16.ensure((size_t)M * c->Cp * 2);
         c->qkv16.ensure((size_t)M * 3 * C * 2);
+        c->la_kt.ensure((size_t)M * C * 2);
+        c->la_vt.ensure((size_t)M * C * 2);
         c->o16.ensure((size_t)M * c->Cp * 2);
         c->r16.ensure((size_t)M * c->Cp * 2);
         c->q16.ensure((size_t)M * C * 2);
@@ -384,13 +414,21 @@ void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * 
                                    w.has_ln1 ? w.ln1_g.as<float>() : nullptr, w.has_ln1 ? w.ln1_b.as<float>() : nullptr,
                                    mod, nullptr, 6 * C, 0, C, s),
                  "ln_modulate");
-    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
-               w.has_qkv_bias ? w.b_qkv.as<float>() : nullptr, sana::kActNone, c->qkv16.as<half_t>(), 3 * C, nullptr,
-               0, s);
-    const half_t * qkv = c->qkv16.as<half_t>();
-    launch_check(sana::linear_attention(qkv, qkv + C, qkv + 2 * C, 3 * C, c->o16.as<half_t>(), c->Cp, (int)B, (int)N,
-                                        (int)c->Hs, (int)c->Ds, c->la_ws.as<float>(), s),
-                 "linear_attention");
+    if (fused_linear_attention(c, N)) {
+        gemm_qkv_split(c, w, B, N, s);
+        launch_check(sana::linear_attention_fused(c->qkv16.as<half_t>(), 3 * C, c->la_kt.as<half_t>(),
+                                                  c->la_vt.as<half_t>(), c->o16.as<half_t>(), c->Cp, (int)B, (int)N,
+                                                  (int)c->Hs, (int)c->Ds, s),
+                     "linear_attention_fused");
+    } else {
+        gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
+                   w.has_qkv_bias ? w.b_qkv.as<float>() : nullptr, sana::kActNone, c->qkv16.as<half_t>(), 3 * C,
+                   nullptr, 0, s);
+        const half_t * qkv = c->qkv16.as<half_t>();
+        launch_check(sana::linear_attention(qkv, qkv + C, qkv + 2 * C, 3 * C, c->o16.as<half_t>(), c->Cp, (int)B,
+                                            (int)N, (int)c->Hs, (int)c->Ds, c->la_ws.as<float>(), s),
+                     "linear_attention");
+    }
     // x += gate_msa * (o Wo^T + bo); r16 = fp16(x) for the cross-attention query
     gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_out.as<half_t>(), c->Cp, M, C, c->Cp, w.b_out.as<float>(),
                mod + 2 * C, nullptr, 6 * C, N, c->x32.as<float>(), C, c->r16.as<half_t>(), c->Cp, s);
@@ -1076,8 +1114,11 @@ int sana_dit_time_gemm(sana_dit * c, int which, int iters, float * avg_ms, doubl
             BlockDev & w = *c->blocks[i % c->L_];
             switch (which) {
                 case 0:
-                    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp, nullptr,
-                               sana::kActNone, c->qkv16.as<half_t>(), 3 * C, nullptr, 0, c->stream);
+                    if (fused_linear_attention(c, N))
+                        gemm_qkv_split(c, w, M / N, N, c->stream);
+                    else
+                        gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
+                                   nullptr, sana::kActNone, c->qkv16.as<half_t>(), 3 * C, nullptr, 0, c->stream);
                     break;
                 case 1:
                     gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_out.as<half_t>(), c->Cp, M, C, c->Cp,

@@ -276,6 +276,32 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                 }
             }
         __syncthreads();
+        if constexpr (MODE == kGemmQKV) {
+            // k and v sections: items (column, 8-row octet), consecutive lanes on
+            // consecutive octets of one column, so each column's 16-byte stores
+            // form one contiguous token run.  Rows of an octet share a batch
+            // (qkv_n % 8 == 0).  The q section is handled below as a plain store.
+            constexpr int OCT = BM / 8;
+            const int C3 = p.qkv_c;
+            for (int item = tid; item < BN * OCT; item += G::NT) {
+                const int oct = item % OCT, cl = item / OCT;
+                const int col = n0 + cl, row0 = m0 + oct * 8;
+                if (col >= p.N || row0 >= p.M || col < C3) continue;
+                const bool is_k = col < 2 * C3;
+                const int ch = col - (is_k ? C3 : 2 * C3);
+                const float bcol = p.bias ? p.bias[col] : 0.0f;
+                f16x8 h;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float v = ct[(oct * 8 + j) * LDC + cl] + bcol;
+                    if (is_k) v = fmaxf(v, 0.0f);
+                    h[j] = (f16)v;
+                }
+                const int b = row0 / p.qkv_n, t0 = row0 - b * p.qkv_n;
+                f16 * dst = reinterpret_cast<f16 *>(is_k ? p.kt16 : p.vt16);
+                *reinterpret_cast<f16x8 *>(dst + ((int64_t)b * C3 + ch) * p.qkv_n + t0) = h;
+            }
+        }
         // Each thread owns one 8-column chunk of the tile for all its rows, so
         // the bias is fetched once; rows step by NT / CPR.
         constexpr int CPR = BN / 8;
@@ -284,6 +310,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
         const int col = n0 + c8;
         const int nc = min(8, p.N - col);
         if (nc <= 0) return;
+        if constexpr (MODE == kGemmQKV) {
+            if (col >= p.qkv_c) return;  // k / v columns were stored above
+        }
         const bool vec8 = p.vec && nc == 8;
         float bv[8];
         if (p.bias && vec8) {
@@ -302,11 +331,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
             const float4 v1 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8 + 4]);
             float v[8] = {v0.x + bv[0], v0.y + bv[1], v0.z + bv[2], v0.w + bv[3],
                           v1.x + bv[4], v1.y + bv[5], v1.z + bv[6], v1.w + bv[7]};
-            if constexpr (MODE == kGemmStore) {
+            if constexpr (MODE == kGemmStore || MODE == kGemmQKV) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     if constexpr (ACT == kActSilu) v[e] = silu_f(v[e]);
                     if constexpr (ACT == kActGelu) v[e] = gelu_tanh_f(v[e]);
+                    if constexpr (MODE == kGemmQKV) v[e] = fmaxf(v[e], 0.0f);
                 }
                 if (vec8) {
                     if (p.out16) {
@@ -398,6 +428,7 @@ hipError_t launch(const GemmParams & p, hipStream_t s) {
     const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
     if (p.mode == kGemmResidual) return launch_mode<BM, BN, WM, WN, STAGES, kGemmResidual, SCHED, kActNone>(p, tiles, s);
     if (p.mode == kGemmVT) return launch_mode<BM, BN, WM, WN, STAGES, kGemmVT, SCHED, kActNone>(p, tiles, s);
+    if (p.mode == kGemmQKV) return launch_mode<BM, BN, WM, WN, STAGES, kGemmQKV, SCHED, kActNone>(p, tiles, s);
     if (p.act == kActSilu) return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActSilu>(p, tiles, s);
     if (p.act == kActGelu) return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActGelu>(p, tiles, s);
     return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActNone>(p, tiles, s);
@@ -417,6 +448,11 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
                               p.vt_ld < p.vt_cols || p.N != p.vt_batch * p.vt_cols || p.M % p.vt_rows))
         return hipErrorInvalidValue;
     if (p.mode == kGemmStore && !p.out16 && !p.out32) return hipErrorInvalidValue;
+    if (p.mode == kGemmQKV &&
+        (!p.out16 || p.out32 || !p.kt16 || !p.vt16 || p.qkv_c <= 0 || p.qkv_c % 8 || p.N != 3 * p.qkv_c ||
+         p.qkv_n <= 0 || p.qkv_n % 8 || p.M % p.qkv_n ||
+         ((reinterpret_cast<uintptr_t>(p.kt16) | reinterpret_cast<uintptr_t>(p.vt16)) & 15)))
+        return hipErrorInvalidValue;
     if (p.gate_a && p.rows_per_batch <= 0) return hipErrorInvalidValue;
     // 16-byte epilogue accesses need 8-element aligned rows and 16-byte aligned bases.
     bool vec = true;

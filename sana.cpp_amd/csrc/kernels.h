@@ -14,6 +14,7 @@ enum GemmMode {
     kGemmStore = 0,     // out16/out32[m, n] = act(acc + bias[n])
     kGemmResidual = 1,  // out32[m, n] += gate(m, n) * (acc + bias[n]); out16 = f16(out32) if set
     kGemmVT = 2,        // transposed-batched store of V^T (see GemmParams::vt_*)
+    kGemmQKV = 3,       // fused q|k|v split for linear attention (see GemmParams::qkv_*)
 };
 
 enum GemmAct { kActNone = 0, kActSilu = 1, kActGelu = 2 };
@@ -43,6 +44,14 @@ struct GemmParams {
     // stored at out16[((blk * vt_batch + b) * vt_rows + r) * vt_ld + j].
     int vt_rows = 0, vt_cols = 0, vt_batch = 0;
     int64_t vt_ld = 0;
+    // kGemmQKV: output column n of section s = n / qkv_c (q, k, v), channel
+    // c = n % qkv_c, row m = b * qkv_n + t:
+    //   q: out16[m * ldo16 + c] = relu(acc + bias)        (token-major)
+    //   k: kt16[(b * qkv_c + c) * qkv_n + t] = relu(acc + bias)   (token-contiguous)
+    //   v: vt16[(b * qkv_c + c) * qkv_n + t] = acc + bias
+    half_t * kt16 = nullptr;
+    half_t * vt16 = nullptr;
+    int qkv_c = 0, qkv_n = 0;
     int vec = 0;  // set by gemm(): 16-byte epilogue accesses are aligned
 };
 
@@ -86,6 +95,11 @@ hipError_t final_layer(const float * x, const float * emb, const float * table, 
 // ReLU linear attention.  q/k/v fp16 token-major with row stride ld (head h at
 // columns h*D..), out fp16 with row stride ldo.  Workspace: partial states.
 size_t linattn_workspace_floats(int B, int N, int H, int D);
+// Whole linear attention in one launch for head_dim 32, from the kGemmQKV
+// layouts: relu(q) token-major [B*N, ldq], relu(K)^T and V^T [B][H*32][N].
+bool linear_attention_fused_ok(int N, int D);
+hipError_t linear_attention_fused(const half_t * q, int64_t ldq, const half_t * kt, const half_t * vt, half_t * out,
+                                  int64_t ldo, int B, int N, int H, int D, hipStream_t s);
 hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v, int64_t ld, half_t * out,
                             int64_t ldo, int B, int N, int H, int D, float * workspace, hipStream_t s);
 
