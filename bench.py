@@ -114,6 +114,60 @@ def cpu_baseline():
             "host_nproc": os.cpu_count()}
 
 
+def microbench_4096(sana_dit, torch, dev, stream):
+    """Linear attention (16 heads x 72) and the Mix-FFN (inverted GEMM + SiLU,
+    depthwise 3x3 + GLU, point GEMM + gated residual) at 64x64 = 4096 tokens,
+    batch 2, through the kernel-level launchers on `stream`."""
+    L = sana_dit.lib()
+    B, N, H, D, C, E = 2, 4096, 16, 72, 1152, 5760
+    F, M = E // 2, 2 * 4096
+    g = torch.Generator(device=dev).manual_seed(5)
+    q, k, v = (torch.randn((M, C), device=dev, dtype=torch.float16, generator=g) for _ in range(3))
+    o = torch.empty((M, C), device=dev, dtype=torch.float16)
+    ws = torch.empty(L.sana_hip_linear_attention_workspace(B, N, H, D) // 4 + 1, device=dev, dtype=torch.float32)
+    x16 = torch.randn((M, C), device=dev, dtype=torch.float16, generator=g)
+    w_inv = torch.randn((E, C), device=dev, dtype=torch.float16, generator=g) * 0.02
+    b_inv = torch.zeros(E, device=dev)
+    hid = torch.empty((M, E), device=dev, dtype=torch.float16)
+    w_dw = torch.randn((9, E), device=dev, generator=g) * 0.2
+    b_dw = torch.zeros(E, device=dev)
+    glu = torch.empty((M, F), device=dev, dtype=torch.float16)
+    w_pt = torch.randn((C, F), device=dev, dtype=torch.float16, generator=g) * 0.02
+    x32 = torch.zeros((M, C), device=dev)
+    sp = stream.cuda_stream
+    torch.cuda.synchronize()
+
+    def la():
+        sana_dit.check(L.sana_hip_linear_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), C, o.data_ptr(), C, B, N,
+                                                   H, D, ws.data_ptr(), sp))
+
+    def ffn_parts():
+        sana_dit.check(L.sana_hip_gemm(x16.data_ptr(), C, w_inv.data_ptr(), C, M, E, C, b_inv.data_ptr(), 1,
+                                       hid.data_ptr(), E, None, 0, sp))
+        sana_dit.check(L.sana_hip_dwconv_glu(hid.data_ptr(), E, w_dw.data_ptr(), b_dw.data_ptr(), glu.data_ptr(), F, B,
+                                             64, 64, F, sp))
+        sana_dit.check(L.sana_hip_gemm_residual(glu.data_ptr(), F, w_pt.data_ptr(), F, M, C, F, None, None, None, 0, N,
+                                                x32.data_ptr(), C, None, 0, sp))
+
+    def timed(fn, it=20):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(it):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / it * 1e3
+
+    la_us = timed(la)
+    ffn_us = timed(ffn_parts)
+    la_bytes = 4 * M * C * 2                      # q, k, v in, out
+    ffn_flops = 2 * M * E * C + 2 * M * C * F
+    return {"linear_attention_us": round(la_us, 2), "linear_attention_GBs": round(la_bytes / (la_us * 1e-6) / 1e9, 1),
+            "mixffn_us": round(ffn_us, 2), "mixffn_tflops": round(ffn_flops / (ffn_us * 1e-6) / 1e12, 1),
+            "shape": "B=2, 64x64 tokens, C=1152, self heads 16x72, Mix-FFN 1152->5760->2880->1152"}
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (None when it is absent)."""
@@ -214,6 +268,20 @@ def main():
         ms_w, fl_w = d.time_gemm(which, 20)
         per_gemm[nm] = {"us": round(ms_w * 1e3, 2), "tflops": round(fl_w / (ms_w * 1e-3) / 1e12, 1)}
 
+    # 4096 px forward (latent 128x128, 16384 image tokens, same context): context resident
+    lat5 = torch.from_numpy(rng.standard_normal((1, DIMS["latent_channels"], 128, 128), dtype=np.float32)).to(dev)
+    out5 = torch.empty((B, DIMS["latent_channels"], 128, 128), device=dev, dtype=torch.float32)
+    d.forward_device(lat5, tuple(lat5.shape), TIMESTEP, out5, sp)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for _ in range(3):
+        d.forward_device(lat5, tuple(lat5.shape), TIMESTEP, out5, sp)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    c5_ms = ev0.elapsed_time(ev1) / 3
+    c5_flops = forward_flops(B, 128 * 128, L, with_context=False)
+    c4 = microbench_4096(sana_dit, torch, dev, stream)
+
     step_flops = forward_flops(B, N, L, with_context=True)
     fwd_flops = forward_flops(B, N, L, with_context=False)
     res = {
@@ -245,6 +313,9 @@ def main():
                      "frac": round(gemm_tflops / PEAK_MFMA_TFLOPS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes": GEMM_BYTES, "avg_us": round(gemm_ms * 1e3, 2)},
         "cpu_baseline": cpu,
+        "forward_4096px": {"ms": round(c5_ms, 3), "tflops": round(c5_flops / (c5_ms * 1e-3) / 1e12, 1),
+                           "tokens": 128 * 128, "note": "28 blocks, CFG batch 2, context resident"},
+        "microbench_4096_tokens": c4,
     }
     d.close()
     print(json.dumps(res), flush=True)

@@ -21,9 +21,33 @@ namespace {
 //   summed on the VALU from the same LDS rows.  Each chunk writes its partial
 //   (D+1) x D state.
 // la_reduce_kernel: sums the chunk partials in fixed chunk order (no atomics,
-//   bit-reproducible) into an fp16 hi/lo pair of the state.
+//   bit-reproducible) into an fp16 hi/lo pair of the state, scaled by 2^k.
 // la_apply_kernel: relu(Q) . [S | ksum]^T on MFMA (hi and lo halves), one wave
 //   per 32 tokens, then the division by the denominator column.
+//
+// Range of the fp16 state.  S and ksum grow with the token count (|S| reaches
+// ~7e3 at 1024 tokens of the 0.6B model, so ~1e5 at 16384 tokens, past fp16's
+// 65504).  Each (b, h) state is therefore scaled by a power of two 2^k chosen
+// from an upper bound m of its largest |entry|: m 2^k lies in [2^13, 2^14).
+// Scaling by 2^k is exact in fp32 and cancels in
+// (S . q) / (ksum . q + 1e-15) once the 1e-15 is scaled by 2^k as well.
+
+// Exponent k of the state scale 2^k for an upper bound m of max |S|; a zero,
+// NaN or infinite bound leaves the state unscaled.
+SANA_DEV int la_state_exponent(float m) {
+    if (!(m > 0.0f) || !(m <= 3.402823466e38f)) return 0;
+    int ex;
+    (void)frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1)
+    return min(60, max(-60, 14 - ex));
+}
+
+// Upper bound of max |S| over the nch chunk partials of one (b, h): the sum of
+// their maxima, in chunk order (every kernel computes the same k from it).
+SANA_DEV float la_bound(const float * __restrict__ pmax, int nch) {
+    float m = 0.0f;
+    for (int c = 0; c < nch; ++c) m += pmax[c];
+    return m;
+}
 
 constexpr int kLaSub = 64;                 // tokens per LDS sub-chunk
 constexpr int kLaChunks = 16;              // partial states per (b, h)
@@ -32,7 +56,7 @@ constexpr int kLaRow = kLaSub + 8;         // halves per transposed LDS row (144
 template <int TD>  // ceil(D / 32): 32x32 MFMA tiles per side of the state
 __global__ __launch_bounds__(64) void la_state_kernel(const f16 * __restrict__ k, const f16 * __restrict__ v,
                                                       int64_t ld, int N, int H, int D, int T, int nch, int vec,
-                                                      float * __restrict__ part) {
+                                                      float * __restrict__ part, float * __restrict__ pmax) {
     constexpr int DP = TD * 32;
     __shared__ __attribute__((aligned(16))) f16 Kt[DP][kLaRow];
     __shared__ __attribute__((aligned(16))) f16 Vt[DP][kLaRow];
@@ -137,18 +161,33 @@ __global__ __launch_bounds__(64) void la_state_kernel(const f16 * __restrict__ k
         const int d = lane + 64 * i;
         if (d < D) out[D * D + d] = ks[i];
     }
+    // max |entry| of this partial (padding entries are zero)
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TD; ++i)
+#pragma unroll
+        for (int j = 0; j < TD; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(acc[i][j][q]));
+#pragma unroll
+    for (int i = 0; i < (DP + 63) / 64; ++i) m = fmaxf(m, ks[i]);
+    m = wave_max(m);
+    if (lane == 0) pmax[((int64_t)b * H + h) * nch + c] = m;
 }
 
-// Sums the chunk partials in fixed order and writes the state, transposed to
-// the apply kernel's MFMA operand layout, as an fp16 hi/lo pair:
-// S[r][d] = hi[r][d] + lo[r][d] with hi = f16(S), lo = f16(S - hi), so the fp16
-// products of the apply step carry the fp32 state to ~2^-22 relative error.
-// Layout [NP][KP] (r rows incl. the ksum row r = D, d contiguous), zero padded.
-__global__ __launch_bounds__(256) void la_reduce_kernel(const float * __restrict__ part, int nch, int D, int NP, int KP,
-                                                        f16 * __restrict__ hi, f16 * __restrict__ lo) {
+// Sums the chunk partials in fixed order and writes the state 2^k S, transposed
+// to the apply kernel's MFMA operand layout, as an fp16 hi/lo pair:
+// 2^k S[r][d] = hi[r][d] + lo[r][d] with hi = f16(2^k S), lo = f16(2^k S - hi),
+// so the fp16 products of the apply step carry the fp32 state to ~2^-22
+// relative error.  Layout [NP][KP] (r rows incl. the ksum row r = D, d
+// contiguous), zero padded.
+__global__ __launch_bounds__(256) void la_reduce_kernel(const float * __restrict__ part,
+                                                        const float * __restrict__ pmax, int nch, int D, int NP,
+                                                        int KP, f16 * __restrict__ hi, f16 * __restrict__ lo) {
     const int e = blockIdx.x * 256 + threadIdx.x;
     const int bh = blockIdx.y;
     if (e >= NP * KP) return;
+    const float scale = ldexpf(1.0f, la_state_exponent(la_bound(pmax + (int64_t)bh * nch, nch)));
     const int r = e / KP, d = e - r * KP;
     float s = 0.0f;
     if (r <= D && d < D) {
@@ -156,18 +195,21 @@ __global__ __launch_bounds__(256) void la_reduce_kernel(const float * __restrict
         const float * p = part + (int64_t)bh * nch * E + r * D + d;
         for (int c = 0; c < nch; ++c) s += p[(int64_t)c * E];
     }
+    s *= scale;
     const f16 h = (f16)s;
     hi[(int64_t)bh * NP * KP + e] = h;
     lo[(int64_t)bh * NP * KP + e] = (f16)(s - (float)h);
 }
 
-// out[t][r] = (relu(q) . S^T)[t][r] / ((relu(q) . S^T)[t][D] + 1e-15) on
+// out[t][r] = (relu(q) . S^T)[t][r] / ((relu(q) . S^T)[t][D] + 1e-15) (both
+// terms of the ratio scaled by the state's 2^k) on
 // v_mfma_f32_32x32x16_f16: one wave per 32 tokens of one (b, h).  The A
 // operand (8 consecutive head dims of one token) comes straight from the
 // token-major q rows; columns past D are masked to zero.
 template <int NT, int KS>  // NT: 32-wide column tiles of [S | ksum]; KS: 16-deep steps over d
 __global__ __launch_bounds__(256) void la_apply_kernel(const f16 * __restrict__ q, int64_t ld,
                                                        const f16 * __restrict__ shi, const f16 * __restrict__ slo,
+                                                       const float * __restrict__ pmax, int nch,
                                                        f16 * __restrict__ out, int64_t ldo, int N, int H, int D,
                                                        int vec) {
     constexpr int NP = NT * 32, KP = KS * 16;
@@ -210,6 +252,7 @@ __global__ __launch_bounds__(256) void la_apply_kernel(const f16 * __restrict__ 
     // Lane holds column r = 32 j + (lane & 31), rows t0 + 8*(i/4) + 4*(lane/32) + i%4.
     // The denominator is column D, held by lane (lane & 32) | (D % 32) of tile D / 32.
     const int jd = D >> 5, cd = D & 31;
+    const float eps = ldexpf(1e-15f, la_state_exponent(la_bound(pmax + ((int64_t)b * H + h) * nch, nch)));
     float den[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -217,7 +260,7 @@ __global__ __launch_bounds__(256) void la_apply_kernel(const f16 * __restrict__ 
 #pragma unroll
         for (int j = 0; j < NT; ++j)
             if (j == jd) v = acc[j][i];
-        den[i] = __shfl(v, (lane & 32) | cd, 64) + 1e-15f;
+        den[i] = __shfl(v, (lane & 32) | cd, 64) + eps;
     }
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -239,11 +282,12 @@ __global__ __launch_bounds__(256) void la_apply_kernel(const f16 * __restrict__ 
 //      v_mfma_f32_32x32x16_f16, both operands straight from global memory
 //      (8 consecutive tokens per lane: one 16-byte load).
 //   2. The 8 partial states are summed in LDS in wave order (bit-reproducible)
-//      and stored as an fp16 hi/lo pair, S = hi + lo.
+//      and stored as an fp16 hi/lo pair, 2^k S = hi + lo, k from the sum of
+//      the 8 partials' maxima (the range rule of the three-kernel path).
 //   3. Wave w applies it to its tokens transposed, O^T[r][t] = [S | ksum] .
 //      relu(q)^T, so each lane holds four consecutive head dims of one token
 //      (8-byte stores); the denominator is row 0 of the ksum tile.
-// out[t][r] = O^T[r][t] / (den[t] + 1e-15), as src/transformer_ops.cpp:496-537.
+// out[t][r] = O^T[r][t] / (den[t] + 2^k 1e-15), as src/transformer_ops.cpp:496-537.
 constexpr int kLfWaves = 8;
 constexpr int kLfSrow = 40;  // halves per LDS row of the hi/lo state (80 B rows)
 
@@ -253,6 +297,7 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
     __shared__ float part[kLfWaves][33][32];                       // per-wave S^T (rows d) + ksum row
     __shared__ __attribute__((aligned(16))) f16 sh[2][2][32][kLfSrow];  // [S|ksum tile][hi|lo][row][d]
     __shared__ __attribute__((aligned(16))) f16 ost[kLfWaves][32][kLfSrow];  // per-wave output staging [token][dim]
+    __shared__ float pmax[kLfWaves];                                   // max |entry| of each wave's partial
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5;
     const f16 * K = kt + ((int64_t)b * H + h) * 32 * N;  // rows d = 0..31, N tokens each
@@ -308,7 +353,16 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
         part[w][d][lane & 31] = s[i];
         if ((lane & 31) == 0) part[w][32][d] = ks[i];
     }
+    {
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = fmaxf(m, fmaxf(fabsf(s[i]), ks[i]));
+        m = wave_max(m);
+        if (lane == 0) pmax[w] = m;
+    }
     __syncthreads();
+    const int kexp = la_state_exponent(la_bound(pmax, kLfWaves));
+    const float scale = ldexpf(1.0f, kexp), eps = ldexpf(1e-15f, kexp);
 
     // 2. fixed-order sum of the partials -> hi/lo state tiles.  Tile 0 row r
     // holds S[r][d]; tile 1 row 0 holds ksum[d], rows 1..31 are zero.
@@ -322,6 +376,7 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
             for (int ww = 0; ww < kLfWaves; ++ww) acc += part[ww][32][d];
         }
         // tile 1, r > 0: zero rows
+        acc *= scale;
         const f16 hi = (f16)acc;
         sh[tile][0][r][d] = hi;
         sh[tile][1][r][d] = (f16)(acc - (float)hi);
@@ -344,7 +399,7 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
     // 64-byte token rows, four lanes per token, 16 tokens per store instruction.
     auto apply_store = [&](int t0, const f32x16 & o, const f32x16 & dn) {
         // the denominator of token column (lane & 31) is row 0: i = 0 on the hh = 0 lane
-        const float rden = 1.0f / (__shfl(dn[0], lane & 31, 64) + 1e-15f);
+        const float rden = 1.0f / (__shfl(dn[0], lane & 31, 64) + eps);
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
             f16x4 v4;
@@ -769,7 +824,8 @@ size_t linattn_workspace_floats(int B, int N, int H, int D) {
     const size_t E = (size_t)(D + 1) * D;
     const size_t NP = (size_t)(D + 1 + 31) / 32 * 32, KP = (size_t)(D + 15) / 16 * 16;
     // partial states (fp32, rounded up to 16 bytes) + the hi/lo fp16 state pair (counted in floats)
-    return ((size_t)B * H * E * nch + 3) / 4 * 4 + (size_t)B * H * NP * KP;
+    // + the partials' maxima
+    return ((size_t)B * H * E * nch + 3) / 4 * 4 + (size_t)B * H * NP * KP + (size_t)B * H * nch;
 }
 
 hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v, int64_t ld, half_t * out,
@@ -785,6 +841,7 @@ hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v
     float * part = ws;
     f16 * shi = reinterpret_cast<f16 *>(ws + ((size_t)B * H * E * nch + 3) / 4 * 4);
     f16 * slo = shi + (size_t)B * H * NP * KP;
+    float * pmax = reinterpret_cast<float *>(slo + (size_t)B * H * NP * KP);
     const f16 * qq = reinterpret_cast<const f16 *>(q);
     const f16 * kq = reinterpret_cast<const f16 *>(k);
     const f16 * vq = reinterpret_cast<const f16 *>(v);
@@ -793,16 +850,17 @@ hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v
     const int vec_q = (D % 8 == 0 && ld % 8 == 0 && al16(q)) ? 1 : 0;
     const dim3 g1(nch, H, B);
     const int td = (D + 31) / 32;
-    if (td == 1) hipLaunchKernelGGL((la_state_kernel<1>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part);
-    else if (td == 2) hipLaunchKernelGGL((la_state_kernel<2>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part);
-    else if (td == 3) hipLaunchKernelGGL((la_state_kernel<3>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part);
-    else hipLaunchKernelGGL((la_state_kernel<4>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part);
-    hipLaunchKernelGGL(la_reduce_kernel, dim3((NP * KP + 255) / 256, B * H), dim3(256), 0, s, part, nch, D, NP, KP,
-                       shi, slo);
+    if (td == 1) hipLaunchKernelGGL((la_state_kernel<1>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
+    else if (td == 2) hipLaunchKernelGGL((la_state_kernel<2>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
+    else if (td == 3) hipLaunchKernelGGL((la_state_kernel<3>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
+    else hipLaunchKernelGGL((la_state_kernel<4>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
+    hipLaunchKernelGGL(la_reduce_kernel, dim3((NP * KP + 255) / 256, B * H), dim3(256), 0, s, part, pmax, nch, D,
+                       NP, KP, shi, slo);
     const dim3 g3((N + 127) / 128, H, B);
     f16 * oo = reinterpret_cast<f16 *>(out);
 #define SANA_LA_APPLY(nt, ks)                                                                                     \
-    hipLaunchKernelGGL((la_apply_kernel<nt, ks>), g3, dim3(256), 0, s, qq, ld, shi, slo, oo, ldo, N, H, D, vec_q)
+    hipLaunchKernelGGL((la_apply_kernel<nt, ks>), g3, dim3(256), 0, s, qq, ld, shi, slo, pmax, nch, oo, ldo, N, H, \
+                       D, vec_q)
     // NT = ceil((D + 1) / 32) in 1..4, KS = ceil(D / 16) in 1..7
     if (NT == 1) {
         if (KS == 1) SANA_LA_APPLY(1, 1); else SANA_LA_APPLY(1, 2);

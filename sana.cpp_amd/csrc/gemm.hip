@@ -485,6 +485,12 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
         case 15: return launch<128, 128, 2, 2, 4, 1>(p, s);
         case 16: return launch<128, 128, 2, 2, 4, 2>(p, s);
         case 17: return launch<128, 64, 2, 2, 4, 1>(p, s);
+        case 18: return launch<128, 128, 2, 4, 2, 1>(p, s);
+        case 19: return launch<128, 128, 4, 2, 2, 1>(p, s);
+        case 22: return launch<256, 128, 4, 2, 2, 1>(p, s);
+        case 23: return launch<128, 256, 2, 4, 2, 1>(p, s);
+        case 24: return launch<128, 128, 2, 4, 2, 0>(p, s);
+        case 25: return launch<64, 64, 2, 2, 3, 1>(p, s);
         default: break;
     }
     // Tile choice from measured sweeps on MI355X: grids of <= 160 128x128

@@ -158,6 +158,30 @@ def test_linear_attention(L, B, N, H, D):
     assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
 
 
+@pytest.mark.parametrize("N,D,kscale,vmean,vscale", [(16384, 32, 4.0, 6.0, 1.0), (16384, 72, 4.0, 6.0, 1.0),
+                                                    (64, 32, 1e-3, 0.0, 1e-3), (64, 72, 1e-3, 0.0, 1e-3)],
+                         ids=["big32", "big72", "tiny32", "tiny72"])
+def test_linear_attention_state_range(L, N, D, kscale, vmean, vscale):
+    # |S| = |sum_t relu(k) v| ~ N * 3.2 * 6 = 3e5 (past fp16's 65504) or ~1e-5
+    # (fp16 subnormal): the state's power-of-two scaling keeps both exact
+    B, H = 1, 2
+    rng = np.random.default_rng(N + D)
+    C = H * D
+    q = f16(rng.standard_normal((B, N, C)))
+    k = f16(np.abs(rng.standard_normal((B, N, C))) * kscale)
+    v = f16(rng.standard_normal((B, N, C)) * vscale + vmean)
+    ref = O.linear_attention(q, k, v, H)
+    ws = torch.empty(L.lib().sana_hip_linear_attention_workspace(B, N, H, D) // 4 + 1, device="cuda",
+                     dtype=torch.float32)
+    dq, dk, dv = dev(q, torch.float16), dev(k, torch.float16), dev(v, torch.float16)
+    out = torch.empty((B * N, C), device="cuda", dtype=torch.float16)
+    L.check(L.lib().sana_hip_linear_attention(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), C, out.data_ptr(), C, B,
+                                              N, H, D, ws.data_ptr(), stream()))
+    got = host(out).reshape(B, N, C)
+    assert np.isfinite(got).all()
+    assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
+
+
 def test_linear_attention_negative_query_gives_zero(L):
     # relu(q) == 0 for a whole head row -> numerator 0, denominator 1e-15 -> exactly 0
     B, N, H, D = 1, 64, 2, 32
