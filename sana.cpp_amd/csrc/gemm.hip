@@ -55,6 +55,9 @@ SANA_DEV void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// s_waitcnt lgkmcnt(0): every LDS read of this wave has returned.
+SANA_DEV void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+
 template <int BM, int BN, int WM, int WN, int STAGES>
 struct Cfg {
     static constexpr int NW = WM * WN;
@@ -66,8 +69,13 @@ struct Cfg {
     static constexpr int A_LOADS = BM / 8 / NW, B_LOADS = BN / 8 / NW;  // wave instructions per stage
     static constexpr int LOADS = A_LOADS + B_LOADS;
     static constexpr int CPAD = 4;                                      // fp32 epilogue row padding
-    static constexpr int EPI_BYTES = BM * (BN + CPAD) * 4;
-    static constexpr int LDS_BYTES = (STAGES * STAGE_BYTES > EPI_BYTES) ? STAGES * STAGE_BYTES : EPI_BYTES;
+    // The fp32 epilogue tile is staged in LDS: whole when it fits in the operand
+    // ring or in 80 KB (two workgroups per CU), else one wave row (WTM rows) per pass.
+    static constexpr int RING_BYTES = STAGES * STAGE_BYTES;
+    static constexpr int EPI_ROWS =
+        (BM * (BN + CPAD) * 4 <= (RING_BYTES > 80 * 1024 ? RING_BYTES : 80 * 1024)) ? BM : WTM;
+    static constexpr int EPI_BYTES = EPI_ROWS * (BN + CPAD) * 4;
+    static constexpr int LDS_BYTES = (RING_BYTES > EPI_BYTES) ? RING_BYTES : EPI_BYTES;
     static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows must split into 8-row wave loads");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
     static_assert(LOADS * STAGES < 64, "vmcnt range");
@@ -158,7 +166,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
     // boundary (wait for the next tile's DMA, barrier, refill the freed stage)
     // is placed after the last step's MFMAs are issued, so it overlaps them.
     constexpr int NS = kBK / 16;               // MFMA k-steps per tile
-    constexpr int NB = SCHED == 1 ? NS : 2;    // fragment buffers
+    constexpr int NB = (SCHED == 1 || SCHED == 3) ? NS : 2;    // fragment buffers
     f16x8 af[NB][G::TM], bf[NB][G::TN];
     auto load_frags = [&](int stage, int s, int buf) {
         const unsigned char * sa = smem + stage * G::STAGE_BYTES;
@@ -189,7 +197,32 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
     wait_stages<G::LOADS, STAGES>(min(STAGES - 1, KT - 1));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (SCHED == 1) {
+    if constexpr (SCHED == 3) {
+        // Early stage release: all fragments of tile kt are read into registers,
+        // a barrier confirms every wave is done with the stage, and the stage is
+        // refilled with tile kt+STAGES before the tile's MFMAs run.  With two
+        // stages, two tiles of DMA are in flight during the MFMAs instead of one,
+        // which hides the longer latency of weights that come from HBM.
+        for (int kt = 0; kt < KT; ++kt) {
+            const int st = kt % STAGES;
+            if (kt > 0) {
+                __builtin_amdgcn_sched_barrier(0);
+                wait_stages<G::LOADS, STAGES>(min(STAGES - 1, KT - 1 - kt));
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int s = 0; s < NS; ++s) load_frags(st, s, s);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_lgkmcnt0();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if (kt + STAGES < KT) issue(kt + STAGES, st);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) mfmas(s);
+        }
+    } else if constexpr (SCHED == 1) {
         // every fragment of the tile is requested right after the barrier; the
         // MFMAs of step s wait only for the reads of steps <= s (in-order lgkmcnt)
         for (int kt = 0; kt < KT; ++kt) {
@@ -261,61 +294,25 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
             }
         return;
     } else {
-        __syncthreads();  // every wave is done reading the operand ring
         float * ct = reinterpret_cast<float *>(smem);
         constexpr int LDC = BN + G::CPAD;
-#pragma unroll
-        for (int i = 0; i < G::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < G::TN; ++j) {
-                const int c = wn * G::WTN + j * 32 + (lane & 31);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int rr = wm * G::WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    ct[rr * LDC + c] = acc[i][j][r];
-                }
-            }
-        __syncthreads();
-        if constexpr (MODE == kGemmQKV) {
-            // k and v sections: items (column, 8-row octet), consecutive lanes on
-            // consecutive octets of one column, so each column's 16-byte stores
-            // form one contiguous token run.  Rows of an octet share a batch
-            // (qkv_n % 8 == 0).  The q section is handled below as a plain store.
-            constexpr int OCT = BM / 8;
-            const int C3 = p.qkv_c;
-            for (int item = tid; item < BN * OCT; item += G::NT) {
-                const int oct = item % OCT, cl = item / OCT;
-                const int col = n0 + cl, row0 = m0 + oct * 8;
-                if (col >= p.N || row0 >= p.M || col < C3) continue;
-                const bool is_k = col < 2 * C3;
-                const int ch = col - (is_k ? C3 : 2 * C3);
-                const float bcol = p.bias ? p.bias[col] : 0.0f;
-                f16x8 h;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    float v = ct[(oct * 8 + j) * LDC + cl] + bcol;
-                    if (is_k) v = fmaxf(v, 0.0f);
-                    h[j] = (f16)v;
-                }
-                const int b = row0 / p.qkv_n, t0 = row0 - b * p.qkv_n;
-                f16 * dst = reinterpret_cast<f16 *>(is_k ? p.kt16 : p.vt16);
-                *reinterpret_cast<f16x8 *>(dst + ((int64_t)b * C3 + ch) * p.qkv_n + t0) = h;
-            }
-        }
+        constexpr int ER = G::EPI_ROWS;  // tile rows staged per pass
         // Each thread owns one 8-column chunk of the tile for all its rows, so
-        // the bias is fetched once; rows step by NT / CPR.
+        // the bias is fetched once; rows step by NT / CPR (threads past the
+        // last whole row of chunks stay idle).
         constexpr int CPR = BN / 8;
-        static_assert(G::NT % CPR == 0, "epilogue chunk mapping");
+        static_assert(G::NT >= CPR, "epilogue chunk mapping");
         const int c8 = (tid % CPR) * 8;
         const int col = n0 + c8;
         const int nc = min(8, p.N - col);
-        if (nc <= 0) return;
-        if constexpr (MODE == kGemmQKV) {
-            if (col >= p.qkv_c) return;  // k / v columns were stored above
-        }
+        bool active = nc > 0 && tid < (G::NT / CPR) * CPR;
+        if constexpr (MODE == kGemmQKV) active = active && col < p.qkv_c;  // k / v columns: item loop
         const bool vec8 = p.vec && nc == 8;
         float bv[8];
-        if (p.bias && vec8) {
+        if (!active) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bv[e] = 0.0f;
+        } else if (p.bias && vec8) {
             const float4 b0 = *reinterpret_cast<const float4 *>(p.bias + col);
             const float4 b1 = *reinterpret_cast<const float4 *>(p.bias + col + 4);
             bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
@@ -324,85 +321,131 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) bv[e] = (p.bias && e < nc) ? p.bias[col + e] : 0.0f;
         }
-        for (int rr = tid / CPR; rr < BM; rr += G::NT / CPR) {
-            const int row = m0 + rr;
-            if (row >= p.M) break;
-            const float4 v0 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8]);
-            const float4 v1 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8 + 4]);
-            float v[8] = {v0.x + bv[0], v0.y + bv[1], v0.z + bv[2], v0.w + bv[3],
-                          v1.x + bv[4], v1.y + bv[5], v1.z + bv[6], v1.w + bv[7]};
-            if constexpr (MODE == kGemmStore || MODE == kGemmQKV) {
+        for (int pass = 0; pass < BM / ER; ++pass) {
+            __syncthreads();  // the operand ring (pass 0) or the previous pass's rows are free
+            if (ER == BM || wm == pass) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    if constexpr (ACT == kActSilu) v[e] = silu_f(v[e]);
-                    if constexpr (ACT == kActGelu) v[e] = gelu_tanh_f(v[e]);
-                    if constexpr (MODE == kGemmQKV) v[e] = fmaxf(v[e], 0.0f);
+                for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < G::TN; ++j) {
+                        const int c = wn * G::WTN + j * 32 + (lane & 31);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int rr = (wm * G::WTM - pass * ER) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                            ct[rr * LDC + c] = acc[i][j][r];
+                        }
+                    }
+            }
+            __syncthreads();
+            if constexpr (MODE == kGemmQKV) {
+                // k and v sections: items (column, 8-row octet), consecutive lanes on
+                // consecutive octets of one column, so each column's 16-byte stores
+                // form one contiguous token run.  Rows of an octet share a batch
+                // (qkv_n % 8 == 0).  The q section is handled below as a plain store.
+                constexpr int OCT = ER / 8;
+                const int C3 = p.qkv_c;
+                for (int item = tid; item < BN * OCT; item += G::NT) {
+                    const int oct = item % OCT, cl = item / OCT;
+                    const int col = n0 + cl, row0 = m0 + pass * ER + oct * 8;
+                    if (col >= p.N || row0 >= p.M || col < C3) continue;
+                    const bool is_k = col < 2 * C3;
+                    const int ch = col - (is_k ? C3 : 2 * C3);
+                    const float bcol = p.bias ? p.bias[col] : 0.0f;
+                    f16x8 h;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        float v = ct[(oct * 8 + j) * LDC + cl] + bcol;
+                        if (is_k) v = fmaxf(v, 0.0f);
+                        h[j] = (f16)v;
+                    }
+                    const int b = row0 / p.qkv_n, t0 = row0 - b * p.qkv_n;
+                    f16 * dst = reinterpret_cast<f16 *>(is_k ? p.kt16 : p.vt16);
+                    *reinterpret_cast<f16x8 *>(dst + ((int64_t)b * C3 + ch) * p.qkv_n + t0) = h;
                 }
-                if (vec8) {
-                    if (p.out16) {
-                        f16x8 h;
+            }
+            if (active) {
+                for (int rr = tid / CPR; rr < ER; rr += G::NT / CPR) {
+                    const int row = m0 + pass * ER + rr;
+                    if (row >= p.M) break;
+                    const float4 v0 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8]);
+                    const float4 v1 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8 + 4]);
+                    float v[8] = {v0.x + bv[0], v0.y + bv[1], v0.z + bv[2], v0.w + bv[3],
+                                  v1.x + bv[4], v1.y + bv[5], v1.z + bv[6], v1.w + bv[7]};
+                    if constexpr (MODE == kGemmStore || MODE == kGemmQKV) {
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) h[e] = (f16)v[e];
-                        *reinterpret_cast<f16x8 *>(reinterpret_cast<f16 *>(p.out16) + (int64_t)row * p.ldo16 + col) = h;
-                    }
-                    if (p.out32) {
-                        float * o = p.out32 + (int64_t)row * p.ldo32 + col;
-                        *reinterpret_cast<float4 *>(o) = make_float4(v[0], v[1], v[2], v[3]);
-                        *reinterpret_cast<float4 *>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
-                    }
-                } else {
-                    for (int e = 0; e < nc; ++e) {
-                        if (p.out16) reinterpret_cast<f16 *>(p.out16)[(int64_t)row * p.ldo16 + col + e] = (f16)v[e];
-                        if (p.out32) p.out32[(int64_t)row * p.ldo32 + col + e] = v[e];
-                    }
-                }
-            } else {  // kGemmResidual: x += gate * (acc + bias)
-                const int b = row / p.rows_per_batch;
-                float g[8];
-                if (p.gate_a && vec8) {
-                    const float * ga = p.gate_a + (int64_t)b * p.gate_stride + col;
-                    const float4 g0 = *reinterpret_cast<const float4 *>(ga);
-                    const float4 g1 = *reinterpret_cast<const float4 *>(ga + 4);
-                    g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
-                    g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
-                    if (p.gate_t) {
-                        const float4 t0 = *reinterpret_cast<const float4 *>(p.gate_t + col);
-                        const float4 t1 = *reinterpret_cast<const float4 *>(p.gate_t + col + 4);
-                        g[0] += t0.x; g[1] += t0.y; g[2] += t0.z; g[3] += t0.w;
-                        g[4] += t1.x; g[5] += t1.y; g[6] += t1.z; g[7] += t1.w;
-                    }
-                } else {
+                        for (int e = 0; e < 8; ++e) {
+                            if constexpr (ACT == kActSilu) v[e] = silu_f(v[e]);
+                            if constexpr (ACT == kActGelu) v[e] = gelu_tanh_f(v[e]);
+                            if constexpr (MODE == kGemmQKV) v[e] = fmaxf(v[e], 0.0f);
+                        }
+                        if (vec8) {
+                            if (p.out16) {
+                                f16x8 h;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        g[e] = 1.0f;
-                        if (p.gate_a && e < nc) {
-                            g[e] = p.gate_a[(int64_t)b * p.gate_stride + col + e];
-                            if (p.gate_t) g[e] += p.gate_t[col + e];
+                                for (int e = 0; e < 8; ++e) h[e] = (f16)v[e];
+                                *reinterpret_cast<f16x8 *>(reinterpret_cast<f16 *>(p.out16) + (int64_t)row * p.ldo16 + col) = h;
+                            }
+                            if (p.out32) {
+                                float * o = p.out32 + (int64_t)row * p.ldo32 + col;
+                                *reinterpret_cast<float4 *>(o) = make_float4(v[0], v[1], v[2], v[3]);
+                                *reinterpret_cast<float4 *>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+                            }
+                        } else {
+                            for (int e = 0; e < nc; ++e) {
+                                if (p.out16) reinterpret_cast<f16 *>(p.out16)[(int64_t)row * p.ldo16 + col + e] = (f16)v[e];
+                                if (p.out32) p.out32[(int64_t)row * p.ldo32 + col + e] = v[e];
+                            }
+                        }
+                    } else {  // kGemmResidual: x += gate * (acc + bias)
+                        const int b = row / p.rows_per_batch;
+                        float g[8];
+                        if (p.gate_a && vec8) {
+                            const float * ga = p.gate_a + (int64_t)b * p.gate_stride + col;
+                            const float4 g0 = *reinterpret_cast<const float4 *>(ga);
+                            const float4 g1 = *reinterpret_cast<const float4 *>(ga + 4);
+                            g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w;
+                            g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+                            if (p.gate_t) {
+                                const float4 t0 = *reinterpret_cast<const float4 *>(p.gate_t + col);
+                                const float4 t1 = *reinterpret_cast<const float4 *>(p.gate_t + col + 4);
+                                g[0] += t0.x; g[1] += t0.y; g[2] += t0.z; g[3] += t0.w;
+                                g[4] += t1.x; g[5] += t1.y; g[6] += t1.z; g[7] += t1.w;
+                            }
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {
+                                g[e] = 1.0f;
+                                if (p.gate_a && e < nc) {
+                                    g[e] = p.gate_a[(int64_t)b * p.gate_stride + col + e];
+                                    if (p.gate_t) g[e] += p.gate_t[col + e];
+                                }
+                            }
+                        }
+                        float * xr = p.out32 + (int64_t)row * p.ldo32 + col;
+                        if (vec8) {
+                            const float4 x0 = *reinterpret_cast<const float4 *>(xr);
+                            const float4 x1 = *reinterpret_cast<const float4 *>(xr + 4);
+                            float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) x[e] = x[e] + g[e] * v[e];
+                            *reinterpret_cast<float4 *>(xr) = make_float4(x[0], x[1], x[2], x[3]);
+                            *reinterpret_cast<float4 *>(xr + 4) = make_float4(x[4], x[5], x[6], x[7]);
+                            if (p.out16) {
+                                f16x8 h;
+#pragma unroll
+                                for (int e = 0; e < 8; ++e) h[e] = (f16)x[e];
+                                *reinterpret_cast<f16x8 *>(reinterpret_cast<f16 *>(p.out16) + (int64_t)row * p.ldo16 + col) = h;
+                            }
+                        } else {
+                            for (int e = 0; e < nc; ++e) {
+                                const float nx = xr[e] + g[e] * v[e];
+                                xr[e] = nx;
+                                if (p.out16) reinterpret_cast<f16 *>(p.out16)[(int64_t)row * p.ldo16 + col + e] = (f16)nx;
+                            }
                         }
                     }
                 }
-                float * xr = p.out32 + (int64_t)row * p.ldo32 + col;
-                if (vec8) {
-                    const float4 x0 = *reinterpret_cast<const float4 *>(xr);
-                    const float4 x1 = *reinterpret_cast<const float4 *>(xr + 4);
-                    float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) x[e] = x[e] + g[e] * v[e];
-                    *reinterpret_cast<float4 *>(xr) = make_float4(x[0], x[1], x[2], x[3]);
-                    *reinterpret_cast<float4 *>(xr + 4) = make_float4(x[4], x[5], x[6], x[7]);
-                    if (p.out16) {
-                        f16x8 h;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) h[e] = (f16)x[e];
-                        *reinterpret_cast<f16x8 *>(reinterpret_cast<f16 *>(p.out16) + (int64_t)row * p.ldo16 + col) = h;
-                    }
-                } else {
-                    for (int e = 0; e < nc; ++e) {
-                        const float nx = xr[e] + g[e] * v[e];
-                        xr[e] = nx;
-                        if (p.out16) reinterpret_cast<f16 *>(p.out16)[(int64_t)row * p.ldo16 + col + e] = (f16)nx;
-                    }
-                }
+
             }
         }
     }
@@ -491,13 +534,28 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
         case 23: return launch<128, 256, 2, 4, 2, 1>(p, s);
         case 24: return launch<128, 128, 2, 4, 2, 0>(p, s);
         case 25: return launch<64, 64, 2, 2, 3, 1>(p, s);
+        case 26: return launch<128, 192, 2, 2, 2, 3>(p, s);
+        case 27: return launch<128, 64, 2, 2, 2, 3>(p, s);
+        case 28: return launch<64, 64, 2, 2, 2, 3>(p, s);
+        case 29: return launch<128, 128, 2, 2, 2, 3>(p, s);
         default: break;
     }
-    // Tile choice from measured sweeps on MI355X: grids of <= 160 128x128
-    // tiles use 64x64 tiles to occupy the 256 CUs; otherwise 128x128 tiles with
-    // two stages keep two workgroups resident per CU.
-    const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
-    if (t128 <= 160) return launch<64, 64, 2, 2, 2, 1>(p, s);
+    // Tile choice from sweeps on MI355X with cold weights (each GEMM's weights
+    // come from HBM, as in the 28-block forward).  Every CU pulls at most
+    // ~55 GB/s from L2, so larger tiles (fewer operand bytes per flop) win as
+    // long as the grid still covers the 256 CUs:
+    //  * grids of <= 160 128x128 tiles: 128x64 tiles with early stage release
+    //    when that makes >= 256 tiles, else 64x64 tiles;
+    //  * plain stores whose N splits into 192-wide tiles with >= 256 tiles:
+    //    128x192 with early stage release (two workgroups per CU);
+    //  * otherwise 128x128 tiles with two stages, two workgroups per CU.
+    const int64_t tm128 = (p.M + 127) / 128;
+    const int64_t t128 = tm128 * ((p.N + 127) / 128);
+    if (t128 <= 160) {
+        if (tm128 * ((p.N + 63) / 64) >= 256) return launch<128, 64, 2, 2, 2, 3>(p, s);
+        return launch<64, 64, 2, 2, 2, 1>(p, s);
+    }
+    if (p.mode == kGemmStore && p.N % 192 == 0 && tm128 * (p.N / 192) >= 256) return launch<128, 192, 2, 2, 2, 3>(p, s);
     return launch<128, 128, 2, 2, 2, 1>(p, s);
 }
 
