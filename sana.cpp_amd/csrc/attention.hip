@@ -1,4 +1,5 @@
 // K3 ReLU linear attention and K4 softmax cross-attention.
+#include <algorithm>
 #include <cmath>
 
 #include "hip_common.h"
@@ -287,23 +288,32 @@ __global__ __launch_bounds__(256) void la_apply_kernel(const f16 * __restrict__ 
 //   3. Wave w applies it to its tokens transposed, O^T[r][t] = [S | ksum] .
 //      relu(q)^T, so each lane holds four consecutive head dims of one token
 //      (8-byte stores); the denominator is row 0 of the ksum tile.
+// With `splits` > 1, `splits` workgroups share one (b, h): each builds the
+// whole (small) state and applies it to its own 1/splits of the tokens, so
+// B*H*splits workgroups cover the CUs when B*H alone does not.
 // out[t][r] = O^T[r][t] / (den[t] + 2^k 1e-15), as src/transformer_ops.cpp:496-537.
 constexpr int kLfWaves = 8;
 constexpr int kLfSrow = 40;  // halves per LDS row of the hi/lo state (80 B rows)
 
 __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __restrict__ q, int64_t ldq,
                                                         const f16 * __restrict__ kt, const f16 * __restrict__ vt,
-                                                        f16 * __restrict__ out, int64_t ldo, int N, int H) {
+                                                        f16 * __restrict__ out, int64_t ldo, int N, int H,
+                                                        int splits) {
     __shared__ float part[kLfWaves][33][32];                       // per-wave S^T (rows d) + ksum row
     __shared__ __attribute__((aligned(16))) f16 sh[2][2][32][kLfSrow];  // [S|ksum tile][hi|lo][row][d]
     __shared__ __attribute__((aligned(16))) f16 ost[kLfWaves][32][kLfSrow];  // per-wave output staging [token][dim]
     __shared__ float pmax[kLfWaves];                                   // max |entry| of each wave's partial
-    const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
+    const int bh = blockIdx.x / splits, sp = blockIdx.x - bh * splits, b = bh / H, h = bh - b * H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5;
     const f16 * K = kt + ((int64_t)b * H + h) * 32 * N;  // rows d = 0..31, N tokens each
     const f16 * V = vt + ((int64_t)b * H + h) * 32 * N;
-    const int span = (N / kLfWaves + 15) / 16 * 16;      // tokens per wave, multiple of 16
+    const int span = (N / kLfWaves + 15) / 16 * 16;      // state tokens per wave, multiple of 16
     const int tb = w * span, te = min(N, tb + span);
+    // apply range [ta, tz) of this wave within the workgroup's token share
+    const int per_split = (N + splits - 1) / splits;
+    const int T0 = min(N, sp * per_split), T1 = min(N, T0 + per_split);
+    const int span3 = ((T1 - T0 + kLfWaves - 1) / kLfWaves + 15) / 16 * 16;
+    const int ta = min(T1, T0 + w * span3), tz = min(T1, ta + span3);
 
     // query fragments of the first kQpf apply steps are independent of the
     // state: issue them before anything else
@@ -312,7 +322,7 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
     f16x8 qpf[kQpf][2];
 #pragma unroll
     for (int j = 0; j < kQpf; ++j) {
-        const int tq = min(tb + 32 * j + (lane & 31), N - 1);
+        const int tq = min(ta + 32 * j + (lane & 31), N - 1);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) qpf[j][kk] = *reinterpret_cast<const f16x8 *>(qbase + (int64_t)tq * ldq + kk * 16);
     }
@@ -413,7 +423,7 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
             const int tl = half * 16 + (lane >> 2), c8 = (lane & 3) * 8;
             const f16x8 v8 = *reinterpret_cast<const f16x8 *>(&ost[w][tl][c8]);
             const int t = t0 + tl;
-            if (t < te) *reinterpret_cast<f16x8 *>(out + ((int64_t)b * N + t) * ldo + (int64_t)h * 32 + c8) = v8;
+            if (t < tz) *reinterpret_cast<f16x8 *>(out + ((int64_t)b * N + t) * ldo + (int64_t)h * 32 + c8) = v8;
         }
         __builtin_amdgcn_wave_barrier();
     };
@@ -422,7 +432,7 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) qf[kk] = *reinterpret_cast<const f16x8 *>(qbase + (int64_t)tq * ldq + kk * 16);
     };
-    for (int j = 0, t0 = tb; t0 < te; j += 2, t0 += 64) {
+    for (int j = 0, t0 = ta; t0 < tz; j += 2, t0 += 64) {
         f16x8 qa[2], qb[2];
         if (j + 1 < kQpf) {
 #pragma unroll
@@ -451,7 +461,7 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
                 db = mfma_32x32x16(sa[1][hl][kk], qb[kk], db);
             }
         apply_store(t0, oa, da);
-        if (t0 + 32 < te) apply_store(t0 + 32, ob, db);
+        if (t0 + 32 < tz) apply_store(t0 + 32, ob, db);
     }
 }
 
@@ -812,9 +822,11 @@ hipError_t linear_attention_fused(const half_t * q, int64_t ldq, const half_t * 
         ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kt) | reinterpret_cast<uintptr_t>(vt)) & 15) ||
         (reinterpret_cast<uintptr_t>(out) & 15))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(la_fused_kernel, dim3((unsigned)(B * H)), dim3(64 * kLfWaves), 0, s,
+    // enough workgroups for the 256 CUs: (b, h) pairs times token splits
+    const int splits = (int)std::max<int64_t>(1, std::min<int64_t>(8, 256 / ((int64_t)B * H)));
+    hipLaunchKernelGGL(la_fused_kernel, dim3((unsigned)(B * H * splits)), dim3(64 * kLfWaves), 0, s,
                        reinterpret_cast<const f16 *>(q), ldq, reinterpret_cast<const f16 *>(kt),
-                       reinterpret_cast<const f16 *>(vt), reinterpret_cast<f16 *>(out), ldo, N, H);
+                       reinterpret_cast<const f16 *>(vt), reinterpret_cast<f16 *>(out), ldo, N, H, splits);
     return hipGetLastError();
 }
 

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(64) void dwglu_row_kernel(const f16 * __restrict__ 
             for (int e = 0; e < 8; ++e) {
                 const float d = ad[e] + bd[e];
                 const float gt = ag[e] + bg[e];
-                o[e] = (f16)(d * silu_f(gt));
+                o[e] = (f16)(d * silu_fast(gt));
             }
             *reinterpret_cast<f16x8 *>(ob + ((int64_t)y * Ww + xx) * ldo) = o;
         }

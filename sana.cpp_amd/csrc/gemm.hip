@@ -374,7 +374,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                     if constexpr (MODE == kGemmStore || MODE == kGemmQKV) {
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
-                            if constexpr (ACT == kActSilu) v[e] = silu_f(v[e]);
+                            if constexpr (ACT == kActSilu) v[e] = silu_fast(v[e]);
                             if constexpr (ACT == kActGelu) v[e] = gelu_tanh_f(v[e]);
                             if constexpr (MODE == kGemmQKV) v[e] = fmaxf(v[e], 0.0f);
                         }

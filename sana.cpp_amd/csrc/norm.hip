@@ -69,6 +69,9 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(const float * __restri
 
 // Same as ln_modulate_kernel for rows whose width and strides are multiples of
 // 4: float4 loads of x and of the modulation rows, 8-byte fp16x4 stores.
+// kMax4 = float4 chunks per lane (C <= 256 * kMax4), so the row and its shift /
+// scale vectors stay in registers.
+template <int kMax4>
 __global__ __launch_bounds__(256) void ln_modulate_vec_kernel(const float * __restrict__ x, int64_t ldx,
                                                               f16 * __restrict__ out, int64_t ldo, int M, int C,
                                                               int rpb, float eps, const float * __restrict__ gamma,
@@ -76,20 +79,31 @@ __global__ __launch_bounds__(256) void ln_modulate_vec_kernel(const float * __re
                                                               const float * __restrict__ mod_a,
                                                               const float * __restrict__ mod_t, int64_t mod_stride,
                                                               int64_t shift_off, int64_t scale_off) {
-    constexpr int kMax4 = kMaxPerLane / 4;  // float4 chunks per lane
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= M) return;
     const int n4 = C >> 2;
     const float4 * xr = reinterpret_cast<const float4 *>(x + (int64_t)row * ldx);
-    float4 v[kMax4];
-    float s = 0.0f;
+    const int b = row / rpb;
+    const float4 * sh4 = reinterpret_cast<const float4 *>(mod_a + (int64_t)b * mod_stride + shift_off);
+    const float4 * sc4 = reinterpret_cast<const float4 *>(mod_a + (int64_t)b * mod_stride + scale_off);
+    // the row and its shift / scale vectors are all requested before the
+    // reductions, so their latencies overlap
+    float4 v[kMax4], shv[kMax4], scv[kMax4];
 #pragma unroll
     for (int i = 0; i < kMax4; ++i) {
         const int c4 = lane + 64 * i;
-        v[i] = c4 < n4 ? xr[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        if (c4 < n4) {
+            v[i] = xr[c4];
+            shv[i] = sh4[c4];
+            scv[i] = sc4[c4];
+        } else {
+            v[i] = shv[i] = scv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
     }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMax4; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     const float mean = wave_sum(s) / (float)C;
     float q = 0.0f;
 #pragma unroll
@@ -100,9 +114,6 @@ __global__ __launch_bounds__(256) void ln_modulate_vec_kernel(const float * __re
         }
     }
     const float inv = 1.0f / sqrtf(wave_sum(q) / (float)C + eps);
-    const int b = row / rpb;
-    const float4 * sh4 = reinterpret_cast<const float4 *>(mod_a + (int64_t)b * mod_stride + shift_off);
-    const float4 * sc4 = reinterpret_cast<const float4 *>(mod_a + (int64_t)b * mod_stride + scale_off);
     const float4 * tsh4 = mod_t ? reinterpret_cast<const float4 *>(mod_t + shift_off) : nullptr;
     const float4 * tsc4 = mod_t ? reinterpret_cast<const float4 *>(mod_t + scale_off) : nullptr;
     f16x4 * orow = reinterpret_cast<f16x4 *>(out + (int64_t)row * ldo);
@@ -119,7 +130,7 @@ __global__ __launch_bounds__(256) void ln_modulate_vec_kernel(const float * __re
                 const float4 bb = reinterpret_cast<const float4 *>(beta)[c4];
                 y[0] += bb.x; y[1] += bb.y; y[2] += bb.z; y[3] += bb.w;
             }
-            float4 sh = sh4[c4], sc = sc4[c4];
+            float4 sh = shv[i], sc = scv[i];
             if (tsh4) {
                 const float4 a = tsh4[c4], d = tsc4[c4];
                 sh.x += a.x; sh.y += a.y; sh.z += a.z; sh.w += a.w;
@@ -397,11 +408,18 @@ hipError_t ln_modulate(const float * x, int64_t ldx, half_t * out, int64_t ldo, 
                      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
                        reinterpret_cast<uintptr_t>(mod_a) | reinterpret_cast<uintptr_t>(mod_t) |
                        reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) & 15) == 0;
-    if (vec)
-        hipLaunchKernelGGL(ln_modulate_vec_kernel, dim3((M + 3) / 4), dim3(256), 0, s, x, ldx,
-                           reinterpret_cast<f16 *>(out), ldo, M, C, rpb, eps, gamma, beta, mod_a, mod_t, mod_stride,
-                           shift_off, scale_off);
-    else
+    if (vec) {
+#define SANA_LN_VEC(n4)                                                                                           \
+    hipLaunchKernelGGL((ln_modulate_vec_kernel<n4>), dim3((M + 3) / 4), dim3(256), 0, s, x, ldx,                   \
+                       reinterpret_cast<f16 *>(out), ldo, M, C, rpb, eps, gamma, beta, mod_a, mod_t, mod_stride,  \
+                       shift_off, scale_off)
+        const int per = (C / 4 + 63) / 64;  // float4 chunks per lane
+        if (per <= 2) SANA_LN_VEC(2);
+        else if (per <= 3) SANA_LN_VEC(3);
+        else if (per <= 5) SANA_LN_VEC(5);
+        else SANA_LN_VEC(kMaxPerLane / 4);
+#undef SANA_LN_VEC
+    } else
         hipLaunchKernelGGL(ln_modulate_kernel, dim3((M + 3) / 4), dim3(256), 0, s, x, ldx,
                            reinterpret_cast<f16 *>(out), ldo, M, C, rpb, eps, gamma, beta, mod_a, mod_t, mod_stride,
                            shift_off, scale_off);
