@@ -186,6 +186,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-calib", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the extra 4096 px forward and 4096-token microbenchmark lines (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for {args.gpus}); "
@@ -268,19 +270,23 @@ def main():
         ms_w, fl_w = d.time_gemm(which, 20)
         per_gemm[nm] = {"us": round(ms_w * 1e3, 2), "tflops": round(fl_w / (ms_w * 1e-3) / 1e12, 1)}
 
-    # 4096 px forward (latent 128x128, 16384 image tokens, same context): context resident
-    lat5 = torch.from_numpy(rng.standard_normal((1, DIMS["latent_channels"], 128, 128), dtype=np.float32)).to(dev)
-    out5 = torch.empty((B, DIMS["latent_channels"], 128, 128), device=dev, dtype=torch.float32)
-    d.forward_device(lat5, tuple(lat5.shape), TIMESTEP, out5, sp)
-    torch.cuda.synchronize()
-    ev0.record(stream)
-    for _ in range(3):
+    extras = {}
+    if not args.no_extras:
+        # 4096 px forward (latent 128x128, 16384 image tokens, same context): context resident
+        lat5 = torch.from_numpy(rng.standard_normal((1, DIMS["latent_channels"], 128, 128), dtype=np.float32)).to(dev)
+        out5 = torch.empty((B, DIMS["latent_channels"], 128, 128), device=dev, dtype=torch.float32)
         d.forward_device(lat5, tuple(lat5.shape), TIMESTEP, out5, sp)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    c5_ms = ev0.elapsed_time(ev1) / 3
-    c5_flops = forward_flops(B, 128 * 128, L, with_context=False)
-    c4 = microbench_4096(sana_dit, torch, dev, stream)
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for _ in range(3):
+            d.forward_device(lat5, tuple(lat5.shape), TIMESTEP, out5, sp)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        c5_ms = ev0.elapsed_time(ev1) / 3
+        c5_flops = forward_flops(B, 128 * 128, L, with_context=False)
+        extras["forward_4096px"] = {"ms": round(c5_ms, 3), "tflops": round(c5_flops / (c5_ms * 1e-3) / 1e12, 1),
+                                    "tokens": 128 * 128, "note": "28 blocks, CFG batch 2, context resident"}
+        extras["microbench_4096_tokens"] = microbench_4096(sana_dit, torch, dev, stream)
 
     step_flops = forward_flops(B, N, L, with_context=True)
     fwd_flops = forward_flops(B, N, L, with_context=False)
@@ -308,14 +314,13 @@ def main():
         "forward_gflop_context_resident": round(fwd_flops / 1e9, 2),
         "gemms": per_gemm,
         "roofline": {"bound": "mfma",
-                     "kernel": "gemm_kernel (128x128 tile, bias+SiLU epilogue): Mix-FFN inverted 2048x5760x1152",
+                     "kernel": "gemm_kernel (128x192 tiles, early stage release, bias+SiLU epilogue): "
+                               "Mix-FFN inverted 2048x5760x1152",
                      "achieved": round(gemm_tflops, 1), "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tflops / PEAK_MFMA_TFLOPS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes": GEMM_BYTES, "avg_us": round(gemm_ms * 1e3, 2)},
         "cpu_baseline": cpu,
-        "forward_4096px": {"ms": round(c5_ms, 3), "tflops": round(c5_flops / (c5_ms * 1e-3) / 1e12, 1),
-                           "tokens": 128 * 128, "note": "28 blocks, CFG batch 2, context resident"},
-        "microbench_4096_tokens": c4,
+        **extras,
     }
     d.close()
     print(json.dumps(res), flush=True)

@@ -237,7 +237,7 @@ def test_cross_attention(L, B, N, Lk, H, D, masked):
     assert rel_l2(got, ref) < 2e-3, rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("B,S,F", [(2, 32, 2880), (1, 16, 64), (1, 3, 5), (2, 1, 8)])
+@pytest.mark.parametrize("B,S,F", [(2, 32, 2880), (2, 64, 2880), (1, 37, 40), (1, 16, 64), (1, 3, 5), (2, 1, 8)])
 def test_dwconv_glu(L, B, S, F):
     rng = np.random.default_rng(S + F)
     E = 2 * F
