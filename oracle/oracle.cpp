@@ -5,6 +5,7 @@
 // re-associated and results match the reference bit for bit).
 #include "oracle.h"
 #include "model_spec.h"
+#include "vae_spec.h"
 
 #include <algorithm>
 #include <cmath>
@@ -581,6 +582,351 @@ void model_forward(const oracle_model & m, const float * latent, size_t Bl, size
             for (size_t c = 0; c < Cl; ++c) np_out[(b * Cl + c) * N + s] = pr[(b * N + s) * Cl + c];
 }
 
+
+// ================================================================ VAE decoder
+// NCHW fp32, as the reference's src/vae.cpp and src/vae_ops.cpp (Linux #else
+// branches).  Every output element sees the reference's sequence of fp32
+// roundings; zero-padding taps are skipped, which leaves every sum unchanged
+// (adding a +-0 product to a running sum that starts at +0 or at a bias never
+// changes it).
+
+// 3x3 same conv.  conv2d_3x3_same_dispatch (src/vae_ops.cpp:196-222) picks
+// im2col + gemm_row_major (:18-95: sum from 0 over k = (ic, ky, kx), bias added
+// after) when Cin*9*H*W <= 9e8, else tap accumulation (:104-194: bias first,
+// taps (ky, kx) outer, input channels inner).
+void vae_conv3x3(const float * in, const float * w, const float * bias, float * out, size_t B, size_t Cin,
+                 size_t Cout, size_t Hh, size_t Ww, int order = -1) {
+    const size_t S = Hh * Ww;
+    const bool tap_order = order < 0 ? Cin * 9 * S > 900000000ULL : order == 1;
+    parallel_rows(B * Cout, [&](size_t r0, size_t r1) {
+        for (size_t r = r0; r < r1; ++r) {
+            const size_t b = r / Cout, oc = r % Cout;
+            float * o = out + r * S;
+            const float * xb = in + b * Cin * S;
+            const float init = (tap_order && bias) ? bias[oc] : 0.0f;
+            for (size_t i = 0; i < S; ++i) o[i] = init;
+            auto add_tap = [&](size_t ic, int ky, int kx) {
+                const float a = w[((oc * Cin + ic) * 3 + ky) * 3 + kx];
+                const float * xc = xb + ic * S;
+                for (size_t y = 0; y < Hh; ++y) {
+                    const long iy = static_cast<long>(y) + ky - 1;
+                    if (iy < 0 || iy >= static_cast<long>(Hh)) continue;
+                    const size_t x0 = kx == 0 ? 1 : 0, x1 = kx == 2 ? Ww - 1 : Ww;
+                    const float * src = xc + iy * Ww + (kx - 1);
+                    float * dst = o + y * Ww;
+                    for (size_t x = x0; x < x1; ++x) dst[x] += a * src[x];
+                }
+            };
+            if (!tap_order) {
+                for (size_t ic = 0; ic < Cin; ++ic)
+                    for (int ky = 0; ky < 3; ++ky)
+                        for (int kx = 0; kx < 3; ++kx) add_tap(ic, ky, kx);
+                if (bias)
+                    for (size_t i = 0; i < S; ++i) o[i] += bias[oc];
+            } else {
+                for (int ky = 0; ky < 3; ++ky)
+                    for (int kx = 0; kx < 3; ++kx)
+                        for (size_t ic = 0; ic < Cin; ++ic) add_tap(ic, ky, kx);
+            }
+        }
+    });
+}
+
+// conv2d_1x1 (src/common_ops.cpp:247-309, conv2d_1x1_blocked): bias first, then
+// input channels in order.
+void vae_conv1x1(const float * in, const float * w, const float * bias, float * out, size_t B, size_t Cin,
+                 size_t Cout, size_t S) {
+    parallel_rows(B * Cout, [&](size_t r0, size_t r1) {
+        for (size_t r = r0; r < r1; ++r) {
+            const size_t b = r / Cout, oc = r % Cout;
+            float * o = out + r * S;
+            const float init = bias ? bias[oc] : 0.0f;
+            for (size_t i = 0; i < S; ++i) o[i] = init;
+            for (size_t ic = 0; ic < Cin; ++ic) {
+                const float a = w[oc * Cin + ic];
+                const float * x = in + (b * Cin + ic) * S;
+                for (size_t i = 0; i < S; ++i) o[i] += a * x[i];
+            }
+        }
+    });
+}
+
+// grouped_conv2d_1x1 (src/vae_ops.cpp:243-300): per group gemm_row_major from 0.
+void vae_grouped1x1(const float * in, const float * w, float * out, size_t B, size_t Cin, size_t Cout,
+                    size_t groups, size_t S) {
+    const size_t ipg = Cin / groups, opg = Cout / groups;
+    parallel_rows(B * Cout, [&](size_t r0, size_t r1) {
+        for (size_t r = r0; r < r1; ++r) {
+            const size_t b = r / Cout, oc = r % Cout, g = oc / opg;
+            float * o = out + r * S;
+            for (size_t i = 0; i < S; ++i) o[i] = 0.0f;
+            for (size_t k = 0; k < ipg; ++k) {
+                const float a = w[oc * ipg + k];
+                const float * x = in + (b * Cin + g * ipg + k) * S;
+                for (size_t i = 0; i < S; ++i) o[i] += a * x[i];
+            }
+        }
+    });
+}
+
+// depthwise_conv5x5_process_plane (src/common_ops.cpp:628-649): per output the
+// 25 taps in (ky, kx) order skipping the outside, bias last.
+void vae_dw5x5(const float * in, const float * w, const float * bias, float * out, size_t B, size_t C, size_t Hh,
+               size_t Ww) {
+    parallel_rows(B * C, [&](size_t r0, size_t r1) {
+        for (size_t r = r0; r < r1; ++r) {
+            const size_t c = r % C;
+            const float * x = in + r * Hh * Ww;
+            float * o = out + r * Hh * Ww;
+            for (size_t y = 0; y < Hh; ++y)
+                for (size_t xx = 0; xx < Ww; ++xx) {
+                    float sum = 0.0f;
+                    for (int ky = 0; ky < 5; ++ky)
+                        for (int kx = 0; kx < 5; ++kx) {
+                            const long iy = static_cast<long>(y) + ky - 2, ix = static_cast<long>(xx) + kx - 2;
+                            if (iy >= 0 && iy < static_cast<long>(Hh) && ix >= 0 && ix < static_cast<long>(Ww))
+                                sum += x[iy * Ww + ix] * w[(c * 5 + ky) * 5 + kx];
+                        }
+                    if (bias) sum += bias[c];
+                    o[y * Ww + xx] = sum;
+                }
+        }
+    });
+}
+
+// rms_norm_4d_channelwise (src/vae_ops.cpp:476-560): per pixel sum of squares
+// over channels with std::fma in channel order, 1 / sqrt(sum * (1/C) + eps),
+// then (x * inv) * w (+ b).
+void vae_rms_norm(const float * in, const float * w, const float * bias, float * out, size_t B, size_t C, size_t S,
+                  float eps) {
+    const float inv_c = 1.0f / static_cast<float>(C);
+    parallel_rows(B * ((S + 63) / 64), [&](size_t r0, size_t r1) {
+        for (size_t r = r0; r < r1; ++r) {
+            const size_t nb = (S + 63) / 64, b = r / nb, s0 = (r % nb) * 64, s1 = std::min(S, s0 + 64);
+            float ss[64], inv[64];
+            for (size_t i = s0; i < s1; ++i) ss[i - s0] = 0.0f;
+            for (size_t c = 0; c < C; ++c) {
+                const float * x = in + (b * C + c) * S;
+                for (size_t i = s0; i < s1; ++i) ss[i - s0] = std::fma(x[i], x[i], ss[i - s0]);
+            }
+            for (size_t i = s0; i < s1; ++i) inv[i - s0] = 1.0f / std::sqrt(ss[i - s0] * inv_c + eps);
+            for (size_t c = 0; c < C; ++c) {
+                const float * x = in + (b * C + c) * S;
+                float * o = out + (b * C + c) * S;
+                for (size_t i = s0; i < s1; ++i) {
+                    float v = x[i] * inv[i - s0] * w[c];
+                    if (bias) v += bias[c];
+                    o[i] = v;
+                }
+            }
+        }
+    });
+}
+
+// run_vae_upsample_block (src/vae_ops.cpp:808-821): nearest 2x (:330-375), the
+// 3x3 conv, then add_upsample_shortcut_2x_inplace (:386-445):
+// out[oc, 2y+i, 2x+j] += in[(4 oc + 2i + j) / repeats, y, x].
+void vae_upsample(const float * in, const float * w, const float * bias, float * out, size_t B, size_t Cin,
+                  size_t Cout, size_t Hh, size_t Ww, bool shortcut) {
+    const size_t H2 = 2 * Hh, W2 = 2 * Ww;
+    std::vector<float> up(B * Cin * H2 * W2);
+    for (size_t r = 0; r < B * Cin; ++r)
+        for (size_t y = 0; y < H2; ++y)
+            for (size_t x = 0; x < W2; ++x) up[(r * H2 + y) * W2 + x] = in[(r * Hh + y / 2) * Ww + x / 2];
+    vae_conv3x3(up.data(), w, bias, out, B, Cin, Cout, H2, W2);
+    if (!shortcut) return;
+    if ((Cout * 4) % Cin != 0) throw std::invalid_argument("VAE upsample shortcut channel ratio is invalid");
+    const size_t rep = Cout * 4 / Cin;
+    for (size_t b = 0; b < B; ++b)
+        for (size_t oc = 0; oc < Cout; ++oc)
+            for (size_t y = 0; y < Hh; ++y)
+                for (size_t x = 0; x < Ww; ++x)
+                    for (size_t q = 0; q < 4; ++q) {
+                        const size_t ic = (oc * 4 + q) / rep;
+                        out[((b * Cout + oc) * H2 + 2 * y + q / 2) * W2 + 2 * x + q % 2] +=
+                            in[((b * Cin + ic) * Hh + y) * Ww + x];
+                    }
+}
+
+// NCHW <-> token-major for the GLUMBConv restatement (pure data movement).
+void nchw_to_tokens(const float * in, float * out, size_t B, size_t C, size_t S) {
+    for (size_t b = 0; b < B; ++b)
+        for (size_t c = 0; c < C; ++c)
+            for (size_t i = 0; i < S; ++i) out[(b * S + i) * C + c] = in[(b * C + c) * S + i];
+}
+void tokens_to_nchw(const float * in, float * out, size_t B, size_t C, size_t S) {
+    for (size_t b = 0; b < B; ++b)
+        for (size_t c = 0; c < C; ++c)
+            for (size_t i = 0; i < S; ++i) out[(b * C + c) * S + i] = in[(b * S + i) * C + c];
+}
+
+struct VaeModel {
+    std::vector<size_t> ch;
+    std::vector<bool> attn;
+    size_t latent = 32, head_dim = 32, expand = 4;
+    float scaling = 0.41407f;
+    std::map<std::string, std::vector<float>> w;
+    std::map<std::string, std::vector<size_t>> shape;
+    const float * p(const std::string & n) const {
+        auto it = w.find(n);
+        if (it == w.end()) throw std::invalid_argument("missing vae weight " + n);
+        return it->second.data();
+    }
+};
+
+// run_vae_res_block (src/vae_ops.cpp:570-583)
+void vae_res_block(const VaeModel & m, const std::string & q, const float * in, float * out, size_t B, size_t C,
+                   size_t Hh, size_t Ww) {
+    const size_t n = B * C * Hh * Ww;
+    std::vector<float> h(n), h2(n);
+    vae_conv3x3(in, m.p(q + "conv1.weight"), m.p(q + "conv1.bias"), h.data(), B, C, C, Hh, Ww);
+    for (float & v : h) v = silu(v);
+    vae_conv3x3(h.data(), m.p(q + "conv2.weight"), nullptr, h2.data(), B, C, C, Hh, Ww);
+    vae_rms_norm(h2.data(), m.p(q + "norm.weight"), m.p(q + "norm.bias"), out, B, C, Hh * Ww, 1e-5f);
+    for (size_t i = 0; i < n; ++i) out[i] += in[i];
+}
+
+// run_vae_glumb_conv (src/vae_ops.cpp:585-607): glumb_conv (src/common_ops.cpp:733-761), RMSNorm, + input.
+void vae_glumb_block(const VaeModel & m, const std::string & q, const float * in, float * out, size_t B, size_t C,
+                     size_t Hh, size_t Ww) {
+    const size_t S = Hh * Ww, n = B * C * S, E = 2 * m.expand * C;
+    std::vector<float> tok(n), gt(n), g(n);
+    nchw_to_tokens(in, tok.data(), B, C, S);
+    glumb_conv(tok.data(), m.p(q + "conv_out.conv_inverted.weight"), m.p(q + "conv_out.conv_inverted.bias"),
+               m.p(q + "conv_out.conv_depth.weight"), m.p(q + "conv_out.conv_depth.bias"),
+               m.p(q + "conv_out.conv_point.weight"), gt.data(), B, Hh, Ww, C, E, C);
+    tokens_to_nchw(gt.data(), g.data(), B, C, S);
+    vae_rms_norm(g.data(), m.p(q + "conv_out.norm.weight"), m.p(q + "conv_out.norm.bias"), out, B, C, S, 1e-5f);
+    for (size_t i = 0; i < n; ++i) out[i] += in[i];
+}
+
+// run_vae_multiscale_attention (src/vae_ops.cpp:640-806).  Channel groups of
+// 3 * D consecutive channels (of q|k|v concatenated, then of the multiscale
+// branch) are the heads: q = the group's first D channels, k the next D, v the
+// last D.  Per head: scores[r][d] = sum_t vp[r][t] relu(k)[d][t] over t in
+// order (vp = v with a row of ones appended), hidden[r][t] = sum_d
+// scores[r][d] relu(q)[d][t] over d in order, out = hidden[d] / (hidden[D] + 1e-15).
+void vae_msattn(const VaeModel & m, const std::string & q, const float * in, float * out, size_t B, size_t C,
+                size_t Hh, size_t Ww) {
+    const size_t S = Hh * Ww, D = m.head_dim, inner = C, heads = inner / D;
+    std::vector<float> qkv(B * 3 * inner * S), ms(B * 3 * inner * S), dw(B * 3 * inner * S);
+    {
+        std::vector<float> t(B * inner * S);
+        const char * names[3] = {"attn.to_q.weight", "attn.to_k.weight", "attn.to_v.weight"};
+        for (int j = 0; j < 3; ++j) {
+            vae_conv1x1(in, m.p(q + names[j]), nullptr, t.data(), B, C, inner, S);
+            for (size_t b = 0; b < B; ++b)
+                std::copy(t.begin() + b * inner * S, t.begin() + (b + 1) * inner * S,
+                          qkv.begin() + (b * 3 + j) * inner * S);
+        }
+    }
+    vae_dw5x5(qkv.data(), m.p(q + "attn.to_qkv_multiscale.0.proj_in.weight"), nullptr, dw.data(), B, 3 * inner, Hh,
+              Ww);
+    vae_grouped1x1(dw.data(), m.p(q + "attn.to_qkv_multiscale.0.proj_out.weight"), ms.data(), B, 3 * inner,
+                   3 * inner, 3 * heads, S);
+    const size_t merged_heads = 2 * heads;
+    std::vector<float> merged(B * merged_heads * D * S);
+    parallel_rows(B * merged_heads, [&](size_t r0, size_t r1) {
+        std::vector<float> qm(D * S), km(D * S), vm((D + 1) * S), sc((D + 1) * D), hid((D + 1) * S);
+        for (size_t r = r0; r < r1; ++r) {
+            const size_t b = r / merged_heads, g = r % merged_heads;
+            const bool msb = g >= heads;
+            const size_t lg = msb ? g - heads : g;
+            const float * src = (msb ? ms.data() : qkv.data()) + (b * 3 * inner + lg * 3 * D) * S;
+            for (size_t d = 0; d < D; ++d)
+                for (size_t t = 0; t < S; ++t) {
+                    qm[d * S + t] = std::max(0.0f, src[d * S + t]);
+                    km[d * S + t] = std::max(0.0f, src[(D + d) * S + t]);
+                    vm[d * S + t] = src[(2 * D + d) * S + t];
+                }
+            for (size_t t = 0; t < S; ++t) vm[D * S + t] = 1.0f;
+            for (size_t rr = 0; rr <= D; ++rr) {
+                float * srow = sc.data() + rr * D;
+                for (size_t d = 0; d < D; ++d) srow[d] = 0.0f;
+                for (size_t t = 0; t < S; ++t) {
+                    const float a = vm[rr * S + t];
+                    for (size_t d = 0; d < D; ++d) srow[d] += a * km[d * S + t];
+                }
+            }
+            for (size_t rr = 0; rr <= D; ++rr) {
+                float * h = hid.data() + rr * S;
+                for (size_t t = 0; t < S; ++t) h[t] = 0.0f;
+                for (size_t d = 0; d < D; ++d) {
+                    const float a = sc[rr * D + d];
+                    for (size_t t = 0; t < S; ++t) h[t] += a * qm[d * S + t];
+                }
+            }
+            float * mg = merged.data() + (b * merged_heads + g) * D * S;
+            for (size_t t = 0; t < S; ++t) {
+                const float den = hid[D * S + t] + 1e-15f;
+                for (size_t d = 0; d < D; ++d) mg[d * S + t] = hid[d * S + t] / den;
+            }
+        }
+    });
+    std::vector<float> o(B * C * S);
+    vae_conv1x1(merged.data(), m.p(q + "attn.to_out.weight"), nullptr, o.data(), B, merged_heads * D, C, S);
+    vae_rms_norm(o.data(), m.p(q + "attn.norm_out.weight"), m.p(q + "attn.norm_out.bias"), out, B, C, S, 1e-5f);
+    for (size_t i = 0; i < B * C * S; ++i) out[i] += in[i];
+}
+
+// run_vae_decoder_input (src/vae.cpp:216-241): conv_in, then
+// add_repeated_channels_inplace (src/vae_ops.cpp:451-471).
+void vae_decoder_input(const VaeModel & m, const float * scaled, float * out, size_t B, size_t Hh, size_t Ww) {
+    const size_t top = m.ch.back(), S = Hh * Ww, rep = top / m.latent;
+    vae_conv3x3(scaled, m.p("decoder.conv_in.weight"), m.p("decoder.conv_in.bias"), out, B, m.latent, top, Hh, Ww);
+    for (size_t b = 0; b < B; ++b)
+        for (size_t c = 0; c < m.latent; ++c)
+            for (size_t r = 0; r < rep; ++r) {
+                float * o = out + (b * top + c * rep + r) * S;
+                const float * x = scaled + (b * m.latent + c) * S;
+                for (size_t i = 0; i < S; ++i) o[i] += x[i];
+            }
+}
+
+// run_vae_decode (src/vae.cpp:243-325).
+void vae_decode(const VaeModel & m, const float * latent, float * image, size_t B, size_t Hh, size_t Ww) {
+    const size_t L = m.ch.size();
+    std::vector<float> scaled(latent, latent + B * m.latent * Hh * Ww);
+    const float inv = 1.0f / m.scaling;
+    for (float & v : scaled) v *= inv;
+    size_t C = m.ch.back(), h = Hh, w = Ww;
+    std::vector<float> cur(B * C * h * w), nxt;
+    vae_decoder_input(m, scaled.data(), cur.data(), B, Hh, Ww);
+    for (size_t lv = L; lv-- > 0;) {
+        const std::string p = "decoder.up_blocks." + std::to_string(lv) + ".";
+        size_t base = 0;
+        if (lv + 1 < L) {
+            const size_t Co = m.ch[lv];
+            nxt.assign(B * Co * 4 * h * w, 0.0f);
+            vae_upsample(cur.data(), m.p(p + "0.conv.weight"), m.p(p + "0.conv.bias"), nxt.data(), B, C, Co, h, w,
+                         true);
+            cur.swap(nxt);
+            C = Co;
+            h *= 2;
+            w *= 2;
+            base = 1;
+        }
+        for (size_t l = base; l < base + 3; ++l) {
+            const std::string q = p + std::to_string(l) + ".";
+            nxt.assign(cur.size(), 0.0f);
+            if (!m.attn[lv]) {
+                vae_res_block(m, q, cur.data(), nxt.data(), B, C, h, w);
+                cur.swap(nxt);
+            } else {
+                vae_msattn(m, q, cur.data(), nxt.data(), B, C, h, w);
+                cur.swap(nxt);
+                vae_glumb_block(m, q, cur.data(), nxt.data(), B, C, h, w);
+                cur.swap(nxt);
+            }
+        }
+    }
+    nxt.assign(cur.size(), 0.0f);
+    vae_rms_norm(cur.data(), m.p("decoder.norm_out.weight"), m.p("decoder.norm_out.bias"), nxt.data(), B, C, h * w,
+                 1e-5f);
+    for (float & v : nxt) v = std::max(0.0f, v);
+    vae_conv3x3(nxt.data(), m.p("decoder.conv_out.weight"), m.p("decoder.conv_out.bias"), image, B, C, 3, h, w);
+}
+
 template <class F>
 int guard(F f) {
     try {
@@ -814,6 +1160,115 @@ int oracle_scheduler_timesteps(size_t steps, float * ts, float * sig) {
     std::copy(t.begin(), t.end(), ts);
     std::copy(s.begin(), s.end(), sig);
     return 0;
+}
+
+
+// ---------------------------------------------------------------- VAE API
+struct oracle_vae : VaeModel {};
+
+int oracle_vae_conv3x3(const float * in, const float * w, const float * bias, float * out, size_t B, size_t Cin,
+                       size_t Cout, size_t Hh, size_t Ww, int order) {
+    if (order < -1 || order > 1) return fail("order must be -1 (as the reference dispatches), 0 (im2col) or 1 (taps)");
+    return guard([&] { vae_conv3x3(in, w, bias, out, B, Cin, Cout, Hh, Ww, order); });
+}
+int oracle_vae_conv1x1(const float * in, const float * w, const float * bias, float * out, size_t B, size_t Cin,
+                       size_t Cout, size_t S) {
+    return guard([&] { vae_conv1x1(in, w, bias, out, B, Cin, Cout, S); });
+}
+int oracle_vae_grouped_conv1x1(const float * in, const float * w, float * out, size_t B, size_t Cin, size_t Cout,
+                               size_t groups, size_t S) {
+    if (groups == 0 || Cin % groups || Cout % groups) return fail("channels must be divisible by groups");
+    return guard([&] { vae_grouped1x1(in, w, out, B, Cin, Cout, groups, S); });
+}
+int oracle_vae_dw5x5(const float * in, const float * w, const float * bias, float * out, size_t B, size_t C,
+                     size_t Hh, size_t Ww) {
+    return guard([&] { vae_dw5x5(in, w, bias, out, B, C, Hh, Ww); });
+}
+int oracle_vae_rms_norm(const float * in, const float * w, const float * bias, float * out, size_t B, size_t C,
+                        size_t S, float eps) {
+    return guard([&] { vae_rms_norm(in, w, bias, out, B, C, S, eps); });
+}
+int oracle_vae_upsample(const float * in, const float * w, const float * bias, float * out, size_t B, size_t Cin,
+                        size_t Cout, size_t Hh, size_t Ww, int shortcut) {
+    return guard([&] { vae_upsample(in, w, bias, out, B, Cin, Cout, Hh, Ww, shortcut != 0); });
+}
+
+oracle_vae * oracle_vae_create(int full) {
+    auto * m = new oracle_vae();
+    const vae_spec::Config c = full ? vae_spec::full_config() : vae_spec::small_config();
+    m->ch = c.channels;
+    m->attn = c.attn;
+    m->latent = c.latent;
+    m->head_dim = c.head_dim;
+    m->expand = c.expand;
+    for (const vae_spec::Entry & e : vae_spec::manifest(c)) {
+        m->shape[e.name] = e.shape;
+        m->w[e.name].assign(vae_spec::numel(e.shape), 0.0f);
+    }
+    return m;
+}
+void oracle_vae_destroy(oracle_vae * m) { delete m; }
+
+int oracle_vae_generate(oracle_vae * m) {
+    return guard([&] {
+        const vae_spec::Config c = m->ch.size() == vae_spec::full_config().channels.size() &&
+                                           m->ch == vae_spec::full_config().channels
+                                       ? vae_spec::full_config()
+                                       : vae_spec::small_config();
+        for (const vae_spec::Entry & e : vae_spec::manifest(c)) {
+            std::vector<float> & t = m->w.at(e.name);
+            std::vector<float> r(std::max<size_t>(t.size(), 16));
+            randn(r.data(), r.size(), e.seed);
+            for (size_t i = 0; i < t.size(); ++i) t[i] = e.norm ? 1.0f + 0.1f * r[i] : 0.02f * r[i];
+        }
+    });
+}
+int oracle_vae_set(oracle_vae * m, const char * name, const float * data, size_t n) {
+    auto it = m->w.find(name);
+    if (it == m->w.end()) return fail(std::string("unknown vae weight ") + name);
+    if (it->second.size() != n) return fail(std::string("size mismatch for ") + name);
+    std::copy(data, data + n, it->second.begin());
+    return 0;
+}
+int oracle_vae_get(const oracle_vae * m, const char * name, float * out, size_t n) {
+    auto it = m->w.find(name);
+    if (it == m->w.end()) return fail(std::string("unknown vae weight ") + name);
+    if (it->second.size() != n) return fail(std::string("size mismatch for ") + name);
+    std::copy(it->second.begin(), it->second.end(), out);
+    return 0;
+}
+int oracle_vae_decoder_input(const oracle_vae * m, const float * latent, size_t B, size_t Hh, size_t Ww,
+                             float * out) {
+    return guard([&] {
+        std::vector<float> sc(latent, latent + B * m->latent * Hh * Ww);
+        const float inv = 1.0f / m->scaling;
+        for (float & v : sc) v *= inv;
+        vae_decoder_input(*m, sc.data(), out, B, Hh, Ww);
+    });
+}
+int oracle_vae_res_block(const oracle_vae * m, size_t level, size_t layer, const float * in, float * out, size_t B,
+                         size_t Hh, size_t Ww) {
+    return guard([&] {
+        const std::string q = "decoder.up_blocks." + std::to_string(level) + "." + std::to_string(layer) + ".";
+        vae_res_block(*m, q, in, out, B, m->ch.at(level), Hh, Ww);
+    });
+}
+int oracle_vae_attention(const oracle_vae * m, size_t level, size_t layer, const float * in, float * out,
+                         size_t B, size_t Hh, size_t Ww) {
+    return guard([&] {
+        const std::string q = "decoder.up_blocks." + std::to_string(level) + "." + std::to_string(layer) + ".";
+        vae_msattn(*m, q, in, out, B, m->ch.at(level), Hh, Ww);
+    });
+}
+int oracle_vae_glumb(const oracle_vae * m, size_t level, size_t layer, const float * in, float * out, size_t B,
+                     size_t Hh, size_t Ww) {
+    return guard([&] {
+        const std::string q = "decoder.up_blocks." + std::to_string(level) + "." + std::to_string(layer) + ".";
+        vae_glumb_block(*m, q, in, out, B, m->ch.at(level), Hh, Ww);
+    });
+}
+int oracle_vae_decode(const oracle_vae * m, const float * latent, size_t B, size_t Hh, size_t Ww, float * image) {
+    return guard([&] { vae_decode(*m, latent, image, B, Hh, Ww); });
 }
 
 }  // extern "C"

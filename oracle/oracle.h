@@ -143,6 +143,45 @@ int oracle_model_loop(const oracle_model * m, const float * latent, size_t Bl, s
 /* Scheduler (src/scheduler.cpp).  Timesteps/sigmas of the default config. */
 int oracle_scheduler_timesteps(size_t steps, float * timesteps, float * sigmas /* steps+1 */);
 
+/* ---- DC-AE VAE decoder (src/vae.cpp, src/vae_ops.cpp), NCHW fp32 ----
+ * Weights in PyTorch order (attention linears [out, in], convs [out, in, kh, kw]). */
+/* 3x3 same conv.  order -1: the reference's size-dependent choice
+ * (src/vae_ops.cpp:211-218); 0: im2col order (:18-95); 1: tap order (:104-194). */
+int oracle_vae_conv3x3(const float * in, const float * w, const float * bias, float * out, size_t B, size_t Cin,
+                       size_t Cout, size_t H, size_t W, int order);
+int oracle_vae_conv1x1(const float * in, const float * w, const float * bias, float * out, size_t B, size_t Cin,
+                       size_t Cout, size_t HW);
+int oracle_vae_grouped_conv1x1(const float * in, const float * w, float * out, size_t B, size_t Cin, size_t Cout,
+                               size_t groups, size_t HW);
+int oracle_vae_dw5x5(const float * in, const float * w, const float * bias, float * out, size_t B, size_t C,
+                     size_t H, size_t W);
+/* Per-pixel RMSNorm over channels (eps), weight and optional bias. */
+int oracle_vae_rms_norm(const float * in, const float * w, const float * bias, float * out, size_t B, size_t C,
+                        size_t HW, float eps);
+/* nearest 2x upsample, 3x3 conv, optional pixel-shuffled channel-repeat shortcut: out [B, Cout, 2H, 2W]. */
+int oracle_vae_upsample(const float * in, const float * w, const float * bias, float * out, size_t B, size_t Cin,
+                        size_t Cout, size_t H, size_t W, int shortcut);
+
+/* Whole decoder with the synthetic weights of oracle/vae_spec.h (full = 1: the
+ * Sana 1.0 DC-AE f32c32 decoder, 0: the small test decoder). */
+typedef struct oracle_vae oracle_vae;
+oracle_vae * oracle_vae_create(int full);
+void oracle_vae_destroy(oracle_vae * m);
+int oracle_vae_generate(oracle_vae * m);
+int oracle_vae_set(oracle_vae * m, const char * name, const float * data, size_t n);
+int oracle_vae_get(const oracle_vae * m, const char * name, float * out, size_t n);
+/* latent / scaling_factor -> conv_in + channel-repeat shortcut: out [B, top, H, W] */
+int oracle_vae_decoder_input(const oracle_vae * m, const float * latent, size_t B, size_t H, size_t W, float * out);
+/* one layer of up block `level` (ResBlock, attention, or GLUMBConv of an EfficientViT layer), NCHW in -> out */
+int oracle_vae_res_block(const oracle_vae * m, size_t level, size_t layer, const float * in, float * out, size_t B,
+                         size_t H, size_t W);
+int oracle_vae_attention(const oracle_vae * m, size_t level, size_t layer, const float * in, float * out,
+                         size_t B, size_t H, size_t W);
+int oracle_vae_glumb(const oracle_vae * m, size_t level, size_t layer, const float * in, float * out, size_t B,
+                     size_t H, size_t W);
+/* run_vae_decode: latent [B, 32, H, W] -> image [B, 3, H * 2^(levels-1), W * 2^(levels-1)] */
+int oracle_vae_decode(const oracle_vae * m, const float * latent, size_t B, size_t H, size_t W, float * image);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,8 +31,11 @@
 #include "torch_rng.h"
 #include "transformer.h"
 #include "transformer_ops.h"
+#include "vae.h"
+#include "vae_ops.h"
 
 #include "../model_spec.h"
+#include "../vae_spec.h"
 
 namespace {
 
@@ -114,6 +117,74 @@ SanaDenoiserWeights make_denoiser(const Gen & g, const sana_spec::Dims & d, size
         g.loaded("proj_out.weight"), g.loaded("proj_out.bias"),
     };
     return w;
+}
+
+// Seeded DC-AE decoder weights as load_vae_weights (src/vae.cpp:140-167)
+// would hand them over: linear attention weights reshaped to 1x1 convs by the
+// reference's own linear_weight_to_conv1x1, everything else as stored.
+struct VaeGen {
+    std::unordered_map<std::string, vae_spec::Entry> by_name;
+    explicit VaeGen(const vae_spec::Config & c) {
+        for (const vae_spec::Entry & e : vae_spec::manifest(c)) by_name[e.name] = e;
+    }
+    Tensor operator()(const std::string & name) const {
+        auto it = by_name.find(name);
+        if (it == by_name.end()) throw std::runtime_error("no such vae weight " + name);
+        const vae_spec::Entry & e = it->second;
+        Tensor t(e.shape);
+        const size_t n = t.numel();
+        // randn_torch_cpu needs >= 16 values: smaller tensors take the head of a 16-value draw
+        const Tensor r = randn_torch_cpu({std::max<size_t>(n, 16)}, e.seed);
+        for (size_t i = 0; i < n; ++i) {
+            const float v = r.data()[i];
+            t.data()[i] = e.norm ? 1.0f + 0.1f * v : 0.02f * v;
+        }
+        return t;
+    }
+};
+
+SanaVaeWeights make_vae(const vae_spec::Config & c) {
+    VaeGen g(c);
+    SanaVaeDecoderWeights dec{
+        g("decoder.conv_in.weight"), g("decoder.conv_in.bias"), g("decoder.norm_out.weight"),
+        g("decoder.norm_out.bias"), g("decoder.conv_out.weight"), g("decoder.conv_out.bias"), {}};
+    const size_t L = c.channels.size();
+    for (size_t i = 0; i < L; ++i) {
+        const std::string p = "decoder.up_blocks." + std::to_string(i) + ".";
+        SanaVaeUpBlockWeights ub;
+        size_t base = 0;
+        if (i + 1 < L) {
+            ub.upsample_conv_weight = g(p + "0.conv.weight");
+            ub.upsample_conv_bias = g(p + "0.conv.bias");
+            ub.is_res_block = !c.attn[i];
+            base = 1;
+        }
+        for (size_t l = base; l < base + 3; ++l) {
+            const std::string q = p + std::to_string(l) + ".";
+            if (ub.is_res_block) {
+                ub.res_blocks.push_back(SanaVaeResBlockWeights{g(q + "conv1.weight"), g(q + "conv1.bias"),
+                                                               g(q + "conv2.weight"), g(q + "norm.weight"),
+                                                               g(q + "norm.bias")});
+            } else {
+                SanaVaeAttentionWeights a{
+                    linear_weight_to_conv1x1(g(q + "attn.to_q.weight")),
+                    linear_weight_to_conv1x1(g(q + "attn.to_k.weight")),
+                    linear_weight_to_conv1x1(g(q + "attn.to_v.weight")),
+                    g(q + "attn.to_qkv_multiscale.0.proj_in.weight"),
+                    g(q + "attn.to_qkv_multiscale.0.proj_out.weight"),
+                    linear_weight_to_conv1x1(g(q + "attn.to_out.weight")),
+                    g(q + "attn.norm_out.weight"), g(q + "attn.norm_out.bias")};
+                SanaVaeGlumbConvWeights m{
+                    g(q + "conv_out.conv_inverted.weight"), g(q + "conv_out.conv_inverted.bias"),
+                    g(q + "conv_out.conv_depth.weight"), g(q + "conv_out.conv_depth.bias"),
+                    g(q + "conv_out.conv_point.weight"), g(q + "conv_out.norm.weight"),
+                    g(q + "conv_out.norm.bias")};
+                ub.attn_glumb_layers.push_back(SanaVaeAttnGlumbLayerWeights{a, m});
+            }
+        }
+        dec.up_blocks.push_back(std::move(ub));
+    }
+    return SanaVaeWeights{std::move(dec), 0.41407f, (size_t)1 << (L - 1)};
 }
 
 Tensor repeat_batch(const Tensor & x, size_t r) {
@@ -212,7 +283,10 @@ int usage() {
         "  ref_harness block SELF_HEADS CROSS_HEADS SIDE T OUTDIR\n"
         "  ref_harness forward SELF_HEADS CROSS_HEADS SIDE T MASK CHECK_STEP OUTDIR\n"
         "  ref_harness loop SELF_HEADS CROSS_HEADS SIDE STEPS GUIDANCE MASK OUTDIR\n"
-        "  ref_harness time-block SELF_HEADS CROSS_HEADS BATCH SIDE REPS\n");
+        "  ref_harness time-block SELF_HEADS CROSS_HEADS BATCH SIDE REPS\n"
+        "  ref_harness vae small|full SIDE OUTDIR\n"
+        "  ref_harness vae-conv SIDE CIN COUT OUTDIR\n"
+        "  ref_harness vae-digest small|full\n");
     return 2;
 }
 
@@ -304,6 +378,52 @@ int main(int argc, char ** argv) {
             Tensor fin = run_full_denoising_loop_with_cfg(latent, caption, gs, st, cfg, w, mask ? &bias : nullptr);
             std::printf("loop_ms %.3f\n", now_ms() - t0);
             dump(out, "final_latent", fin);
+            return 0;
+        }
+        if (mode == "vae-conv" && argc == 6) {
+            // both summation orders of the reference's 3x3 conv at one size
+            const size_t side = std::stoul(argv[2]), cin = std::stoul(argv[3]), cout = std::stoul(argv[4]);
+            const std::string out = argv[5];
+            Tensor x = randn_torch_cpu({1, cin, side, side}, 51);
+            Tensor w = randn_torch_cpu({cout, cin, 3, 3}, 52);
+            w.mul_inplace_scalar(0.05f);
+            Tensor b = randn_torch_cpu({std::max<size_t>(cout, 16)}, 53);
+            Tensor bias({cout});
+            for (size_t i = 0; i < cout; ++i) bias.data()[i] = b.data()[i];
+            dump(out, "x", x);
+            dump(out, "w", w);
+            dump(out, "bias", bias);
+            dump(out, "im2col", conv2d_3x3_im2col_gemm(x, w, &bias));
+            dump(out, "tap", conv2d_3x3_tap_accumulate(x, w, &bias));
+            return 0;
+        }
+        if ((mode == "vae" && argc == 5) || (mode == "vae-digest" && argc == 3)) {
+            const std::string which = argv[2];
+            const vae_spec::Config c = which == "full" ? vae_spec::full_config() : vae_spec::small_config();
+            if (mode == "vae-digest") {
+                VaeGen vg(c);
+                for (const vae_spec::Entry & e : vae_spec::manifest(c)) {
+                    Tensor t = vg(e.name);
+                    uint64_t h = 14695981039346656037ULL;
+                    const unsigned char * p = reinterpret_cast<const unsigned char *>(t.data().data());
+                    for (size_t i = 0; i < t.numel() * 4; ++i) { h ^= p[i]; h *= 1099511628211ULL; }
+                    std::printf("%s %016llx\n", e.name.c_str(), static_cast<unsigned long long>(h));
+                }
+                return 0;
+            }
+            const size_t side = std::stoul(argv[3]);
+            const std::string out = argv[4];
+            SanaVaeWeights w = make_vae(c);
+            Tensor latent = randn_torch_cpu({1, c.latent, side, side}, 42);
+            dump(out, "latent", latent);
+            Tensor scaled = latent;
+            scaled.mul_inplace_scalar(1.0f / w.scaling_factor);
+            Tensor h0 = run_vae_decoder_input(scaled, w.decoder, true);
+            dump(out, "decoder_input", h0);
+            double t0 = now_ms();
+            Tensor img = run_vae_decode(latent, w);
+            std::printf("vae_decode_ms %.3f\n", now_ms() - t0);
+            dump(out, "image", img);
             return 0;
         }
         if (mode == "time-block" && argc == 7) {

@@ -15,6 +15,15 @@ Cases (one .npz each):
                (checked bit-exact against forward + CFG + scheduler)
   cfg2_mask    same forward with the Gemma padding mask (1 / 40 real tokens)
   cfg3         20-step DPM-Solver++ loop, guidance 4.5, final latent
+  cfg5         full 28-block forward at 4096 px (latent 128x128, 16384
+               tokens), t=999, no mask
+  vae_small    the reference's run_vae_decode on the small synthetic DC-AE
+               decoder of oracle/vae_spec.h, latent 8x8 -> 64x64 RGB
+  vae_conv     both summation orders of the reference's 3x3 conv
+               (conv2d_3x3_im2col_gemm, conv2d_3x3_tap_accumulate)
+  vae_full     run_vae_decode on the full Sana 1.0 DC-AE f32c32 decoder,
+               latent 32x32 -> 1024x1024 RGB
+  vae_weights  64-bit FNV-1a digest of every synthetic VAE weight (small, full)
   weights      64-bit FNV-1a digest of every generated weight tensor (the
                reference's randn_torch_cpu, seed 1000 + sorted index)
 
@@ -45,6 +54,15 @@ CASES = {
     "cfg2_mask": (["forward", "36", "16", "32", "999", "1", "0"],
                   {"context": (2, 300, 1152), "noise_pred": (2, 32, 32, 32), "guided": (1, 32, 32, 32)}),
     "cfg3": (["loop", "36", "16", "32", "20", "4.5", "0"], {"final_latent": (1, 32, 32, 32)}),
+    "cfg5": (["forward", "36", "16", "128", "999", "0", "0"],
+             {"context": (2, 300, 1152), "noise_pred": (2, 32, 128, 128), "guided": (1, 32, 128, 128)}),
+    "vae_small": (["vae", "small", "8"],
+                  {"latent": (1, 32, 8, 8), "decoder_input": (1, 128, 8, 8), "image": (1, 3, 64, 64)}),
+    "vae_conv": (["vae-conv", "13", "24", "40"],
+                 {"x": (1, 24, 13, 13), "w": (40, 24, 3, 3), "bias": (40,), "im2col": (1, 40, 13, 13),
+                  "tap": (1, 40, 13, 13)}),
+    "vae_full": (["vae", "full", "32"],
+                 {"latent": (1, 32, 32, 32), "decoder_input": (1, 1024, 32, 32), "image": (1, 3, 1024, 1024)}),
 }
 FULL_LIMIT = 70000      # tensors up to this many values are stored whole
 SUBSAMPLE = 4096
@@ -62,12 +80,30 @@ def weights():
     print("wrote weights:", len(names), "tensors", flush=True)
 
 
+def vae_weights():
+    out = {}
+    for which in ("small", "full"):
+        res = subprocess.run([EXE, "vae-digest", which], capture_output=True, text=True, check=True)
+        names, digests = [], []
+        for ln in res.stdout.splitlines():
+            n, h = ln.split()
+            names.append(n)
+            digests.append(int(h, 16))
+        out[which + "_names"] = np.array(names)
+        out[which + "_fnv1a"] = np.array(digests, dtype=np.uint64)
+    np.savez_compressed(os.path.join(HERE, "vae_weights.npz"), **out)
+    print("wrote vae_weights", flush=True)
+
+
 def main(names):
     if not os.path.exists(EXE):
         sys.exit(f"{EXE} missing: build it with `make -C oracle/ref` (needs /root/reference)")
     for name in names:
         if name == "weights":
             weights()
+            continue
+        if name == "vae_weights":
+            vae_weights()
             continue
         args, tensors = CASES[name]
         with tempfile.TemporaryDirectory() as tmp:
@@ -98,4 +134,4 @@ def main(names):
 
 
 if __name__ == "__main__":
-    main(sys.argv[1:] or list(CASES) + ["weights"])
+    main(sys.argv[1:] or list(CASES) + ["weights", "vae_weights"])

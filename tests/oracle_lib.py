@@ -276,3 +276,145 @@ def mask_bias(L=300, uncond_real=1, cond_real=40):
     b[0, :uncond_real] = 0.0
     b[1, :cond_real] = 0.0
     return b
+
+
+# ---------------------------------------------------------------- VAE decoder
+SMALL_VAE = dict(latent=32, channels=(64, 64, 128, 128), attn=(False, False, True, True), head_dim=32, expand=4)
+FULL_VAE = dict(latent=32, channels=(128, 256, 512, 512, 1024, 1024), attn=(False, False, False, True, True, True),
+                head_dim=32, expand=4)
+
+
+def vae_manifest(cfg):
+    """GGUF name -> PyTorch-order shape of the synthetic decoder (oracle/vae_spec.h)."""
+    ch, attn, L = cfg["channels"], cfg["attn"], len(cfg["channels"])
+    m = {"decoder.conv_in.weight": (ch[-1], cfg["latent"], 3, 3), "decoder.conv_in.bias": (ch[-1],),
+         "decoder.norm_out.weight": (ch[0],), "decoder.norm_out.bias": (ch[0],),
+         "decoder.conv_out.weight": (3, ch[0], 3, 3), "decoder.conv_out.bias": (3,)}
+    for i in range(L):
+        p, C, base = f"decoder.up_blocks.{i}.", ch[i], 0
+        if i + 1 < L:
+            m[p + "0.conv.weight"] = (C, ch[i + 1], 3, 3)
+            m[p + "0.conv.bias"] = (C,)
+            base = 1
+        for l in range(base, base + 3):
+            q = f"{p}{l}."
+            if not attn[i]:
+                m.update({q + "conv1.weight": (C, C, 3, 3), q + "conv1.bias": (C,), q + "conv2.weight": (C, C, 3, 3),
+                          q + "norm.weight": (C,), q + "norm.bias": (C,)})
+            else:
+                Hd = cfg["expand"] * C
+                m.update({q + "attn.to_q.weight": (C, C), q + "attn.to_k.weight": (C, C),
+                          q + "attn.to_v.weight": (C, C),
+                          q + "attn.to_qkv_multiscale.0.proj_in.weight": (3 * C, 1, 5, 5),
+                          q + "attn.to_qkv_multiscale.0.proj_out.weight": (3 * C, cfg["head_dim"], 1, 1),
+                          q + "attn.to_out.weight": (C, 2 * C), q + "attn.norm_out.weight": (C,),
+                          q + "attn.norm_out.bias": (C,),
+                          q + "conv_out.conv_inverted.weight": (2 * Hd, C, 1, 1),
+                          q + "conv_out.conv_inverted.bias": (2 * Hd,),
+                          q + "conv_out.conv_depth.weight": (2 * Hd, 1, 3, 3),
+                          q + "conv_out.conv_depth.bias": (2 * Hd,),
+                          q + "conv_out.conv_point.weight": (C, Hd, 1, 1), q + "conv_out.norm.weight": (C,),
+                          q + "conv_out.norm.bias": (C,)})
+    return m
+
+
+class Vae:
+    """Whole-decoder oracle with the synthetic weights (or supplied ones)."""
+
+    def __init__(self, full=False, generate=True):
+        self.cfg = FULL_VAE if full else SMALL_VAE
+        L = lib()
+        L.oracle_vae_create.restype = ctypes.c_void_p
+        L.oracle_vae_create.argtypes = [ctypes.c_int]
+        L.oracle_vae_destroy.argtypes = [ctypes.c_void_p]
+        self.h = L.oracle_vae_create(1 if full else 0)
+        if generate:
+            check(L.oracle_vae_generate(ctypes.c_void_p(self.h)))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().oracle_vae_destroy(ctypes.c_void_p(self.h))
+            self.h = None
+
+    def get(self, name, shape=None):
+        shape = shape or vae_manifest(self.cfg)[name]
+        out = np.empty(shape, np.float32)
+        check(lib().oracle_vae_get(ctypes.c_void_p(self.h), name.encode(), fp(out), _sz(out.size)))
+        return out
+
+    def set(self, name, arr):
+        arr = f32(arr)
+        check(lib().oracle_vae_set(ctypes.c_void_p(self.h), name.encode(), fp(arr), _sz(arr.size)))
+
+    def upscale(self):
+        return 2 ** (len(self.cfg["channels"]) - 1)
+
+    def decoder_input(self, latent):
+        latent = f32(latent)
+        B, _, H, W = latent.shape
+        out = np.empty((B, self.cfg["channels"][-1], H, W), np.float32)
+        check(lib().oracle_vae_decoder_input(ctypes.c_void_p(self.h), fp(latent), _sz(B), _sz(H), _sz(W), fp(out)))
+        return out
+
+    def layer(self, kind, level, layer, x):
+        x = f32(x)
+        B, C, H, W = x.shape
+        out = np.empty_like(x)
+        fn = {"res": lib().oracle_vae_res_block, "attn": lib().oracle_vae_attention,
+              "glumb": lib().oracle_vae_glumb}[kind]
+        check(fn(ctypes.c_void_p(self.h), _sz(level), _sz(layer), fp(x), fp(out), _sz(B), _sz(H), _sz(W)))
+        return out
+
+    def decode(self, latent):
+        latent = f32(latent)
+        B, _, H, W = latent.shape
+        s = self.upscale()
+        out = np.empty((B, 3, H * s, W * s), np.float32)
+        check(lib().oracle_vae_decode(ctypes.c_void_p(self.h), fp(latent), _sz(B), _sz(H), _sz(W), fp(out)))
+        return out
+
+
+def vae_conv3x3(x, w, b=None, order=-1):
+    """order -1: as the reference dispatches by size; 0: im2col order; 1: tap order."""
+    x, w = f32(x), f32(w)
+    B, Cin, H, W = x.shape
+    out = np.empty((B, w.shape[0], H, W), np.float32)
+    check(lib().oracle_vae_conv3x3(fp(x), fp(w), fp(None if b is None else f32(b)), fp(out), _sz(B), _sz(Cin),
+                                   _sz(w.shape[0]), _sz(H), _sz(W), ctypes.c_int(order)))
+    return out
+
+
+def vae_rms_norm(x, w, b=None, eps=1e-5):
+    x = f32(x)
+    B, C, H, W = x.shape
+    out = np.empty_like(x)
+    check(lib().oracle_vae_rms_norm(fp(x), fp(f32(w)), fp(None if b is None else f32(b)), fp(out), _sz(B), _sz(C),
+                                    _sz(H * W), ctypes.c_float(eps)))
+    return out
+
+
+def vae_dw5x5(x, w, b=None):
+    x = f32(x)
+    B, C, H, W = x.shape
+    out = np.empty_like(x)
+    check(lib().oracle_vae_dw5x5(fp(x), fp(f32(w)), fp(None if b is None else f32(b)), fp(out), _sz(B), _sz(C),
+                                 _sz(H), _sz(W)))
+    return out
+
+
+def vae_grouped_conv1x1(x, w, groups):
+    x, w = f32(x), f32(w)
+    B, Cin, H, W = x.shape
+    out = np.empty((B, w.shape[0], H, W), np.float32)
+    check(lib().oracle_vae_grouped_conv1x1(fp(x), fp(w), fp(out), _sz(B), _sz(Cin), _sz(w.shape[0]), _sz(groups),
+                                           _sz(H * W)))
+    return out
+
+
+def vae_upsample(x, w, b, shortcut=True):
+    x, w = f32(x), f32(w)
+    B, Cin, H, W = x.shape
+    out = np.empty((B, w.shape[0], 2 * H, 2 * W), np.float32)
+    check(lib().oracle_vae_upsample(fp(x), fp(w), fp(f32(b)), fp(out), _sz(B), _sz(Cin), _sz(w.shape[0]), _sz(H),
+                                    _sz(W), ctypes.c_int(1 if shortcut else 0)))
+    return out

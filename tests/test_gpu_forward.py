@@ -62,6 +62,30 @@ def test_forward_1024px_vs_reference(full_model, case, masked):
     assert gerr < TOL_FORWARD
 
 
+def test_forward_4096px_vs_reference(full_model):
+    """4096 px (latent 128x128, 16384 image tokens): the reference's CPU forward
+    is too large to store whole, so the fixture keeps a strided subsample of
+    noise_pred and guided plus their L2 norms."""
+    path = os.path.join(GOLDEN, "cfg5.npz")
+    if not os.path.exists(path):
+        pytest.skip("cfg5 golden not generated")
+    m, d = full_model
+    fx = golden("cfg5")
+    latent = O.randn((1, 32, 128, 128), 42)
+    caption = O.randn((2, 300, 2304), 43)
+    d.set_context(caption, projected=False)
+    got = d.forward(latent, 999.0)
+    guided = got[:1] + np.float32(4.5) * (got[1:] - got[:1])
+    res = {}
+    for name, arr in (("noise_pred", got), ("guided", guided)):
+        stride = int(fx[name + "__stride"])
+        res[name] = rel_l2(arr.reshape(-1)[::stride], fx[name + "__sub"])
+        norm_err = abs(np.linalg.norm(arr.astype(np.float64)) / float(fx[name + "__l2"]) - 1.0)
+        print(f"cfg5 {name}: subsample rel_l2 {res[name]:.2e}, L2 norm rel diff {norm_err:.2e}")
+        assert res[name] < TOL_FORWARD
+        assert norm_err < TOL_FORWARD
+
+
 def test_forward_deterministic(full_model):
     m, d = full_model
     latent = O.randn((1, 32, 32, 32), 42)
