@@ -23,6 +23,13 @@ Prints ONE JSON line (rank 0, N = 1 only):
   cpu_baseline             the reference's own CPU block_forward (compiled
                            from source into oracle/_ref, 1 thread) on one
                            block of the same workload, median of 6, x28
+  peaks_measured           the dense fp16 MFMA rate of independent MFMA chains
+                           (sana_hip_mfma_peak) and the HBM rate of a 1 GiB
+                           device copy, on this GPU
+  forward_roofline         lower bound of the step, sum over kernels of
+                           max(flops / MFMA peak, bytes / HBM peak), with the
+                           spec and the measured peaks, and the measured step
+                           as a fraction of it
 
 --pmc-calib adds, before the timed region, three launches of a plain copy
 kernel over 256 MiB (torch.neg: 256 MiB read + 256 MiB written), the known
@@ -72,6 +79,63 @@ def forward_flops(B, N, L, d=DIMS, with_context=True):
     if with_context:
         total += 2 * B * L * d["caption_dim"] * C + 2 * B * L * C * C   # caption projection
     return total
+
+
+def step_lower_bound_ms(B, N, L, p_mfma_tflops, p_hbm_gbs, d=DIMS):
+    """Roofline lower bound of one step: every kernel at max(flops / MFMA peak,
+    bytes / HBM peak).  GEMMs are counted by flops; the bandwidth kernels by
+    their compulsory fp16 activation / fp32 residual interface bytes (no
+    re-reads, no weights): LN+modulate x2, linear attention, cross attention,
+    dwconv+GLU."""
+    C, E, F = d["hidden"], d["ffn"], d["ffn"] // 2
+    Hs, Hc = d["self_heads"], d["cross_heads"]
+    Ds, Dc = C // Hs, C // Hc
+    M = B * N
+    fl = lambda f: f / (p_mfma_tflops * 1e12) * 1e3
+    by = lambda b: b / (p_hbm_gbs * 1e9) * 1e3
+    gemm = 2 * M * C * 3 * C + 3 * 2 * M * C * C + 2 * M * C * E + 2 * M * F * C + 2 * 2 * B * L * C * C
+    blk = fl(gemm)
+    blk += 2 * by(M * C * 4 + M * C * 2)                                       # LN + modulate
+    blk += max(fl(2 * 2 * B * N * Hs * (Ds + 1) * Ds), by(4 * M * C * 2))     # linear attention
+    blk += max(fl(2 * 2 * B * Hc * N * L * Dc), by(2 * M * C * 2 + 2 * B * L * C * 2))   # cross attention
+    blk += max(fl(2 * M * E * 9), by(M * E * 2 + M * F * 2))                  # dwconv + GLU
+    total = d["layers"] * blk
+    total += fl(2 * M * d["latent_channels"] * C * 2 + 2 * B * (256 * C + C * C + C * 6 * C))
+    total += fl(2 * B * L * d["caption_dim"] * C + 2 * B * L * C * C)
+    return total
+
+
+def measured_peaks(sana_dit, torch, dev, stream):
+    """MFMA ceiling from sana_hip_mfma_peak and HBM rate from a 1 GiB copy, both
+    timed with HIP events on `stream`."""
+    import ctypes
+    L = sana_dit.lib()
+    wg, iters = 2048, 64
+    sink = torch.empty(wg * 256, device=dev, dtype=torch.float32)
+    fl = ctypes.c_double()
+    sp = stream.cuda_stream
+    sana_dit.check(L.sana_hip_mfma_peak(wg, iters, sink.data_ptr(), sp, ctypes.byref(fl)))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(3):
+        sana_dit.check(L.sana_hip_mfma_peak(wg, iters, sink.data_ptr(), sp, ctypes.byref(fl)))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    mfma = fl.value * 3 / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    n = 1 << 28                                      # 1 GiB of fp32
+    src = torch.ones(n, device=dev, dtype=torch.float32)
+    dst = torch.empty_like(src)
+    with torch.cuda.stream(stream):
+        dst.copy_(src)
+        e0.record(stream)
+        for _ in range(5):
+            dst.copy_(src)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    hbm = 5 * 2 * n * 4 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst, sink
+    return {"mfma_tflops": round(mfma, 1), "hbm_gbs": round(hbm, 1),
+            "how": "8 independent fp16 32x32x16 MFMA chains x 2048 workgroups; 1 GiB device copy (read + write)"}
 
 
 def cpu_baseline():
@@ -288,6 +352,10 @@ def main():
                                     "tokens": 128 * 128, "note": "28 blocks, CFG batch 2, context resident"}
         extras["microbench_4096_tokens"] = microbench_4096(sana_dit, torch, dev, stream)
 
+    peaks = measured_peaks(sana_dit, torch, dev, stream)
+    lb_spec = step_lower_bound_ms(B, N, L, PEAK_MFMA_TFLOPS, PEAK_HBM_GBS)
+    lb_meas = step_lower_bound_ms(B, N, L, peaks["mfma_tflops"], peaks["hbm_gbs"])
+
     step_flops = forward_flops(B, N, L, with_context=True)
     fwd_flops = forward_flops(B, N, L, with_context=False)
     res = {
@@ -320,6 +388,12 @@ def main():
                      "frac": round(gemm_tflops / PEAK_MFMA_TFLOPS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes": GEMM_BYTES, "avg_us": round(gemm_ms * 1e3, 2)},
         "cpu_baseline": cpu,
+        "peaks_measured": peaks,
+        "forward_roofline": {"lower_bound_ms_spec_peaks": round(lb_spec, 4), "frac_spec": round(lb_spec / wall_ms, 4),
+                             "lower_bound_ms_measured_peaks": round(lb_meas, 4),
+                             "frac_measured": round(lb_meas / wall_ms, 4),
+                             "note": "sum over kernels of max(flops/MFMA peak, bytes/HBM peak) for one step; "
+                                     "frac = lower bound / measured ms_per_step"},
         **extras,
     }
     d.close()

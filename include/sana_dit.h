@@ -144,6 +144,49 @@ int sana_dit_time_embed(sana_dit * ctx, const float * t, int64_t B, float * embe
  * FLOPs.  Overwrites the forward's activation buffers. */
 int sana_dit_time_gemm(sana_dit * ctx, int which, int iters, float * avg_ms, double * flops);
 
+/* ---- DC-AE VAE decoder: latent -> RGB (src/vae.h:11-92, src/vae.cpp) ----
+ * Levels are indexed as the reference's decoder.up_blocks.{i} (level 0 = the
+ * output resolution, the last level = the latent resolution, processed
+ * first).  Every level holds three ResBlocks or three EfficientViT layers
+ * (multiscale ReLU linear attention + GLUMBConv); every level but the last
+ * starts with a nearest-2x upsample conv with a pixel-shuffled shortcut.
+ * Channel counts must be multiples of 64 (<= 1024), head_dim 32. */
+#define SANA_VAE_MAX_LEVELS 8
+typedef struct sana_vae sana_vae;
+typedef struct {
+    int64_t latent_channels;                 /* 32 */
+    int64_t levels;                          /* up blocks, <= SANA_VAE_MAX_LEVELS */
+    int64_t channels[SANA_VAE_MAX_LEVELS];   /* per level */
+    int32_t attention[SANA_VAE_MAX_LEVELS];  /* 1: EfficientViT layers, 0: ResBlocks */
+    int64_t head_dim;                        /* 32 */
+    int64_t expand;                          /* GLUMBConv expansion (hidden = expand * C) */
+    float scaling_factor;                    /* SanaVaeWeights::scaling_factor, 0.41407 */
+    int device;
+} sana_vae_config;
+int sana_vae_create(const sana_vae_config * cfg, sana_vae ** out);
+int sana_vae_destroy(sana_vae * vae);
+/* One tensor by its GGUF name and PyTorch-order shape (the names and shapes
+ * load_vae_weights reads, src/vae.cpp:10-118,140-167; attention linears
+ * [out, in]).  fp32 host data; converted and laid out for the device. */
+int sana_vae_set_weight(sana_vae * vae, const char * name, const float * data, const int64_t * shape, int ndim);
+/* SANA_ERR_STATE naming the first missing tensor, else SANA_OK. */
+int sana_vae_check_weights(sana_vae * vae);
+/* All tensors from one GGUF (F32, F16 or BF16 payloads). */
+int sana_vae_load_gguf(sana_vae * vae, const char * path);
+/* run_vae_decode (src/vae.cpp:243-325): latent [B, Cl, H, W] fp32 ->
+ * image [B, 3, H * 2^(levels-1), W * 2^(levels-1)] fp32.  Host pointers. */
+int sana_vae_decode(sana_vae * vae, const float * latent, int64_t B, int64_t H, int64_t W, float * image);
+/* Same on device pointers, asynchronous on `stream`. */
+int sana_vae_decode_device(sana_vae * vae, const float * latent, int64_t B, int64_t H, int64_t W, float * image,
+                           void * stream);
+
+/* Measured MFMA ceiling for roofline reports (no counterpart in the reference):
+ * `workgroups` x 256 threads run `iters` steps of 8 independent fp16
+ * v_mfma_f32_32x32x16 chains with no memory traffic, asynchronously on `stream`;
+ * `sink` (device, workgroups * 256 floats) receives the sums; *flops is the
+ * work of the launch.  The caller times it (e.g. with events). */
+int sana_hip_mfma_peak(int64_t workgroups, int64_t iters, float * sink, void * stream, double * flops);
+
 /* GGUF index inspection (no GPU needed): number of tensors, and the name,
  * PyTorch-order shape (up to 4 dims), ggml type and absolute payload offset of
  * tensor i -- the fields load_gguf_weight_index records (src/weights_io.cpp:152-158). */

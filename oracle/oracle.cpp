@@ -1193,6 +1193,26 @@ int oracle_vae_upsample(const float * in, const float * w, const float * bias, f
     return guard([&] { vae_upsample(in, w, bias, out, B, Cin, Cout, Hh, Ww, shortcut != 0); });
 }
 
+oracle_vae * oracle_vae_create_config(size_t latent, size_t levels, const size_t * channels, const int * attn) {
+    vae_spec::Config c;
+    c.latent = latent;
+    for (size_t i = 0; i < levels; ++i) {
+        c.channels.push_back(channels[i]);
+        c.attn.push_back(attn[i] != 0);
+    }
+    auto * m = new oracle_vae();
+    m->ch = c.channels;
+    m->attn = c.attn;
+    m->latent = c.latent;
+    m->head_dim = c.head_dim;
+    m->expand = c.expand;
+    for (const vae_spec::Entry & e : vae_spec::manifest(c)) {
+        m->shape[e.name] = e.shape;
+        m->w[e.name].assign(vae_spec::numel(e.shape), 0.0f);
+    }
+    return m;
+}
+
 oracle_vae * oracle_vae_create(int full) {
     auto * m = new oracle_vae();
     const vae_spec::Config c = full ? vae_spec::full_config() : vae_spec::small_config();
@@ -1211,10 +1231,12 @@ void oracle_vae_destroy(oracle_vae * m) { delete m; }
 
 int oracle_vae_generate(oracle_vae * m) {
     return guard([&] {
-        const vae_spec::Config c = m->ch.size() == vae_spec::full_config().channels.size() &&
-                                           m->ch == vae_spec::full_config().channels
-                                       ? vae_spec::full_config()
-                                       : vae_spec::small_config();
+        vae_spec::Config c;
+        c.latent = m->latent;
+        c.channels = m->ch;
+        c.attn = m->attn;
+        c.head_dim = m->head_dim;
+        c.expand = m->expand;
         for (const vae_spec::Entry & e : vae_spec::manifest(c)) {
             std::vector<float> & t = m->w.at(e.name);
             std::vector<float> r(std::max<size_t>(t.size(), 16));

@@ -166,6 +166,8 @@ int oracle_vae_upsample(const float * in, const float * w, const float * bias, f
  * Sana 1.0 DC-AE f32c32 decoder, 0: the small test decoder). */
 typedef struct oracle_vae oracle_vae;
 oracle_vae * oracle_vae_create(int full);
+/* Any decoder shape (levels up to 8; head dim 32, expansion 4), same seeding rule. */
+oracle_vae * oracle_vae_create_config(size_t latent, size_t levels, const size_t * channels, const int * attn);
 void oracle_vae_destroy(oracle_vae * m);
 int oracle_vae_generate(oracle_vae * m);
 int oracle_vae_set(oracle_vae * m, const char * name, const float * data, size_t n);

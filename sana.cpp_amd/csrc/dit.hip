@@ -28,69 +28,14 @@
 #include <vector>
 
 #include "../../include/sana_dit.h"
+#include "host_util.h"
 #include "kernels.h"
 
 using sana::half_t;
 
 namespace {
 
-thread_local std::string g_last_error;
-
-int set_err(int code, const char * fmt, ...) {
-    char buf[1024];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(buf, sizeof(buf), fmt, ap);
-    va_end(ap);
-    g_last_error = buf;
-    return code;
-}
-
-struct SanaError {
-    int code;
-    std::string msg;
-};
-
-[[noreturn]] void throw_err(int code, const std::string & m) { throw SanaError{code, m}; }
-
-void hip_check(hipError_t e, const char * what) {
-    if (e != hipSuccess) {
-        throw_err(e == hipErrorOutOfMemory ? SANA_ERR_OUT_OF_MEMORY : SANA_ERR_HIP,
-                  std::string(what) + ": " + hipGetErrorString(e));
-    }
-}
-
-void launch_check(hipError_t e, const char * what) {
-    if (e == hipErrorInvalidValue) throw_err(SANA_ERR_SHAPE, std::string(what) + ": shape not supported by kernel");
-    hip_check(e, what);
-}
-
-int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
-
-// Device allocation owned by the context.
-struct DevMem {
-    void * p = nullptr;
-    size_t bytes = 0;
-    DevMem() = default;
-    DevMem(const DevMem &) = delete;
-    DevMem & operator=(const DevMem &) = delete;
-    ~DevMem() {
-        if (p) (void)hipFree(p);
-    }
-    void ensure(size_t n, bool zero = true) {
-        if (n <= bytes && p) return;
-        if (p) hip_check(hipFree(p), "hipFree");
-        p = nullptr;
-        bytes = 0;
-        hip_check(hipMalloc(&p, n ? n : 16), "hipMalloc");
-        bytes = n;
-        if (zero) hip_check(hipMemset(p, 0, n), "hipMemset");
-    }
-    template <class T>
-    T * as() const {
-        return static_cast<T *>(p);
-    }
-};
+using namespace sana_host;
 
 struct BlockDev {
     DevMem w_qkv, b_qkv, w_out, b_out, w_cq, b_cq, w_co, b_co, w_inv, b_inv, w_dw, b_dw, w_pt;
@@ -559,21 +504,6 @@ void run_graph(sana_dit * c,
         it = c->graphs.emplace(key, e).first;
     }
     hip_check(hipGraphLaunch(it->second.exec, s), "hipGraphLaunch");
-}
-
-template <class F>
-int guarded(F f) {
-    try {
-        f();
-        return SANA_OK;
-    } catch (const SanaError & e) {
-        g_last_error = e.msg;
-        return e.code;
-    } catch (const std::bad_alloc &) {
-        return set_err(SANA_ERR_OUT_OF_MEMORY, "host allocation failed");
-    } catch (const std::exception & e) {
-        return set_err(SANA_ERR_HIP, "%s", e.what());
-    }
 }
 
 struct BlockSuffix {
@@ -1225,6 +1155,16 @@ int sana_hip_dwconv_glu(const void * x, int64_t ldx, const float * wt, const flo
         launch_check(sana::dwconv_glu(static_cast<const half_t *>(x), ldx, wt, bias, static_cast<half_t *>(out), ldo,
                                       (int)B, (int)Hh, (int)Ww, (int)F, static_cast<hipStream_t>(stream)),
                      "dwconv_glu");
+    });
+}
+
+int sana_hip_mfma_peak(int64_t workgroups, int64_t iters, float * sink, void * stream, double * flops) {
+    return guarded([&] {
+        if (workgroups <= 0 || workgroups > 65536 || iters <= 0 || iters > (1 << 24) || !sink || !flops)
+            throw SanaError{SANA_ERR_INVALID_ARGUMENT, "mfma_peak: workgroups in [1, 65536], iters in [1, 2^24], "
+                                                       "sink and flops required"};
+        launch_check(sana::mfma_peak((int)workgroups, (int)iters, sink, static_cast<hipStream_t>(stream)), "mfma_peak");
+        *flops = sana::mfma_peak_flops((int)workgroups, (int)iters);
     });
 }
 

@@ -95,7 +95,9 @@ SANA_DEV void wait_stages(int keep) {
     wait_vmcnt<0>();
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int MODE, int SCHED, int ACT>
+// CONV: 0 plain A rows; 1 implicit 3x3 conv over a zero-bordered NHWC input;
+// 2 the same over the nearest-2x upsample of the input (GemmParams::conv).
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, int SCHED, int ACT, int CONV = 0>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
     using G = Cfg<BM, BN, WM, WN, STAGES>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -126,10 +128,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
     const int lchunk = (lane & 7) ^ lrow;
     const f16 * asrc[G::A_LOADS];
     const f16 * bsrc[G::B_LOADS];
+    // conv: output pixel (image, y, x) of each A load row; asrc is the image's bordered input base
+    int cy[CONV ? G::A_LOADS : 1], cx[CONV ? G::A_LOADS : 1];
 #pragma unroll
     for (int i = 0; i < G::A_LOADS; ++i) {
         const int r = (wid + i * G::NW) * 8 + lrow;
-        asrc[i] = reinterpret_cast<const f16 *>(p.A) + (int64_t)min(m0 + r, p.M - 1) * p.lda + lchunk * 8;
+        const int m = min(m0 + r, p.M - 1);
+        if constexpr (CONV == 0) {
+            asrc[i] = reinterpret_cast<const f16 *>(p.A) + (int64_t)m * p.lda + lchunk * 8;
+        } else {
+            const int hw = p.conv_h * p.conv_w;
+            const int img = m / hw, rem = m - img * hw;
+            cy[i] = rem / p.conv_w;
+            cx[i] = rem - cy[i] * p.conv_w;
+            const int ih = CONV == 2 ? p.conv_h / 2 : p.conv_h, iw = CONV == 2 ? p.conv_w / 2 : p.conv_w;
+            asrc[i] = reinterpret_cast<const f16 *>(p.A) + (int64_t)img * (ih + 2) * (iw + 2) * p.lda + lchunk * 8;
+        }
     }
 #pragma unroll
     for (int i = 0; i < G::B_LOADS; ++i) {
@@ -139,9 +153,35 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
     auto issue = [&](int kt, int st) {
         unsigned char * base = smem + st * G::STAGE_BYTES;
         const int k0 = kt * kBK;
+        if constexpr (CONV == 0) {
 #pragma unroll
-        for (int i = 0; i < G::A_LOADS; ++i)
-            __builtin_amdgcn_global_load_lds(static_cast<const void *>(asrc[i] + k0), SANA_LDS(base + (wid + i * G::NW) * 1024), 16, 0, 0);
+            for (int i = 0; i < G::A_LOADS; ++i)
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(asrc[i] + k0),
+                                                 SANA_LDS(base + (wid + i * G::NW) * 1024), 16, 0, 0);
+        } else {
+            // k-tile kt = (tap, 64-channel chunk): one 128-byte run of the source pixel
+            const int cpt = (int)(p.lda >> 6);
+            const int tap = kt / cpt, c0 = (kt - tap * cpt) << 6;
+            const int ky = tap / 3, kx = tap - 3 * ky;
+#pragma unroll
+            for (int i = 0; i < G::A_LOADS; ++i) {
+                int sr, sc, wp;
+                if constexpr (CONV == 1) {
+                    // bordered input: output (y, x) at tap (ky, kx) reads (y + ky, x + kx)
+                    sr = cy[i] + ky;
+                    sc = cx[i] + kx;
+                    wp = p.conv_w + 2;
+                } else {
+                    // upsampled coordinate u = y + ky - 1 in [-1, conv_h]: the border outside
+                    const int u = cy[i] + ky - 1, v = cx[i] + kx - 1;
+                    sr = u < 0 ? 0 : (u >= p.conv_h ? p.conv_h / 2 + 1 : (u >> 1) + 1);
+                    sc = v < 0 ? 0 : (v >= p.conv_w ? p.conv_w / 2 + 1 : (v >> 1) + 1);
+                    wp = p.conv_w / 2 + 2;
+                }
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(asrc[i] + ((int64_t)sr * wp + sc) * p.lda + c0),
+                                                 SANA_LDS(base + (wid + i * G::NW) * 1024), 16, 0, 0);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < G::B_LOADS; ++i)
             __builtin_amdgcn_global_load_lds(static_cast<const void *>(bsrc[i] + k0), SANA_LDS(base + G::A_BYTES + (wid + i * G::NW) * 1024),
@@ -321,6 +361,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) bv[e] = (p.bias && e < nc) ? p.bias[col + e] : 0.0f;
         }
+        // fp16 output row of tile row `row`: plain, or inside the bordered grid of a conv output
+        auto orow16 = [&](int row) -> int64_t {
+            if constexpr (CONV != 0) {
+                if (p.out16_pad) {
+                    const int hw = p.conv_h * p.conv_w;
+                    const int img = row / hw, rem = row - img * hw;
+                    const int y = rem / p.conv_w, x = rem - y * p.conv_w;
+                    return ((int64_t)img * (p.conv_h + 2) + y + 1) * (p.conv_w + 2) + x + 1;
+                }
+            }
+            return row;
+        };
         for (int pass = 0; pass < BM / ER; ++pass) {
             __syncthreads();  // the operand ring (pass 0) or the previous pass's rows are free
             if (ER == BM || wm == pass) {
@@ -383,7 +435,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                                 f16x8 h;
 #pragma unroll
                                 for (int e = 0; e < 8; ++e) h[e] = (f16)v[e];
-                                *reinterpret_cast<f16x8 *>(reinterpret_cast<f16 *>(p.out16) + (int64_t)row * p.ldo16 + col) = h;
+                                *reinterpret_cast<f16x8 *>(reinterpret_cast<f16 *>(p.out16) + orow16(row) * p.ldo16 + col) = h;
                             }
                             if (p.out32) {
                                 float * o = p.out32 + (int64_t)row * p.ldo32 + col;
@@ -392,7 +444,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                             }
                         } else {
                             for (int e = 0; e < nc; ++e) {
-                                if (p.out16) reinterpret_cast<f16 *>(p.out16)[(int64_t)row * p.ldo16 + col + e] = (f16)v[e];
+                                if (p.out16) reinterpret_cast<f16 *>(p.out16)[orow16(row) * p.ldo16 + col + e] = (f16)v[e];
                                 if (p.out32) p.out32[(int64_t)row * p.ldo32 + col + e] = v[e];
                             }
                         }
@@ -434,13 +486,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                                 f16x8 h;
 #pragma unroll
                                 for (int e = 0; e < 8; ++e) h[e] = (f16)x[e];
-                                *reinterpret_cast<f16x8 *>(reinterpret_cast<f16 *>(p.out16) + (int64_t)row * p.ldo16 + col) = h;
+                                *reinterpret_cast<f16x8 *>(reinterpret_cast<f16 *>(p.out16) + orow16(row) * p.ldo16 + col) = h;
                             }
                         } else {
                             for (int e = 0; e < nc; ++e) {
                                 const float nx = xr[e] + g[e] * v[e];
                                 xr[e] = nx;
-                                if (p.out16) reinterpret_cast<f16 *>(p.out16)[(int64_t)row * p.ldo16 + col + e] = (f16)nx;
+                                if (p.out16) reinterpret_cast<f16 *>(p.out16)[orow16(row) * p.ldo16 + col + e] = (f16)nx;
                             }
                         }
                     }
@@ -455,15 +507,31 @@ bool set_lds_limit(const void * k, size_t lds) {
     return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int MODE, int SCHED, int ACT>
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, int SCHED, int ACT, int CONV = 0>
 hipError_t launch_mode(const GemmParams & p, int tiles, hipStream_t s) {
     using G = Cfg<BM, BN, WM, WN, STAGES>;
     static const bool attr = set_lds_limit(
-        reinterpret_cast<const void *>(&gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT>), G::LDS_BYTES);
+        reinterpret_cast<const void *>(&gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT, CONV>), G::LDS_BYTES);
     (void)attr;
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT>), dim3(tiles), dim3(G::NT),
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT, CONV>), dim3(tiles), dim3(G::NT),
                        G::LDS_BYTES, s, p);
     return hipGetLastError();
+}
+
+// Implicit 3x3 convolutions: plain stores (optionally SiLU) and residual updates.
+template <int BM, int BN, int WM, int WN, int STAGES, int SCHED, int CONV>
+hipError_t launch_conv_mode(const GemmParams & p, hipStream_t s) {
+    const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+    if (p.mode == kGemmResidual)
+        return launch_mode<BM, BN, WM, WN, STAGES, kGemmResidual, SCHED, kActNone, CONV>(p, tiles, s);
+    if (p.act == kActSilu) return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActSilu, CONV>(p, tiles, s);
+    return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActNone, CONV>(p, tiles, s);
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES, int SCHED>
+hipError_t launch_conv(const GemmParams & p, hipStream_t s) {
+    if (p.conv == 2) return launch_conv_mode<BM, BN, WM, WN, STAGES, SCHED, 2>(p, s);
+    return launch_conv_mode<BM, BN, WM, WN, STAGES, SCHED, 1>(p, s);
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES, int SCHED = 0>
@@ -484,7 +552,17 @@ using namespace gemm_detail;
 hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     GemmParams p = p_in;
     if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % kBK != 0) return hipErrorInvalidValue;
-    if (!p.A || !p.W || p.lda < p.K || p.ldw < p.K || p.lda % 8 || p.ldw % 8) return hipErrorInvalidValue;
+    if (p.conv < 0 || p.conv > 2) return hipErrorInvalidValue;
+    if (p.conv) {
+        // implicit 3x3 conv: K = 9 taps x lda channels, M whole images of conv_h x conv_w
+        if (p.conv_h <= 0 || p.conv_w <= 0 || p.lda <= 0 || p.lda % kBK || p.K != 9 * p.lda ||
+            p.M % (p.conv_h * p.conv_w) || (p.mode != kGemmStore && p.mode != kGemmResidual) ||
+            (p.conv == 2 && (p.conv_h % 2 || p.conv_w % 2)))
+            return hipErrorInvalidValue;
+    } else if (p.out16_pad || p.lda < p.K) {
+        return hipErrorInvalidValue;
+    }
+    if (!p.A || !p.W || p.ldw < p.K || p.lda % 8 || p.ldw % 8) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(p.A) | reinterpret_cast<uintptr_t>(p.W)) & 15) return hipErrorInvalidValue;
     if (p.mode == kGemmResidual && !p.out32) return hipErrorInvalidValue;
     if (p.mode == kGemmVT && (!p.out16 || p.vt_rows <= 0 || p.vt_cols <= 0 || p.vt_batch <= 0 ||
@@ -505,6 +583,10 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     if (p.gate_t) vec = vec && (reinterpret_cast<uintptr_t>(p.gate_t) & 15) == 0;
     if (p.bias) vec = vec && (reinterpret_cast<uintptr_t>(p.bias) & 15) == 0;
     p.vec = vec ? 1 : 0;
+    if (p.conv) {
+        if (p.N <= 64) return launch_conv<128, 64, 2, 2, 2, 3>(p, s);
+        return launch_conv<128, 128, 2, 2, 2, 1>(p, s);
+    }
     static const int forced = [] {
         const char * e = std::getenv("SANA_GEMM_VARIANT");
         return e ? std::atoi(e) : -1;

@@ -52,6 +52,15 @@ struct GemmParams {
     half_t * kt16 = nullptr;
     half_t * vt16 = nullptr;
     int qkv_c = 0, qkv_n = 0;
+    // Implicit 3x3 "same" convolution (conv = 1), optionally on the nearest-2x
+    // upsample of its input (conv = 2).  Output pixel m = (b * conv_h + y) *
+    // conv_w + x of a conv_h x conv_w grid; A is the input in NHWC fp16 with a
+    // one-pixel zero border ([B][(ih + 2) * (iw + 2)][lda], ih x iw = the
+    // output grid, or half of it for conv = 2), lda = channels per tap (a
+    // multiple of 64), K = 9 * lda with tap-major weights W[n][(ky * 3 + kx) *
+    // lda + c].  With out16_pad the fp16 output goes to the interior of a
+    // bordered [B][(conv_h + 2) * (conv_w + 2)][ldo16] buffer.
+    int conv = 0, conv_h = 0, conv_w = 0, out16_pad = 0;
     int vec = 0;  // set by gemm(): 16-byte epilogue accesses are aligned
 };
 
@@ -113,6 +122,11 @@ hipError_t cross_attention(const half_t * q, int64_t ldq, const half_t * k, int6
 // Depthwise 3x3 (zero pad, bias) + GLU gate on a token-major grid:
 // x fp16 [B, H*W, ldx] (E = 2F channels), wt fp32 tap-major [9][E], bias [E],
 // out[b, t, c] = f16(d(c) * silu(d(F + c))), out fp16 [B*H*W, ldo].
+// Measured MFMA ceiling: `workgroups` x 256 threads of independent fp16
+// 32x32x16 MFMA chains, `iters` steps; sink holds workgroups * 256 floats.
+hipError_t mfma_peak(int workgroups, int iters, float * sink, hipStream_t s);
+double mfma_peak_flops(int workgroups, int iters);
+
 hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const float * bias, half_t * out, int64_t ldo,
                       int B, int Hh, int Ww, int F, hipStream_t s);
 

@@ -31,6 +31,15 @@ class Config(ctypes.Structure):
                 ("latent_channels", _i64), ("self_heads", _i64), ("cross_heads", _i64), ("device", ctypes.c_int)]
 
 
+SANA_VAE_MAX_LEVELS = 8
+
+
+class VaeConfig(ctypes.Structure):
+    _fields_ = [("latent_channels", _i64), ("levels", _i64), ("channels", _i64 * SANA_VAE_MAX_LEVELS),
+                ("attention", ctypes.c_int32 * SANA_VAE_MAX_LEVELS), ("head_dim", _i64), ("expand", _i64),
+                ("scaling_factor", ctypes.c_float), ("device", ctypes.c_int)]
+
+
 # name -> (restype, argtypes); exactly the entry points of include/sana_dit.h
 PROTOTYPES = {
     "sana_dit_last_error": (ctypes.c_char_p, []),
@@ -71,6 +80,14 @@ PROTOTYPES = {
     "sana_hip_cross_attention": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
                                                 _i64, _i64, _vp]),
     "sana_hip_dwconv_glu": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "sana_hip_mfma_peak": (ctypes.c_int, [_i64, _i64, _vp, _vp, ctypes.POINTER(ctypes.c_double)]),
+    "sana_vae_create": (ctypes.c_int, [ctypes.POINTER(VaeConfig), ctypes.POINTER(_vp)]),
+    "sana_vae_destroy": (ctypes.c_int, [_vp]),
+    "sana_vae_set_weight": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, ctypes.POINTER(_i64), ctypes.c_int]),
+    "sana_vae_check_weights": (ctypes.c_int, [_vp]),
+    "sana_vae_load_gguf": (ctypes.c_int, [_vp, ctypes.c_char_p]),
+    "sana_vae_decode": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp]),
+    "sana_vae_decode_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "sana_op_gemm_f32": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, ctypes.c_int, _vp, _i64,
                                         _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "sana_op_unary_f32": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_int, _vp]),
@@ -283,3 +300,55 @@ def manifest(layers=28, hidden=1152, ffn=5760, caption_dim=2304, latent_channels
         "caption_norm.weight": (C,), "scale_shift_table": (2, C), "proj_out.weight": (latent_channels, C),
         "proj_out.bias": (latent_channels,)})
     return shapes
+
+
+class Vae:
+    """One device context of the DC-AE VAE decoder (weights and workspace).
+
+    channels / attention are per level as the reference's decoder.up_blocks.{i}
+    (level 0 = output resolution)."""
+
+    def __init__(self, channels, attention, latent_channels=32, head_dim=32, expand=4, scaling_factor=0.41407,
+                 device=0):
+        n = len(channels)
+        cfg = VaeConfig()
+        cfg.latent_channels, cfg.levels, cfg.head_dim, cfg.expand = latent_channels, n, head_dim, expand
+        cfg.scaling_factor, cfg.device = scaling_factor, device
+        for i in range(n):
+            cfg.channels[i] = channels[i]
+            cfg.attention[i] = 1 if attention[i] else 0
+        self.cfg, self.levels, self.latent_channels = cfg, n, latent_channels
+        h = _vp()
+        check(lib().sana_vae_create(ctypes.byref(cfg), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().sana_vae_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def set_weight(self, name, arr):
+        arr = _f32(arr)
+        shape = (_i64 * arr.ndim)(*arr.shape)
+        check(lib().sana_vae_set_weight(self.h, name.encode(), ptr(arr), shape, arr.ndim))
+
+    def check_weights(self):
+        check(lib().sana_vae_check_weights(self.h))
+
+    def load_gguf(self, path):
+        check(lib().sana_vae_load_gguf(self.h, str(path).encode()))
+
+    def decode(self, latent):
+        latent = _f32(latent)
+        B, _, H, W = latent.shape
+        s = 2 ** (self.levels - 1)
+        out = np.empty((B, 3, H * s, W * s), np.float32)
+        check(lib().sana_vae_decode(self.h, ptr(latent), B, H, W, ptr(out)))
+        return out
+
+    def decode_device(self, latent, shape, image, stream):
+        B, _, H, W = shape
+        check(lib().sana_vae_decode_device(self.h, ptr(latent), B, H, W, ptr(image), stream))

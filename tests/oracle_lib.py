@@ -321,13 +321,22 @@ def vae_manifest(cfg):
 class Vae:
     """Whole-decoder oracle with the synthetic weights (or supplied ones)."""
 
-    def __init__(self, full=False, generate=True):
-        self.cfg = FULL_VAE if full else SMALL_VAE
+    def __init__(self, full=False, generate=True, cfg=None):
         L = lib()
         L.oracle_vae_create.restype = ctypes.c_void_p
         L.oracle_vae_create.argtypes = [ctypes.c_int]
+        L.oracle_vae_create_config.restype = ctypes.c_void_p
+        L.oracle_vae_create_config.argtypes = [_sz, _sz, ctypes.POINTER(_sz), ctypes.POINTER(ctypes.c_int)]
         L.oracle_vae_destroy.argtypes = [ctypes.c_void_p]
-        self.h = L.oracle_vae_create(1 if full else 0)
+        if cfg is not None:
+            self.cfg = dict(SMALL_VAE, **cfg)
+            n = len(self.cfg["channels"])
+            ch = (_sz * n)(*self.cfg["channels"])
+            at = (ctypes.c_int * n)(*[1 if a else 0 for a in self.cfg["attn"]])
+            self.h = L.oracle_vae_create_config(self.cfg["latent"], n, ch, at)
+        else:
+            self.cfg = FULL_VAE if full else SMALL_VAE
+            self.h = L.oracle_vae_create(1 if full else 0)
         if generate:
             check(L.oracle_vae_generate(ctypes.c_void_p(self.h)))
 
