@@ -650,8 +650,9 @@ __global__ __launch_bounds__(256) void xattn_fast_kernel(const f16 * __restrict_
         if (ks < KS && d0 + 8 <= D) qf[ks] = *reinterpret_cast<const f16x8 *>(qr + d0);
     }
 
-    // stage K rows (zero past D and past L) and V^T rows (zero past D; keys
-    // past L are zero in vt): all loads in flight before the LDS stores
+    // stage K rows (zero past D and past L) and V^T rows (zero past D and past
+    // L, whatever the padding of vt holds): all loads in flight before the LDS
+    // stores
     const f16 * kb = k + (int64_t)b * L * ldk + (int64_t)h * D;
     const f16 * vb = vt + ((int64_t)b * H * D + (int64_t)h * D) * ldvt;
     f16x8 kreg[KN], vreg[VN];
@@ -670,6 +671,11 @@ __global__ __launch_bounds__(256) void xattn_fast_kernel(const f16 * __restrict_
 #pragma unroll
         for (int e = 0; e < 8; ++e) vreg[j][e] = (f16)0.0f;
         if (idx < 96 * VCH && dim < D && c8 < LP) vreg[j] = *reinterpret_cast<const f16x8 *>(vb + (int64_t)dim * ldvt + c8);
+        if (c8 + 8 > L) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (c8 + e >= L) vreg[j][e] = (f16)0.0f;
+        }
     }
     for (int key = tid; key < LP; key += 256)
         bs[key] = key < L ? (bias ? bias[(int64_t)b * L + key] * kLog2e : 0.0f) : -INFINITY;

@@ -133,14 +133,12 @@ void upload_f16(DevMem & dst, const float * src, int64_t rows, int64_t cols, int
         for (int64_t c = 0; c < cols; ++c)
             h[(size_t)r * ld + c] = (half_t)(transposed ? src[c * rows + r] : src[r * cols + c]);
     if (!dst.p) dst.ensure((size_t)total_rows * ld * sizeof(half_t));
-    hip_check(hipMemcpy(dst.as<half_t>() + (size_t)row_offset * ld, h.data(), h.size() * sizeof(half_t),
-                        hipMemcpyHostToDevice),
-              "upload");
+    copy_to_device(dst.as<half_t>() + (size_t)row_offset * ld, h.data(), h.size() * sizeof(half_t), "upload");
 }
 
 void upload_f32(DevMem & dst, const float * src, size_t n, size_t offset = 0, size_t total = 0) {
     if (!dst.p) dst.ensure((total ? total : n) * sizeof(float));
-    hip_check(hipMemcpy(dst.as<float>() + offset, src, n * sizeof(float), hipMemcpyHostToDevice), "upload");
+    copy_to_device(dst.as<float>() + offset, src, n * sizeof(float), "upload");
 }
 
 void upload_f32_transposed(DevMem & dst, const float * src, int64_t rows, int64_t cols, bool src_transposed) {
@@ -767,6 +765,8 @@ int sana_dit_get_context(sana_dit * c, float * out) {
     if (!c || !out) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
     if (!c->ctx_ready) return set_err(SANA_ERR_STATE, "no context set");
     return guarded([&] {
+        // the context may have been computed on the context's stream or a caller's
+        hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
         hip_check(hipMemcpy(out, c->ctx32.p, (size_t)c->ctx_B * c->ctx_L * c->C * 4, hipMemcpyDeviceToHost),
                   "download context");
     });

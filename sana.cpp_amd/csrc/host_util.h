@@ -64,13 +64,27 @@ struct DevMem {
         bytes = 0;
         hip_check(hipMalloc(&p, n ? n : 16), "hipMalloc");
         bytes = n;
-        if (zero) hip_check(hipMemset(p, 0, n), "hipMemset");
+        if (zero) {
+            // A device memset may return before it completes, and work on a
+            // non-blocking stream is not ordered after the null stream: wait
+            // for the fill so every later launch sees the zeros.
+            hip_check(hipMemset(p, 0, n), "hipMemset");
+            hip_check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        }
     }
     template <class T>
     T * as() const {
         return static_cast<T *>(p);
     }
 };
+
+// Host -> device copy that has landed when it returns: a pageable-source
+// hipMemcpy may return once the data is staged, and a non-blocking stream is
+// not ordered after the null stream's DMA.
+inline void copy_to_device(void * dst, const void * src, size_t bytes, const char * what) {
+    hip_check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), what);
+    hip_check(hipStreamSynchronize(nullptr), what);
+}
 
 // Runs f, translating SanaError, allocation failures and other exceptions into
 // a SANA_ERR_* code with the message in g_last_error.

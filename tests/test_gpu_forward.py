@@ -135,6 +135,8 @@ def test_small_loop_vs_oracle(small_model):
     d.set_context(caption, projected=False)
     ts, sg = O.scheduler_timesteps(6)
     got = d.denoise_loop(latent, ts, sg, 4.5)
+    assert np.isfinite(ref).all(), "oracle loop not finite"
+    assert np.isfinite(got).all(), "device loop not finite"
     err = rel_l2(got, ref)
     print(f"small loop rel_l2 {err:.2e}")
     assert err < TOL_LOOP
