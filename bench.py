@@ -31,6 +31,10 @@ Prints ONE JSON line (rank 0, N = 1 only):
                            spec and the measured peaks, and the measured step
                            as a fraction of it
 
+  vae_decode_1024px        the DC-AE decode of one 32x32x32 latent to a
+                           1024x1024 image (the stage after the denoising
+                           loop), ms and TFLOP/s
+
 --pmc-calib adds, before the timed region, three launches of a plain copy
 kernel over 256 MiB (torch.neg: 256 MiB read + 256 MiB written), the known
 size the HBM counters are scaled by.
@@ -232,6 +236,64 @@ def microbench_4096(sana_dit, torch, dev, stream):
             "shape": "B=2, 64x64 tokens, C=1152, self heads 16x72, Mix-FFN 1152->5760->2880->1152"}
 
 
+VAE_CHANNELS = (128, 256, 512, 512, 1024, 1024)   # DC-AE f32c32 decoder of Sana 1.0, level 0 = output
+VAE_ATTENTION = (False, False, False, True, True, True)
+
+
+def vae_flops(h, w, channels=VAE_CHANNELS, attention=VAE_ATTENTION, latent=32, head=32, expand=4):
+    """Multiply-add flops (x2) of one DC-AE decode of an h x w latent: 3x3 convs
+    as 9-tap GEMMs, the multiscale attention (q|k|v, depthwise 5x5, grouped
+    1x1, two linear attentions, to_out) and GLUMBConv."""
+    L = len(channels)
+    f = 2 * 9 * latent * channels[-1] * h * w
+    for i in range(L - 1, -1, -1):
+        C, s = channels[i], 2 ** (L - 1 - i)
+        P = h * s * w * s
+        if i + 1 < L:
+            f += 2 * 9 * channels[i + 1] * C * P
+        for _ in range(3):
+            if not attention[i]:
+                f += 2 * (2 * 9 * C * C * P)
+            else:
+                E = expand * C
+                f += 2 * P * 3 * C * C + 2 * 25 * 3 * C * P + 2 * head * 3 * C * P
+                f += 2 * (C // head) * 2 * (2 * (head + 1) * head * P)
+                f += 2 * P * C * 2 * C + 2 * P * 2 * E * C + 2 * 9 * 2 * E * P + 2 * P * C * E
+    return f + 2 * 9 * channels[0] * 3 * h * w * 4 ** (L - 1)
+
+
+def vae_decode_1024px(sana_dit, torch, dev, stream, rng):
+    """DC-AE decode of one 32x32x32 latent to a 1024x1024 image on the device
+    (sana_vae_decode_device), seeded N(0, 0.02) weights, RMSNorm weights
+    1 + 0.1 N(0, 1); mean of 3 decodes after one warm-up."""
+    import numpy as np
+    v = sana_dit.Vae(VAE_CHANNELS, VAE_ATTENTION)
+    for name, shape in sana_dit.vae_manifest(VAE_CHANNELS, VAE_ATTENTION).items():
+        z = rng.standard_normal(shape, dtype=np.float32)
+        norm = name.endswith("norm.weight") or name.endswith("norm_out.weight")
+        v.set_weight(name, 1 + np.float32(0.1) * z if norm else z * np.float32(0.02))
+    v.check_weights()
+    lat = torch.from_numpy(rng.standard_normal((1, 32, SIDE, SIDE), dtype=np.float32)).to(dev)
+    img = torch.empty((1, 3, 1024, 1024), device=dev, dtype=torch.float32)
+    sp = stream.cuda_stream
+    v.decode_device(lat, tuple(lat.shape), img, sp)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(3):
+        v.decode_device(lat, tuple(lat.shape), img, sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 3
+    if not torch.isfinite(img).all():
+        raise RuntimeError("non-finite decoded image")
+    v.close()
+    fl = vae_flops(SIDE, SIDE)
+    return {"ms": round(ms, 3), "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "gflop": round(fl / 1e9, 1),
+            "shape": "latent 1x32x32x32 -> image 1x3x1024x1024, DC-AE f32c32 (128/256/512 ResBlocks, "
+                     "512/1024/1024 EfficientViT)"}
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (None when it is absent)."""
@@ -351,6 +413,7 @@ def main():
         extras["forward_4096px"] = {"ms": round(c5_ms, 3), "tflops": round(c5_flops / (c5_ms * 1e-3) / 1e12, 1),
                                     "tokens": 128 * 128, "note": "28 blocks, CFG batch 2, context resident"}
         extras["microbench_4096_tokens"] = microbench_4096(sana_dit, torch, dev, stream)
+        extras["vae_decode_1024px"] = vae_decode_1024px(sana_dit, torch, dev, stream, rng)
 
     peaks = measured_peaks(sana_dit, torch, dev, stream)
     lb_spec = step_lower_bound_ms(B, N, L, PEAK_MFMA_TFLOPS, PEAK_HBM_GBS)

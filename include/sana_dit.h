@@ -176,6 +176,11 @@ int sana_vae_load_gguf(sana_vae * vae, const char * path);
 /* run_vae_decode (src/vae.cpp:243-325): latent [B, Cl, H, W] fp32 ->
  * image [B, 3, H * 2^(levels-1), W * 2^(levels-1)] fp32.  Host pointers. */
 int sana_vae_decode(sana_vae * vae, const float * latent, int64_t B, int64_t H, int64_t W, float * image);
+/* run_vae_decoder_input (src/vae.cpp:211-241): conv_in of latent [B, Cl, H, W]
+ * (no scaling), plus the channel-repeat shortcut when in_shortcut != 0 ->
+ * out [B, C_top, H, W] fp32.  Needs only the conv_in tensors.  Host pointers. */
+int sana_vae_decoder_input(sana_vae * vae, const float * latent, int64_t B, int64_t H, int64_t W, int in_shortcut,
+                           float * out);
 /* Same on device pointers, asynchronous on `stream`. */
 int sana_vae_decode_device(sana_vae * vae, const float * latent, int64_t B, int64_t H, int64_t W, float * image,
                            void * stream);

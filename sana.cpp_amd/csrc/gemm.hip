@@ -620,6 +620,11 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
         case 27: return launch<128, 64, 2, 2, 2, 3>(p, s);
         case 28: return launch<64, 64, 2, 2, 2, 3>(p, s);
         case 29: return launch<128, 128, 2, 2, 2, 3>(p, s);
+        case 30: return launch<128, 96, 4, 1, 2, 3>(p, s);
+        case 31: return launch<128, 96, 4, 1, 2, 1>(p, s);
+        case 32: return launch<128, 96, 2, 1, 2, 3>(p, s);
+        case 33: return launch<128, 96, 4, 1, 3, 1>(p, s);
+        case 34: return launch<128, 96, 4, 1, 4, 1>(p, s);
         default: break;
     }
     // Tile choice from sweeps on MI355X with cold weights (each GEMM's weights

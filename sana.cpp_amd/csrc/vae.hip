@@ -49,9 +49,11 @@ constexpr int kVaeHead = 32;  // head dim and grouped-conv group size
 // Scaled latent (x / scaling_factor, NCHW fp32) -> the bordered NHWC fp16
 // conv_in input [B][(h + 2) * (w + 2)][64] (channels past Cl and the border
 // zero), and the channel-repeat shortcut of run_vae_decoder_input
-// (src/vae.cpp:233-240): x32[p][c] = scaled[c / rep] at pixel p.
+// (src/vae.cpp:233-240): x32[p][c] = scaled[c / rep] at pixel p (0 without
+// the shortcut).
 __global__ void vae_prep_kernel(const float * __restrict__ lat, int B, int Cl, int h, int w, float inv_sf,
-                                f16 * __restrict__ pad, int ldp, float * __restrict__ x32, int Ctop, int rep) {
+                                f16 * __restrict__ pad, int ldp, float * __restrict__ x32, int Ctop, int rep,
+                                int shortcut) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t npad = (int64_t)B * (h + 2) * (w + 2) * ldp;
     if (i < npad) {
@@ -68,7 +70,7 @@ __global__ void vae_prep_kernel(const float * __restrict__ lat, int B, int Cl, i
         const int oc = (int)(i % Ctop);
         const int64_t p = i / Ctop;
         const int xx = (int)(p % w), yy = (int)((p / w) % h), b = (int)(p / ((int64_t)w * h));
-        x32[i] = lat[(((int64_t)b * Cl + oc / rep) * h + yy) * w + xx] * inv_sf;
+        x32[i] = shortcut ? lat[(((int64_t)b * Cl + oc / rep) * h + yy) * w + xx] * inv_sf : 0.0f;
     }
 }
 
@@ -242,14 +244,16 @@ __global__ __launch_bounds__(256) void vae_grouped32_kernel(const f16 * __restri
     *reinterpret_cast<f16x4 *>(out + (int64_t)pix * C + g * 32 + o0) = o;
 }
 
-// conv_out result [P][3] (NHWC) -> image [B][3][H][W].
-__global__ void vae_to_nchw_kernel(const float * __restrict__ in, float * __restrict__ img, int B, int H, int W) {
+// NHWC [B * H * W][C] -> NCHW [B][C][H][W] (the conv_out image, C = 3, or the
+// conv_in stage output).
+__global__ void vae_to_nchw_kernel(const float * __restrict__ in, float * __restrict__ img, int B, int C, int H,
+                                   int W) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t hw = (int64_t)H * W;
-    if (i >= (int64_t)B * 3 * hw) return;
+    if (i >= (int64_t)B * C * hw) return;
     const int64_t s = i % hw;
-    const int c = (int)((i / hw) % 3), b = (int)(i / (3 * hw));
-    img[i] = in[((int64_t)b * hw + s) * 3 + c];
+    const int c = (int)((i / hw) % C), b = (int)(i / (C * hw));
+    img[i] = in[((int64_t)b * hw + s) * C + c];
 }
 
 unsigned blocks_for(int64_t n, int per = 256) { return (unsigned)((n + per - 1) / per); }
@@ -291,7 +295,7 @@ namespace {
 
 void upload(DevMem & d, const void * src, size_t bytes) {
     d.ensure(bytes, false);
-    hip_check(hipMemcpy(d.p, src, bytes, hipMemcpyHostToDevice), "hipMemcpy weights");
+    copy_to_device(d.p, src, bytes, "hipMemcpy weights");
 }
 
 void upload_f32(DevMem & d, const float * src, size_t n) { upload(d, src, n * 4); }
@@ -608,7 +612,7 @@ void decode(sana_vae * v, const float * lat, int64_t B, int64_t h, int64_t w, fl
         const int64_t n = std::max<int64_t>(B * (h + 2) * (w + 2) * clp, B * h * w * top);
         hipLaunchKernelGGL(vae_prep_kernel, dim3(blocks_for(n)), dim3(256), 0, s, lat, (int)B, (int)v->Cl, (int)h,
                            (int)w, 1.0f / v->scaling, v->lat16.as<f16>(), (int)clp, v->x32.as<float>(), (int)top,
-                           (int)rep);
+                           (int)rep, 1);
         launch_check(hipGetLastError(), "vae prep");
     }
     DevMem * cur = &v->pad0;   // bordered fp16 input of the next 3x3 conv
@@ -706,7 +710,28 @@ void decode(sana_vae * v, const float * lat, int64_t B, int64_t h, int64_t w, fl
     gemm_conv(1, cur->as<half_t>(), C, v->cout_w, B, H, W, 3, v->cout_b.as<float>(), sana::kActNone, false, nullptr,
               nullptr, false, v->o32.as<float>(), s);
     hipLaunchKernelGGL(vae_to_nchw_kernel, dim3(blocks_for(B * 3 * H * W)), dim3(256), 0, s, v->o32.as<float>(), img,
-                       (int)B, (int)H, (int)W);
+                       (int)B, 3, (int)H, (int)W);
+    launch_check(hipGetLastError(), "vae to nchw");
+}
+
+// run_vae_decoder_input (src/vae.cpp:211-241) on device pointers: conv_in of
+// the unscaled latent (+ shortcut) -> out NCHW [B, top, h, w].
+void decoder_input(sana_vae * v, const float * lat, int64_t B, int64_t h, int64_t w, bool shortcut, float * out,
+                   hipStream_t s) {
+    for (const char * n : {"decoder.conv_in.weight", "decoder.conv_in.bias"})
+        if (!v->loaded.count(n)) throw_err(SANA_ERR_STATE, std::string("vae weight not set: ") + n);
+    if (B <= 0 || h <= 0 || w <= 0) throw_err(SANA_ERR_INVALID_ARGUMENT, "vae decoder input: empty latent");
+    const int64_t top = v->lv[v->L - 1]->C, clp = round_up(v->Cl, 64), rep = top / v->Cl;
+    v->lat16.ensure((size_t)(B * (h + 2) * (w + 2) * clp) * 2, false);
+    v->x32.ensure((size_t)(B * h * w * top) * 4, false);
+    const int64_t n = std::max<int64_t>(B * (h + 2) * (w + 2) * clp, B * h * w * top);
+    hipLaunchKernelGGL(vae_prep_kernel, dim3(blocks_for(n)), dim3(256), 0, s, lat, (int)B, (int)v->Cl, (int)h, (int)w,
+                       1.0f, v->lat16.as<f16>(), (int)clp, v->x32.as<float>(), (int)top, (int)rep, shortcut ? 1 : 0);
+    launch_check(hipGetLastError(), "vae prep");
+    gemm_conv(1, v->lat16.as<half_t>(), clp, v->cin_w, B, h, w, top, v->cin_b.as<float>(), sana::kActNone, true,
+              v->x32.as<float>(), nullptr, false, nullptr, s);
+    hipLaunchKernelGGL(vae_to_nchw_kernel, dim3(blocks_for(B * top * h * w)), dim3(256), 0, s, v->x32.as<float>(), out,
+                       (int)B, (int)top, (int)h, (int)w);
     launch_check(hipGetLastError(), "vae to nchw");
 }
 
@@ -834,6 +859,23 @@ int sana_vae_decode_device(sana_vae * v, const float * latent, int64_t B, int64_
     return guarded([&] {
         hip_check(hipSetDevice(v->device), "hipSetDevice");
         decode(v, latent, B, H, W, image, static_cast<hipStream_t>(stream));
+    });
+}
+
+int sana_vae_decoder_input(sana_vae * v, const float * latent, int64_t B, int64_t H, int64_t W, int in_shortcut,
+                           float * out) {
+    if (!v || !latent || !out) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] {
+        hip_check(hipSetDevice(v->device), "hipSetDevice");
+        if (B <= 0 || H <= 0 || W <= 0) throw_err(SANA_ERR_INVALID_ARGUMENT, "vae decoder input: empty latent");
+        const int64_t top = v->lv[v->L - 1]->C;
+        const size_t nl = (size_t)(B * v->Cl * H * W), no = (size_t)(B * top * H * W);
+        DevMem dl, dout;
+        dl.ensure(nl * 4, false);
+        dout.ensure(no * 4, false);
+        hip_check(hipMemcpy(dl.p, latent, nl * 4, hipMemcpyHostToDevice), "hipMemcpy latent");
+        decoder_input(v, dl.as<float>(), B, H, W, in_shortcut != 0, dout.as<float>(), nullptr);
+        hip_check(hipMemcpy(out, dout.p, no * 4, hipMemcpyDeviceToHost), "hipMemcpy decoder input");
     });
 }
 

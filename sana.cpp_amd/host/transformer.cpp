@@ -26,6 +26,7 @@
 
 #include "../../include/sana_dit.h"
 #include "../csrc/gguf.h"
+#include "fingerprint.h"
 
 namespace {
 
@@ -63,33 +64,10 @@ std::vector<int64_t> shape64(const Tensor & t) {
 
 // ---------------------------------------------------------------- fingerprints
 
-void mix(uint64_t & h, uint64_t v) {
-    h ^= v;
-    h *= 1099511628211ULL;
-}
-
-// Storage address, shape and values (all of them up to 4096, else 64 spread
-// samples plus the last) of one tensor.
-void fingerprint(uint64_t & h, const Tensor & t) {
-    const std::vector<float> & d = t.data();
-    mix(h, static_cast<uint64_t>(reinterpret_cast<uintptr_t>(d.data())));
-    mix(h, t.rank());
-    for (size_t s : t.shape()) mix(h, s);
-    const size_t n = d.size(), step = n <= 4096 ? 1 : n / 64;
-    for (size_t i = 0; i < n; i += step) {
-        uint32_t b;
-        std::memcpy(&b, &d[i], 4);
-        mix(h, b);
-    }
-    if (n) {
-        uint32_t b;
-        std::memcpy(&b, &d[n - 1], 4);
-        mix(h, b);
-    }
-}
+using sana_fp::mix;
 
 uint64_t block_fingerprint(const SanaBlockWeights * blocks, size_t count) {
-    uint64_t h = 14695981039346656037ULL;
+    uint64_t h = sana_fp::kSeed;
     mix(h, count);
     for (size_t i = 0; i < count; ++i) {
         const SanaBlockWeights & w = blocks[i];
@@ -99,7 +77,7 @@ uint64_t block_fingerprint(const SanaBlockWeights * blocks, size_t count) {
               &w.cross_k_weight, &w.cross_k_bias, &w.cross_v_weight, &w.cross_v_bias, &w.cross_out_weight,
               &w.cross_out_bias, &w.mlp_norm_gamma, &w.mlp_norm_beta, &w.ff_inverted_weight, &w.ff_inverted_bias,
               &w.ff_depth_weight, &w.ff_depth_bias, &w.ff_point_weight})
-            fingerprint(h, *t);
+            sana_fp::tensor(h, *t);
         mix(h, w.self_num_heads);
         mix(h, w.cross_num_heads);
     }
@@ -107,14 +85,14 @@ uint64_t block_fingerprint(const SanaBlockWeights * blocks, size_t count) {
 }
 
 uint64_t top_fingerprint(const SanaDenoiserWeights & w) {
-    uint64_t h = 14695981039346656037ULL;
+    uint64_t h = sana_fp::kSeed;
     for (const Tensor * t :
          {&w.caption.linear_1_weight, &w.caption.linear_1_bias, &w.caption.linear_2_weight, &w.caption.linear_2_bias,
           &w.patch_embed_weight, &w.patch_embed_bias, &w.time_embed_linear_1_weight, &w.time_embed_linear_1_bias,
           &w.time_embed_linear_2_weight, &w.time_embed_linear_2_bias, &w.time_projection_weight,
           &w.time_projection_bias, &w.caption_norm_weight, &w.final_scale_shift_table, &w.proj_out_weight,
           &w.proj_out_bias})
-        fingerprint(h, *t);
+        sana_fp::tensor(h, *t);
     return h;
 }
 

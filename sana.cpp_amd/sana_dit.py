@@ -87,6 +87,7 @@ PROTOTYPES = {
     "sana_vae_check_weights": (ctypes.c_int, [_vp]),
     "sana_vae_load_gguf": (ctypes.c_int, [_vp, ctypes.c_char_p]),
     "sana_vae_decode": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp]),
+    "sana_vae_decoder_input": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "sana_vae_decode_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "sana_op_gemm_f32": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, ctypes.c_int, _vp, _i64,
                                         _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
@@ -302,6 +303,40 @@ def manifest(layers=28, hidden=1152, ffn=5760, caption_dim=2304, latent_channels
     return shapes
 
 
+def vae_manifest(channels, attention, latent_channels=32, head_dim=32, expand=4):
+    """{GGUF tensor name: PyTorch-order shape} of the DC-AE decoder weights the
+    loader reads (src/vae.cpp:10-118): conv_in / norm_out / conv_out, then per
+    up block an upsample conv (all but the innermost block) and three ResBlocks
+    or three EfficientViT layers (multiscale attention + GLUMBConv)."""
+    L, top, out = len(channels), channels[-1], channels[0]
+    shapes = {"decoder.conv_in.weight": (top, latent_channels, 3, 3), "decoder.conv_in.bias": (top,),
+              "decoder.norm_out.weight": (out,), "decoder.norm_out.bias": (out,),
+              "decoder.conv_out.weight": (3, out, 3, 3), "decoder.conv_out.bias": (3,)}
+    for i, C in enumerate(channels):
+        p = f"decoder.up_blocks.{i}."
+        base = 0
+        if i + 1 < L:
+            shapes.update({p + "0.conv.weight": (C, channels[i + 1], 3, 3), p + "0.conv.bias": (C,)})
+            base = 1
+        for l in range(base, base + 3):
+            q = f"{p}{l}."
+            if not attention[i]:
+                shapes.update({q + "conv1.weight": (C, C, 3, 3), q + "conv1.bias": (C,),
+                               q + "conv2.weight": (C, C, 3, 3), q + "norm.weight": (C,), q + "norm.bias": (C,)})
+            else:
+                E = expand * C
+                shapes.update({
+                    q + "attn.to_q.weight": (C, C), q + "attn.to_k.weight": (C, C), q + "attn.to_v.weight": (C, C),
+                    q + "attn.to_qkv_multiscale.0.proj_in.weight": (3 * C, 1, 5, 5),
+                    q + "attn.to_qkv_multiscale.0.proj_out.weight": (3 * C, head_dim, 1, 1),
+                    q + "attn.to_out.weight": (C, 2 * C), q + "attn.norm_out.weight": (C,),
+                    q + "attn.norm_out.bias": (C,), q + "conv_out.conv_inverted.weight": (2 * E, C, 1, 1),
+                    q + "conv_out.conv_inverted.bias": (2 * E,), q + "conv_out.conv_depth.weight": (2 * E, 1, 3, 3),
+                    q + "conv_out.conv_depth.bias": (2 * E,), q + "conv_out.conv_point.weight": (C, E, 1, 1),
+                    q + "conv_out.norm.weight": (C,), q + "conv_out.norm.bias": (C,)})
+    return shapes
+
+
 class Vae:
     """One device context of the DC-AE VAE decoder (weights and workspace).
 
@@ -321,10 +356,11 @@ class Vae:
         h = _vp()
         check(lib().sana_vae_create(ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
+        self._destroy = lib().sana_vae_destroy  # still callable during interpreter shutdown
 
     def close(self):
         if getattr(self, "h", None):
-            lib().sana_vae_destroy(self.h)
+            self._destroy(self.h)
             self.h = None
 
     def __del__(self):
@@ -347,6 +383,14 @@ class Vae:
         s = 2 ** (self.levels - 1)
         out = np.empty((B, 3, H * s, W * s), np.float32)
         check(lib().sana_vae_decode(self.h, ptr(latent), B, H, W, ptr(out)))
+        return out
+
+    def decoder_input(self, latent, in_shortcut=True):
+        """conv_in (+ channel-repeat shortcut) of an unscaled latent: [B, C_top, H, W]."""
+        latent = _f32(latent)
+        B, _, H, W = latent.shape
+        out = np.empty((B, self.cfg.channels[self.levels - 1], H, W), np.float32)
+        check(lib().sana_vae_decoder_input(self.h, ptr(latent), B, H, W, int(in_shortcut), ptr(out)))
         return out
 
     def decode_device(self, latent, shape, image, stream):

@@ -14,6 +14,11 @@
 //                            small model) against the oracle's tensors; with
 //                            `run`, also the denoise loop on the loaded weights
 //                            (GPU) against the oracle's loop
+//   dropin_test vae FILE [run]
+//                            vae.h: load_vae_weights on FILE (a GGUF of the
+//                            small synthetic DC-AE decoder) against the oracle's
+//                            tensors; with `run`, run_vae_decode and
+//                            run_vae_decoder_input on the GPU against the oracle
 //   dropin_test full-loop CAPTION LATENT STEPS OUT
 //                            the denoise stage of sana_infer on the seeded
 //                            Sana-0.6B model (28 blocks, 36/16 heads, guidance
@@ -37,6 +42,7 @@
 #include "torch_rng.h"
 #include "transformer.h"
 #include "transformer_ops.h"
+#include "vae.h"
 #include "weights_io.h"
 
 namespace {
@@ -706,6 +712,127 @@ int full_loop(const std::string & caption_path, const std::string & latent_path,
     return 0;
 }
 
+// ---------------------------------------------------------------- VAE (vae.h)
+
+SanaVaeWeights tiny_vae() {
+    SanaVaeDecoderWeights d{Tensor({8, 4, 3, 3}), Tensor({8}), Tensor({8}), Tensor({8}),
+                            Tensor({3, 8, 3, 3}), Tensor({3}), {}};
+    d.up_blocks.emplace_back();
+    return SanaVaeWeights{std::move(d), 0.5f, 32};
+}
+
+// Host-side vae.h: up block discovery and the validators' exception types
+// (src/vae.cpp:98-209); no GPU call.
+void vae_host_tests() {
+    std::unordered_map<std::string, SavedWeightInfo> idx;
+    for (const char * n : {"decoder.up_blocks.10.0.conv.weight", "decoder.up_blocks.2.1.conv1.weight",
+                           "decoder.up_blocks.2.0.conv.weight", "decoder.up_blocks.x.0.w", "decoder.up_blocks..w",
+                           "decoder.up_blocks.3", "decoder.conv_in.weight", "encoder.up_blocks.1.w"})
+        idx[n] = SavedWeightInfo{};
+    check(find_vae_decoder_up_block_prefixes(idx) == std::vector<std::string>{"decoder.up_blocks.2",
+                                                                               "decoder.up_blocks.10"},
+          "up block prefixes: numeric order, malformed names skipped");
+    validate_vae_weights(tiny_vae());
+    check(true, "a well-formed decoder validates");
+    auto bad = [](const std::function<void(SanaVaeWeights &)> & f, const std::string & what) {
+        SanaVaeWeights w = tiny_vae();
+        f(w);
+        throws<std::invalid_argument>([&] { validate_vae_weights(w); }, what);
+    };
+    bad([](SanaVaeWeights & w) { w.decoder.conv_in_weight = Tensor({8, 4, 3}); }, "conv_in rank");
+    bad([](SanaVaeWeights & w) { w.decoder.up_blocks.clear(); }, "no up blocks");
+    bad([](SanaVaeWeights & w) { w.decoder.conv_in_bias = Tensor({7}); }, "conv_in bias size");
+    bad([](SanaVaeWeights & w) { w.decoder.conv_out_weight = Tensor({3, 6, 3, 3}); }, "norm_out vs conv_out");
+    bad([](SanaVaeWeights & w) { w.scaling_factor = 0.0f; }, "scaling factor");
+    bad([](SanaVaeWeights & w) { w.spatial_compression_ratio = 0; }, "compression ratio");
+    const SanaVaeWeights w = tiny_vae();
+    throws<std::invalid_argument>([&] { run_vae_decode(Tensor({1, 4, 8}), w); }, "decode of a rank-3 latent");
+    throws<std::invalid_argument>([&] { run_vae_decode(Tensor({1, 5, 2, 2}), w); }, "decode latent channels");
+    throws<std::invalid_argument>([&] { run_vae_decoder_input(Tensor({1, 5, 2, 2}), w.decoder); },
+                                  "decoder input channels");
+    check(run_vae_decode(Tensor({0, 4, 2, 2}), w).shape() == std::vector<size_t>({0, 3, 2, 2}),
+          "empty batch decodes to an empty image");
+}
+
+Tensor oracle_vae_tensor(const oracle_vae * o, const std::string & name, std::vector<size_t> shape) {
+    Tensor t(std::move(shape));
+    check(oracle_vae_get(o, name.c_str(), t.data().data(), t.numel()) == 0, "oracle tensor " + name);
+    return t;
+}
+
+Tensor wave_latent(std::vector<size_t> shape, float phase) {
+    Tensor t(std::move(shape));
+    for (size_t i = 0; i < t.numel(); ++i) t.data()[i] = std::sin(0.37f * static_cast<float>(i) + phase) * 1.3f;
+    return t;
+}
+
+// load_vae_weights on a GGUF of the small synthetic decoder (64/64/128/128,
+// ResBlocks at the two outer levels), then the device decode against the oracle.
+void vae_tests(const std::string & path, bool run) {
+    const auto idx = load_weight_index(path);
+    const auto prefixes = find_vae_decoder_up_block_prefixes(idx);
+    check(prefixes.size() == 4 && prefixes[0] == "decoder.up_blocks.0" && prefixes[3] == "decoder.up_blocks.3",
+          "four up block prefixes");
+    SanaVaeWeights w = load_vae_weights("", idx, 0.41407f, 32);
+    validate_vae_weights(w);
+    const auto & ub = w.decoder.up_blocks;
+    check(ub.size() == 4 && ub[0].is_res_block && ub[1].is_res_block && !ub[2].is_res_block && !ub[3].is_res_block,
+          "res / attention up blocks");
+    check(ub[2].upsample_conv_weight.has_value() && !ub[3].upsample_conv_weight.has_value(),
+          "the innermost block has no upsample");
+    check(ub[0].res_blocks.size() == 3 && ub[3].attn_glumb_layers.size() == 3, "three layers per block");
+    check(ub[3].attn_glumb_layers[0].attention.to_q_weight_conv1x1.shape() == std::vector<size_t>({128, 128, 1, 1}),
+          "attention linears in conv 1x1 form");
+    oracle_vae * o = oracle_vae_create(0);
+    check(oracle_vae_generate(o) == 0, "oracle weights");
+    auto same = [&](const Tensor & t, const std::string & n, std::vector<size_t> shape) {
+        const Tensor r = oracle_vae_tensor(o, n, std::move(shape));
+        check(t.data() == r.data(), "loaded tensor " + n);
+    };
+    same(w.decoder.conv_in_weight, "decoder.conv_in.weight", {128, 32, 3, 3});
+    same(w.decoder.conv_out_bias, "decoder.conv_out.bias", {3});
+    same(*ub[1].upsample_conv_weight, "decoder.up_blocks.1.0.conv.weight", {64, 128, 3, 3});
+    same(ub[0].res_blocks[2].conv2_weight, "decoder.up_blocks.0.3.conv2.weight", {64, 64, 3, 3});
+    same(ub[3].attn_glumb_layers[1].attention.to_out_weight_conv1x1, "decoder.up_blocks.3.1.attn.to_out.weight",
+         {128, 256});
+    same(ub[2].attn_glumb_layers[2].glumb.conv_depth_weight, "decoder.up_blocks.2.3.conv_out.conv_depth.weight",
+         {1024, 1, 3, 3});
+    if (run) {
+        for (const auto & shape : {std::vector<size_t>{1, 32, 8, 8}, std::vector<size_t>{2, 32, 4, 6}}) {
+            const Tensor lat = wave_latent(shape, 0.3f);
+            const size_t B = shape[0], H = shape[2], W = shape[3];
+            const Tensor img = run_vae_decode(lat, w);
+            check(img.shape() == std::vector<size_t>({B, 3, 8 * H, 8 * W}), "decoded image shape");
+            Tensor ref({B, 3, 8 * H, 8 * W});
+            check(oracle_vae_decode(o, lat.data().data(), B, H, W, ref.data().data()) == 0, "oracle decode");
+            close_l2(img.data(), ref.data(), 2e-3, "run_vae_decode " + std::to_string(B) + "x" + std::to_string(H) +
+                                                       "x" + std::to_string(W));
+            check(run_vae_decode(lat, w).data() == img.data(), "second decode (resident weights) is identical");
+        }
+        // run_vae_decoder_input takes the latent already divided by the scaling factor
+        const Tensor lat = wave_latent({1, 32, 5, 7}, 1.1f);
+        Tensor scaled = lat;
+        for (float & v : scaled.data()) v *= 1.0f / 0.41407f;
+        Tensor ref({1, 128, 5, 7});
+        check(oracle_vae_decoder_input(o, lat.data().data(), 1, 5, 7, ref.data().data()) == 0, "oracle conv_in");
+        close_l2(run_vae_decoder_input(scaled, w.decoder).data(), ref.data(), 2e-3, "run_vae_decoder_input");
+        // a refilled weight is uploaded again: conv_out bias + 1 shifts channel 0 by 1
+        const Tensor lat2 = wave_latent({1, 32, 4, 4}, 0.7f);
+        const Tensor before = run_vae_decode(lat2, w);
+        w.decoder.conv_out_bias.data()[0] += 1.0f;
+        const Tensor after = run_vae_decode(lat2, w);
+        float dev0 = 0.0f, dev12 = 0.0f;
+        const size_t hw = 32 * 32;
+        for (size_t i = 0; i < 3 * hw; ++i) {
+            const float d = after.data()[i] - before.data()[i];
+            if (i < hw) dev0 = std::max(dev0, std::fabs(d - 1.0f));
+            else dev12 = std::max(dev12, std::fabs(d));
+        }
+        check(dev0 < 1e-4f && dev12 == 0.0f, "refilled conv_out bias re-uploaded");
+    }
+    oracle_vae_destroy(o);
+}
+
 }  // namespace
 
 int main(int argc, char ** argv) {
@@ -716,6 +843,7 @@ int main(int argc, char ** argv) {
             scheduler_tests();
             transformer_host_tests();
             rng_tests();
+            vae_host_tests();
         } else if (mode == "gpu") {
             gpu_kat_tests();
             gpu_small_model_tests();
@@ -724,10 +852,12 @@ int main(int argc, char ** argv) {
             ops_random_tests();
         } else if (mode == "gguf" && argc > 2) {
             gguf_tests(argv[2], argc > 3 && std::string(argv[3]) == "run");
+        } else if (mode == "vae" && argc > 2) {
+            vae_tests(argv[2], argc > 3 && std::string(argv[3]) == "run");
         } else if (mode == "full-loop" && argc > 5) {
             full_loop(argv[2], argv[3], std::strtoul(argv[4], nullptr, 10), argv[5]);
         } else {
-            std::fprintf(stderr, "usage: dropin_test cpu | gpu | ops | gguf FILE [run] | full-loop CAPTION LATENT STEPS OUT\n");
+            std::fprintf(stderr, "usage: dropin_test cpu | gpu | ops | gguf FILE [run] | vae FILE [run] | full-loop CAPTION LATENT STEPS OUT\n");
             return 2;
         }
     } catch (const std::exception & e) {

@@ -49,3 +49,25 @@ def test_create_rejects_bad_config_without_gpu():
     rc = sana_dit.lib().sana_dit_create(ctypes.byref(cfg), ctypes.byref(h))
     assert rc == sana_dit.SANA_ERR_INVALID_ARGUMENT
     assert b"divisible" in sana_dit.lib().sana_dit_last_error()
+
+
+def test_vae_create_rejects_bad_config_without_gpu():
+    for channels, attn, msg in (((96,), (0,), b"multiples of 64"), ((64, 192), (0, 0), b"shortcut")):
+        cfg = sana_dit.VaeConfig()
+        cfg.latent_channels, cfg.levels, cfg.head_dim, cfg.expand = 32, len(channels), 32, 4
+        cfg.scaling_factor, cfg.device = 0.41407, 0
+        for i, c in enumerate(channels):
+            cfg.channels[i], cfg.attention[i] = c, attn[i]
+        h = ctypes.c_void_p()
+        rc = sana_dit.lib().sana_vae_create(ctypes.byref(cfg), ctypes.byref(h))
+        assert rc == sana_dit.SANA_ERR_INVALID_ARGUMENT
+        assert msg in sana_dit.lib().sana_dit_last_error()
+
+
+def test_vae_manifest_matches_the_reference_weight_set():
+    # the oracle's manifest is pinned name by name against the reference loader
+    # (tests/golden/vae_weights.npz, tests/test_oracle_vae.py)
+    import oracle_lib as O
+    for cfg in (O.FULL_VAE, O.SMALL_VAE):
+        got = sana_dit.vae_manifest(cfg["channels"], cfg["attn"], cfg["latent"])
+        assert got == {k: tuple(v) for k, v in O.vae_manifest(cfg).items()}

@@ -43,6 +43,21 @@ def small_gguf(path, ggml_type=GGML_F32):
     return m, names
 
 
+def small_vae_gguf(path, ggml_type=GGML_F32):
+    v = O.Vae(full=False)
+    write_gguf(path, {n: v.get(n, s) for n, s in O.vae_manifest(v.cfg).items()}, ggml_type=ggml_type)
+    return v
+
+
+def test_dropin_vae_loaders(tmp_path):
+    """vae.h: find_vae_decoder_up_block_prefixes + load_vae_weights on a GGUF of
+    the small synthetic decoder, tensors compared with the oracle's (no GPU)."""
+    path = str(tmp_path / "vae_small.gguf")
+    small_vae_gguf(path)
+    res = run_exe("vae", path, timeout=120)
+    assert res.returncode == 0 and " 0 failures" in res.stdout
+
+
 def test_dropin_host_api():
     res = run_exe("cpu", timeout=120)
     assert res.returncode == 0 and " 0 failures" in res.stdout
@@ -145,6 +160,36 @@ def test_dropin_loop_on_gguf_weights(tmp_path):
     small_gguf(path)
     res = run_exe("gguf", path, "run", timeout=110)
     assert res.returncode == 0 and " 0 failures" in res.stdout
+
+
+@pytest.mark.gpu
+def test_dropin_vae_decode(tmp_path):
+    """run_vae_decode / run_vae_decoder_input of vae.h on GGUF-loaded weights
+    against the oracle (rel-L2 2e-3), resident-weight reuse and re-upload."""
+    path = str(tmp_path / "vae_small.gguf")
+    small_vae_gguf(path)
+    res = run_exe("vae", path, "run", timeout=110)
+    assert res.returncode == 0 and " 0 failures" in res.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ggml_type", [GGML_F32, GGML_F16])
+def test_vae_load_gguf_abi_decode(tmp_path, ggml_type):
+    """sana_vae_load_gguf, then a decode against the oracle on the same
+    (for F16: the same rounded) weights."""
+    path = str(tmp_path / "vae_small.gguf")
+    v = small_vae_gguf(path, ggml_type)
+    if ggml_type == GGML_F16:
+        for n, s in O.vae_manifest(v.cfg).items():
+            v.set(n, v.get(n, s).astype(np.float16).astype(np.float32))
+    dev = sana_dit.Vae(v.cfg["channels"], v.cfg["attn"])
+    try:
+        dev.load_gguf(path)
+        dev.check_weights()
+        lat = O.randn((1, 32, 6, 6), 5)
+        assert rel_l2(dev.decode(lat), v.decode(lat)) < 2e-3
+    finally:
+        dev.close()
 
 
 @pytest.mark.gpu

@@ -126,3 +126,25 @@ def test_full_decoder_vs_reference():
         assert norm_err < TOL
     finally:
         dev.close()
+
+
+def test_decoder_input_stage():
+    """run_vae_decoder_input: conv_in of the (already scaled) latent, with and
+    without the channel-repeat shortcut; needs only the conv_in tensors."""
+    import sana_dit
+    ora = O.Vae(cfg=CONFIGS["up2"])
+    dev = sana_dit.Vae(ora.cfg["channels"], ora.cfg["attn"])
+    try:
+        for name in ("decoder.conv_in.weight", "decoder.conv_in.bias"):
+            dev.set_weight(name, ora.get(name))
+        lat = O.randn((2, 32, 5, 7), 3)
+        scaled = lat * (np.float32(1.0) / np.float32(0.41407))
+        ref = ora.decoder_input(lat)                     # scales, conv_in, + shortcut
+        got = dev.decoder_input(scaled)
+        assert got.shape == (2, 128, 5, 7)
+        assert rel_l2(got, ref) < TOL
+        rep = 128 // 32
+        short = np.repeat(scaled, rep, axis=1)           # channel oc reads latent channel oc // rep
+        assert rel_l2(dev.decoder_input(scaled, in_shortcut=False), ref - short) < TOL
+    finally:
+        dev.close()
