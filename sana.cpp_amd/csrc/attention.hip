@@ -822,14 +822,14 @@ bool linear_attention_fused_ok(int N, int D) { return D == 32 && N > 0 && N % 16
 
 
 hipError_t linear_attention_fused(const half_t * q, int64_t ldq, const half_t * kt, const half_t * vt, half_t * out,
-                                  int64_t ldo, int B, int N, int H, int D, hipStream_t s) {
+                                  int64_t ldo, int B, int N, int H, int D, hipStream_t s, int co) {
     if (!linear_attention_fused_ok(N, D) || B <= 0 || H <= 0 || ldq < (int64_t)H * D || ldo < (int64_t)H * D ||
         ldq % 8 || ldo % 8 || (int64_t)B * H > 65535 ||
         ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kt) | reinterpret_cast<uintptr_t>(vt)) & 15) ||
         (reinterpret_cast<uintptr_t>(out) & 15))
         return hipErrorInvalidValue;
     // enough workgroups for the 256 CUs: (b, h) pairs times token splits
-    const int splits = (int)std::max<int64_t>(1, std::min<int64_t>(8, 256 / ((int64_t)B * H)));
+    const int splits = (int)std::max<int64_t>(1, std::min<int64_t>(8, 256 / ((int64_t)B * H * std::max(co, 1))));
     hipLaunchKernelGGL(la_fused_kernel, dim3((unsigned)(B * H * splits)), dim3(64 * kLfWaves), 0, s,
                        reinterpret_cast<const f16 *>(q), ldq, reinterpret_cast<const f16 *>(kt),
                        reinterpret_cast<const f16 *>(vt), reinterpret_cast<f16 *>(out), ldo, N, H, splits);

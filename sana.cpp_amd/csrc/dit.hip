@@ -86,6 +86,10 @@ struct sana_dit {
     int64_t C = 0, E = 0, F = 0, Ccap = 0, Cl = 0, L_ = 0, Hs = 0, Hc = 0, Ds = 0, Dc = 0;
     int64_t Cp = 0, Fp = 0, Ccap_p = 0;  // K-padded row strides of GEMM operands
     hipStream_t stream = nullptr;
+    // second branch of a CFG-split forward (the conditional batch row) and
+    // its fork / join events; same (default) priority as `stream`
+    hipStream_t stream2 = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::vector<std::unique_ptr<BlockDev>> blocks;
     DevMem w_k_all, b_k_all, w_v_all, b_v_all, sst_all;  // stacked over blocks
     DevMem w_cap1, b_cap1, w_cap2, b_cap2, cap_norm;
@@ -98,8 +102,8 @@ struct sana_dit {
     // forward workspace
     int64_t ws_M = 0, ws_B = 0;
     DevMem la_kt, la_vt;  // relu(K)^T and V^T per channel, token-contiguous (fused linear attention)
-    DevMem x32, fin32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, d_t, tp, e1, emb, tmod, mod_all, lat_in,
-        np_out;
+    DevMem x32, fin32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, la_ws2, d_t, tp, e1, emb, tmod, mod_all,
+        lat_in, np_out;
     DevMem loop_lat[2], loop_x0[2];  // denoise loop: latent ping-pong and converted-output history
     // graphs keyed by (kind, Bl, H, W, L, pointers)
     std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, const void *, const void *, const void *, const void *>,
@@ -111,6 +115,9 @@ struct sana_dit {
     ~sana_dit() {
         for (auto & kv : graphs)
             if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+        if (ev_fork) (void)hipEventDestroy(ev_fork);
+        if (ev_join) (void)hipEventDestroy(ev_join);
+        if (stream2) (void)hipStreamDestroy(stream2);
         if (stream) (void)hipStreamDestroy(stream);
     }
 };
@@ -163,9 +170,11 @@ void expect_shape(const char * name, const int64_t * shape, int ndim, std::vecto
 // ---------------------------------------------------------------- forward pieces
 // The fused q | k | v projection of the linear-attention path (kGemmQKV):
 // relu(q) token-major into qkv16 (ld 3C), relu(K)^T and V^T into la_kt / la_vt.
-void gemm_qkv_split(sana_dit * c, BlockDev & w, int64_t B, int64_t N, hipStream_t s) {
+void gemm_qkv_split(sana_dit * c, BlockDev & w, int64_t B, int64_t N, const half_t * xa16, half_t * qkv16,
+                    half_t * kt16, half_t * vt16, int co, hipStream_t s) {
     sana::GemmParams p;
-    p.A = c->xa16.as<half_t>();
+    p.co = co;
+    p.A = xa16;
     p.lda = c->Cp;
     p.W = w.w_qkv.as<half_t>();
     p.ldw = c->Cp;
@@ -174,10 +183,10 @@ void gemm_qkv_split(sana_dit * c, BlockDev & w, int64_t B, int64_t N, hipStream_
     p.K = (int)c->Cp;
     p.bias = w.has_qkv_bias ? w.b_qkv.as<float>() : nullptr;
     p.mode = sana::kGemmQKV;
-    p.out16 = c->qkv16.as<half_t>();
+    p.out16 = qkv16;
     p.ldo16 = 3 * c->C;
-    p.kt16 = c->la_kt.as<half_t>();
-    p.vt16 = c->la_vt.as<half_t>();
+    p.kt16 = kt16;
+    p.vt16 = vt16;
     p.qkv_c = (int)c->C;
     p.qkv_n = (int)N;
     launch_check(sana::gemm(p, s), "gemm_qkv");
@@ -190,8 +199,9 @@ bool fused_linear_attention(const sana_dit * c, int64_t N) {
 
 void gemm_store(sana_dit * c, const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N,
                 int64_t K, const float * bias, int act, half_t * o16, int64_t ldo16, float * o32, int64_t ldo32,
-                hipStream_t s) {
+                hipStream_t s, int co = 1) {
     sana::GemmParams p;
+    p.co = co;
     p.A = A;
     p.lda = lda;
     p.W = W;
@@ -212,8 +222,9 @@ void gemm_store(sana_dit * c, const half_t * A, int64_t lda, const half_t * W, i
 
 void gemm_resid(const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
                 const float * bias, const float * gate_a, const float * gate_t, int64_t gate_stride, int64_t rpb,
-                float * x, int64_t ldx, half_t * o16, int64_t ldo16, hipStream_t s) {
+                float * x, int64_t ldx, half_t * o16, int64_t ldo16, hipStream_t s, int co = 1) {
     sana::GemmParams p;
+    p.co = co;
     p.A = A;
     p.lda = lda;
     p.W = W;
@@ -307,6 +318,7 @@ void ensure_forward_buffers(sana_dit * c, int64_t B, int64_t N) {
         c->hid16.ensure((size_t)M * c->E * 2);
         c->glu16.ensure((size_t)M * c->Fp * 2);
         c->la_ws.ensure(sana::linattn_workspace_floats((int)B, (int)N, (int)c->Hs, (int)c->Ds) * 4);
+        c->la_ws2.ensure(sana::linattn_workspace_floats(1, (int)N, (int)c->Hs, (int)c->Ds) * 4);
         c->d_t.ensure((size_t)B * 4);
         c->tp.ensure((size_t)B * 256 * 4);
         c->e1.ensure((size_t)B * C * 4);
@@ -346,61 +358,83 @@ void enqueue_time(sana_dit * c, int64_t B, hipStream_t s) {
 // Stage hook: called after each stage of a block (0 self, 1 cross, 2 ff).
 typedef void (*StageHook)(void *, int);
 
+// One block on batch rows [b0, b0 + B) of a Btot-row batch (the whole batch
+// by default); co is the number of such launches running concurrently on
+// other streams (tile choice).
 void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * xbias, hipStream_t s,
-                   StageHook hook = nullptr, void * hook_ctx = nullptr) {
+                   StageHook hook = nullptr, void * hook_ctx = nullptr, int64_t b0 = 0, int64_t Btot = -1,
+                   int co = 1) {
     BlockDev & w = *c->blocks[i];
-    const int64_t C = c->C, M = B * N, side = (int64_t)std::llround(std::sqrt((double)N));
-    // modulation rows of this block: [B][6C] = shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp
-    const float * mod = c->mod_all.as<float>() + (size_t)i * B * 6 * C;
+    if (Btot < 0) Btot = B;
+    const int64_t C = c->C, M = B * N, side = (int64_t)std::llround(std::sqrt((double)N)), r0 = b0 * N;
+    const int64_t Lc = c->ctx_L;
+    float * x32 = c->x32.as<float>() + r0 * C;
+    half_t * xa16 = c->xa16.as<half_t>() + r0 * c->Cp;
+    half_t * qkv16 = c->qkv16.as<half_t>() + r0 * 3 * C;
+    half_t * o16 = c->o16.as<half_t>() + r0 * c->Cp;
+    half_t * r16 = c->r16.as<half_t>() + r0 * c->Cp;
+    half_t * q16 = c->q16.as<half_t>() + r0 * C;
+    half_t * hid16 = c->hid16.as<half_t>() + r0 * c->E;
+    half_t * glu16 = c->glu16.as<half_t>() + r0 * c->Fp;
+    // modulation rows of this block: [Btot][6C] = shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp
+    const float * mod = c->mod_all.as<float>() + ((size_t)i * Btot + b0) * 6 * C;
     // self attention: LN + modulate(shift_msa, scale_msa)
-    launch_check(sana::ln_modulate(c->x32.as<float>(), C, c->xa16.as<half_t>(), c->Cp, (int)M, (int)C, (int)N, 1e-6f,
+    launch_check(sana::ln_modulate(x32, C, xa16, c->Cp, (int)M, (int)C, (int)N, 1e-6f,
                                    w.has_ln1 ? w.ln1_g.as<float>() : nullptr, w.has_ln1 ? w.ln1_b.as<float>() : nullptr,
                                    mod, nullptr, 6 * C, 0, C, s),
                  "ln_modulate");
     if (fused_linear_attention(c, N)) {
-        gemm_qkv_split(c, w, B, N, s);
-        launch_check(sana::linear_attention_fused(c->qkv16.as<half_t>(), 3 * C, c->la_kt.as<half_t>(),
-                                                  c->la_vt.as<half_t>(), c->o16.as<half_t>(), c->Cp, (int)B, (int)N,
-                                                  (int)c->Hs, (int)c->Ds, s),
+        half_t * kt16 = c->la_kt.as<half_t>() + b0 * C * N;
+        half_t * vt16 = c->la_vt.as<half_t>() + b0 * C * N;
+        gemm_qkv_split(c, w, B, N, xa16, qkv16, kt16, vt16, co, s);
+        launch_check(sana::linear_attention_fused(qkv16, 3 * C, kt16, vt16, o16, c->Cp, (int)B, (int)N, (int)c->Hs,
+                                                  (int)c->Ds, s, co),
                      "linear_attention_fused");
     } else {
-        gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
-                   w.has_qkv_bias ? w.b_qkv.as<float>() : nullptr, sana::kActNone, c->qkv16.as<half_t>(), 3 * C,
-                   nullptr, 0, s);
-        const half_t * qkv = c->qkv16.as<half_t>();
-        launch_check(sana::linear_attention(qkv, qkv + C, qkv + 2 * C, 3 * C, c->o16.as<half_t>(), c->Cp, (int)B,
-                                            (int)N, (int)c->Hs, (int)c->Ds, c->la_ws.as<float>(), s),
+        gemm_store(c, xa16, c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
+                   w.has_qkv_bias ? w.b_qkv.as<float>() : nullptr, sana::kActNone, qkv16, 3 * C, nullptr, 0, s, co);
+        float * ws = (b0 > 0 && B == 1) ? c->la_ws2.as<float>() : c->la_ws.as<float>();
+        launch_check(sana::linear_attention(qkv16, qkv16 + C, qkv16 + 2 * C, 3 * C, o16, c->Cp, (int)B, (int)N,
+                                            (int)c->Hs, (int)c->Ds, ws, s),
                      "linear_attention");
     }
     // x += gate_msa * (o Wo^T + bo); r16 = fp16(x) for the cross-attention query
-    gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_out.as<half_t>(), c->Cp, M, C, c->Cp, w.b_out.as<float>(),
-               mod + 2 * C, nullptr, 6 * C, N, c->x32.as<float>(), C, c->r16.as<half_t>(), c->Cp, s);
+    gemm_resid(o16, c->Cp, w.w_out.as<half_t>(), c->Cp, M, C, c->Cp, w.b_out.as<float>(), mod + 2 * C, nullptr, 6 * C,
+               N, x32, C, r16, c->Cp, s, co);
     if (hook) hook(hook_ctx, 0);
     // cross attention
-    gemm_store(c, c->r16.as<half_t>(), c->Cp, w.w_cq.as<half_t>(), c->Cp, M, C, c->Cp, w.b_cq.as<float>(),
-               sana::kActNone, c->q16.as<half_t>(), C, nullptr, 0, s);
-    const half_t * kc = c->kc.as<half_t>() + i * C;
-    const half_t * vt = c->vt.as<half_t>() + (size_t)i * B * C * c->ctx_Lp;
-    launch_check(sana::cross_attention(c->q16.as<half_t>(), C, kc, c->L_ * C, vt, c->ctx_Lp,
-                                       xbias, c->o16.as<half_t>(), c->Cp, (int)B,
-                                       (int)N, (int)c->ctx_L, (int)c->Hc, (int)c->Dc, s),
+    gemm_store(c, r16, c->Cp, w.w_cq.as<half_t>(), c->Cp, M, C, c->Cp, w.b_cq.as<float>(), sana::kActNone, q16, C,
+               nullptr, 0, s, co);
+    const half_t * kc = c->kc.as<half_t>() + (size_t)b0 * Lc * c->L_ * C + i * C;
+    const half_t * vt = c->vt.as<half_t>() + ((size_t)i * Btot + b0) * C * c->ctx_Lp;
+    launch_check(sana::cross_attention(q16, C, kc, c->L_ * C, vt, c->ctx_Lp, xbias ? xbias + b0 * Lc : nullptr, o16,
+                                       c->Cp, (int)B, (int)N, (int)Lc, (int)c->Hc, (int)c->Dc, s),
                  "cross_attention");
-    gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_co.as<half_t>(), c->Cp, M, C, c->Cp, w.b_co.as<float>(), nullptr,
-               nullptr, 0, N, c->x32.as<float>(), C, nullptr, 0, s);
+    gemm_resid(o16, c->Cp, w.w_co.as<half_t>(), c->Cp, M, C, c->Cp, w.b_co.as<float>(), nullptr, nullptr, 0, N, x32, C,
+               nullptr, 0, s, co);
     if (hook) hook(hook_ctx, 1);
     // Mix-FFN
-    launch_check(sana::ln_modulate(c->x32.as<float>(), C, c->xa16.as<half_t>(), c->Cp, (int)M, (int)C, (int)N, 1e-6f,
+    launch_check(sana::ln_modulate(x32, C, xa16, c->Cp, (int)M, (int)C, (int)N, 1e-6f,
                                    w.has_ln2 ? w.ln2_g.as<float>() : nullptr, w.has_ln2 ? w.ln2_b.as<float>() : nullptr,
                                    mod, nullptr, 6 * C, 3 * C, 4 * C, s),
                  "ln_modulate");
-    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_inv.as<half_t>(), c->Cp, M, c->E, c->Cp, w.b_inv.as<float>(),
-               sana::kActSilu, c->hid16.as<half_t>(), c->E, nullptr, 0, s);
-    launch_check(sana::dwconv_glu(c->hid16.as<half_t>(), c->E, w.w_dw.as<float>(), w.b_dw.as<float>(),
-                                  c->glu16.as<half_t>(), c->Fp, (int)B, (int)side, (int)side, (int)c->F, s),
+    gemm_store(c, xa16, c->Cp, w.w_inv.as<half_t>(), c->Cp, M, c->E, c->Cp, w.b_inv.as<float>(), sana::kActSilu,
+               hid16, c->E, nullptr, 0, s, co);
+    launch_check(sana::dwconv_glu(hid16, c->E, w.w_dw.as<float>(), w.b_dw.as<float>(), glu16, c->Fp, (int)B,
+                                  (int)side, (int)side, (int)c->F, s),
                  "dwconv_glu");
-    gemm_resid(c->glu16.as<half_t>(), c->Fp, w.w_pt.as<half_t>(), c->Fp, M, C, c->Fp, nullptr, mod + 5 * C,
-               nullptr, 6 * C, N, c->x32.as<float>(), C, nullptr, 0, s);
+    gemm_resid(glu16, c->Fp, w.w_pt.as<half_t>(), c->Fp, M, C, c->Fp, nullptr, mod + 5 * C, nullptr, 6 * C, N, x32, C,
+               nullptr, 0, s, co);
     if (hook) hook(hook_ctx, 2);
+}
+
+// Whether a forward over the CFG pair runs its two batch rows as two
+// concurrent chains (graph branches): each kernel then covers half the rows,
+// and the two chains fill each other's launch gaps and tails and share the
+// weights through the caches.
+bool cfg_branches_enabled() {
+    const char * e = std::getenv("SANA_DIT_CFG_BRANCHES");
+    return !(e && e[0] == '0');
 }
 
 void enqueue_forward(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh, int64_t Ww, const float * xbias,
@@ -410,7 +444,20 @@ void enqueue_forward(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh,
                                    c->b_patch.as<float>(), c->x32.as<float>(), (int)c->C, s),
                  "patch_embed");
     enqueue_time(c, B, s);
-    for (int64_t i = 0; i < c->L_; ++i) enqueue_block(c, i, B, N, xbias, s);
+    if (B == 2 && cfg_branches_enabled()) {
+        // batch row 0 on s, row 1 on stream2, forked after the time embedding
+        // and joined before the final layer
+        hip_check(hipEventRecord(c->ev_fork, s), "hipEventRecord");
+        hip_check(hipStreamWaitEvent(c->stream2, c->ev_fork, 0), "hipStreamWaitEvent");
+        for (int64_t i = 0; i < c->L_; ++i) {
+            enqueue_block(c, i, 1, N, xbias, s, nullptr, nullptr, 0, 2, 2);
+            enqueue_block(c, i, 1, N, xbias, c->stream2, nullptr, nullptr, 1, 2, 2);
+        }
+        hip_check(hipEventRecord(c->ev_join, c->stream2), "hipEventRecord");
+        hip_check(hipStreamWaitEvent(s, c->ev_join, 0), "hipStreamWaitEvent");
+    } else {
+        for (int64_t i = 0; i < c->L_; ++i) enqueue_block(c, i, B, N, xbias, s);
+    }
     launch_check(sana::final_layer(c->x32.as<float>(), c->emb.as<float>(), c->sst_final.as<float>(),
                                    c->w_proj.as<float>(), c->b_proj.as<float>(), c->fin32.as<float>(), out, (int)B,
                                    (int)N, (int)c->C,
@@ -547,6 +594,9 @@ int sana_dit_create(const sana_dit_config * cfg, sana_dit ** out) {
         c->Ccap_p = round_up(c->Ccap, 64);
         hip_check(hipSetDevice(cfg->device), "hipSetDevice");
         hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+        hip_check(hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking), "hipStreamCreate");
+        hip_check(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "hipEventCreate");
+        hip_check(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "hipEventCreate");
         for (int64_t i = 0; i < c->L_; ++i) c->blocks.emplace_back(new BlockDev());
         // sinusoid frequencies exactly as the reference computes them in fp32
         // (src/transformer.cpp:89,97-99)
@@ -1045,7 +1095,8 @@ int sana_dit_time_gemm(sana_dit * c, int which, int iters, float * avg_ms, doubl
             switch (which) {
                 case 0:
                     if (fused_linear_attention(c, N))
-                        gemm_qkv_split(c, w, M / N, N, c->stream);
+                        gemm_qkv_split(c, w, M / N, N, c->xa16.as<half_t>(), c->qkv16.as<half_t>(),
+                                       c->la_kt.as<half_t>(), c->la_vt.as<half_t>(), 1, c->stream);
                     else
                         gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
                                    nullptr, sana::kActNone, c->qkv16.as<half_t>(), 3 * C, nullptr, 0, c->stream);

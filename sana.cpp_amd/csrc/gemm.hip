@@ -620,11 +620,6 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
         case 27: return launch<128, 64, 2, 2, 2, 3>(p, s);
         case 28: return launch<64, 64, 2, 2, 2, 3>(p, s);
         case 29: return launch<128, 128, 2, 2, 2, 3>(p, s);
-        case 30: return launch<128, 96, 4, 1, 2, 3>(p, s);
-        case 31: return launch<128, 96, 4, 1, 2, 1>(p, s);
-        case 32: return launch<128, 96, 2, 1, 2, 3>(p, s);
-        case 33: return launch<128, 96, 4, 1, 3, 1>(p, s);
-        case 34: return launch<128, 96, 4, 1, 4, 1>(p, s);
         default: break;
     }
     // Tile choice from sweeps on MI355X with cold weights (each GEMM's weights
@@ -636,13 +631,16 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     //  * plain stores whose N splits into 192-wide tiles with >= 256 tiles:
     //    128x192 with early stage release (two workgroups per CU);
     //  * otherwise 128x128 tiles with two stages, two workgroups per CU.
+    // (tile counts are scaled by the launches that share the CUs, p.co)
+    const int64_t co = std::max(p.co, 1);
     const int64_t tm128 = (p.M + 127) / 128;
-    const int64_t t128 = tm128 * ((p.N + 127) / 128);
+    const int64_t t128 = tm128 * ((p.N + 127) / 128) * co;
     if (t128 <= 160) {
-        if (tm128 * ((p.N + 63) / 64) >= 256) return launch<128, 64, 2, 2, 2, 3>(p, s);
+        if (tm128 * ((p.N + 63) / 64) * co >= 256) return launch<128, 64, 2, 2, 2, 3>(p, s);
         return launch<64, 64, 2, 2, 2, 1>(p, s);
     }
-    if (p.mode == kGemmStore && p.N % 192 == 0 && tm128 * (p.N / 192) >= 256) return launch<128, 192, 2, 2, 2, 3>(p, s);
+    if (p.mode == kGemmStore && p.N % 192 == 0 && tm128 * (p.N / 192) * co >= 256)
+        return launch<128, 192, 2, 2, 2, 3>(p, s);
     return launch<128, 128, 2, 2, 2, 1>(p, s);
 }
 

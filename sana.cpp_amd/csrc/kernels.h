@@ -61,6 +61,10 @@ struct GemmParams {
     // lda + c].  With out16_pad the fp16 output goes to the interior of a
     // bordered [B][(conv_h + 2) * (conv_w + 2)][ldo16] buffer.
     int conv = 0, conv_h = 0, conv_w = 0, out16_pad = 0;
+    // Launches of this shape that run concurrently with this one (on other
+    // streams or graph branches); the tile choice sizes its grid for the CUs
+    // it shares with them.
+    int co = 1;
     int vec = 0;  // set by gemm(): 16-byte epilogue accesses are aligned
 };
 
@@ -107,8 +111,9 @@ size_t linattn_workspace_floats(int B, int N, int H, int D);
 // Whole linear attention in one launch for head_dim 32, from the kGemmQKV
 // layouts: relu(q) token-major [B*N, ldq], relu(K)^T and V^T [B][H*32][N].
 bool linear_attention_fused_ok(int N, int D);
+// co: launches of this shape running concurrently (sizes the token splits).
 hipError_t linear_attention_fused(const half_t * q, int64_t ldq, const half_t * kt, const half_t * vt, half_t * out,
-                                  int64_t ldo, int B, int N, int H, int D, hipStream_t s);
+                                  int64_t ldo, int B, int N, int H, int D, hipStream_t s, int co = 1);
 hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v, int64_t ld, half_t * out,
                             int64_t ldo, int B, int N, int H, int D, float * workspace, hipStream_t s);
 
