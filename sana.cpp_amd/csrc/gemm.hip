@@ -620,14 +620,17 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
         case 27: return launch<128, 64, 2, 2, 2, 3>(p, s);
         case 28: return launch<64, 64, 2, 2, 2, 3>(p, s);
         case 29: return launch<128, 128, 2, 2, 2, 3>(p, s);
+        case 30: return launch<64, 64, 2, 2, 3, 3>(p, s);
         default: break;
     }
     // Tile choice from sweeps on MI355X with cold weights (each GEMM's weights
     // come from HBM, as in the 28-block forward).  Every CU pulls at most
     // ~55 GB/s from L2, so larger tiles (fewer operand bytes per flop) win as
     // long as the grid still covers the 256 CUs:
-    //  * grids of <= 160 128x128 tiles: 128x64 tiles with early stage release
-    //    when that makes >= 256 tiles, else 64x64 tiles;
+    //  * grids of <= 160 128x128 tiles: shared with a concurrent launch (the
+    //    two CFG branches), 64x64 tiles with three stages and early release;
+    //    alone, 128x64 tiles with early stage release when that makes >= 256
+    //    tiles, else 64x64 tiles;
     //  * plain stores whose N splits into 192-wide tiles with >= 256 tiles:
     //    128x192 with early stage release (two workgroups per CU);
     //  * otherwise 128x128 tiles with two stages, two workgroups per CU.
@@ -636,7 +639,8 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     const int64_t tm128 = (p.M + 127) / 128;
     const int64_t t128 = tm128 * ((p.N + 127) / 128) * co;
     if (t128 <= 160) {
-        if (tm128 * ((p.N + 63) / 64) * co >= 256) return launch<128, 64, 2, 2, 2, 3>(p, s);
+        if (co >= 2) return launch<64, 64, 2, 2, 3, 3>(p, s);
+        if (tm128 * ((p.N + 63) / 64) >= 256) return launch<128, 64, 2, 2, 2, 3>(p, s);
         return launch<64, 64, 2, 2, 2, 1>(p, s);
     }
     if (p.mode == kGemmStore && p.N % 192 == 0 && tm128 * (p.N / 192) * co >= 256)
