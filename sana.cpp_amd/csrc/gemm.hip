@@ -389,6 +389,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                     }
             }
             __syncthreads();
+            if constexpr (MODE == kGemmResidual && CONV != 0) {
+                if (p.rn_w) {
+                    // row RMSNorm (the tile spans all N columns): 1 / sqrt(mean(v^2) + eps)
+                    // of v = acc + bias, two threads per row, kept in the row's padding
+                    for (int rr = tid >> 1; rr < ER; rr += G::NT / 2) {
+                        float ss = 0.0f;
+                        for (int c = tid & 1; c < p.N; c += 2) {
+                            const float v = ct[rr * LDC + c] + (p.bias ? p.bias[c] : 0.0f);
+                            ss += v * v;
+                        }
+                        ss += __shfl_xor(ss, 1, 64);
+                        if ((tid & 1) == 0) ct[rr * LDC + BN] = 1.0f / sqrtf(ss / (float)p.N + p.rn_eps);
+                    }
+                    __syncthreads();
+                }
+            }
             if constexpr (MODE == kGemmQKV) {
                 // k and v sections: items (column, 8-row octet), consecutive lanes on
                 // consecutive octets of one column, so each column's 16-byte stores
@@ -415,7 +431,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                     *reinterpret_cast<f16x8 *>(dst + ((int64_t)b * C3 + ch) * p.qkv_n + t0) = h;
                 }
             }
-            if (active) {
+            if (active && MODE != kGemmResidual) {
                 for (int rr = tid / CPR; rr < ER; rr += G::NT / CPR) {
                     const int row = m0 + pass * ER + rr;
                     if (row >= p.M) break;
@@ -443,12 +459,81 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                                 *reinterpret_cast<float4 *>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
                             }
                         } else {
-                            for (int e = 0; e < nc; ++e) {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {  // static indices: v stays in registers
+                                if (e >= nc) continue;
                                 if (p.out16) reinterpret_cast<f16 *>(p.out16)[orow16(row) * p.ldo16 + col + e] = (f16)v[e];
                                 if (p.out32) p.out32[(int64_t)row * p.ldo32 + col + e] = v[e];
                             }
                         }
-                    } else {  // kGemmResidual: x += gate * (acc + bias)
+                    }
+                }
+            }
+            if constexpr (MODE == kGemmResidual) {
+                if (active) {
+                    // x += gate * (acc + bias), or x += rmsnorm(acc + bias).  All of this
+                    // thread's residual rows are loaded first (one batch of loads in
+                    // flight), then updated and stored.
+                    constexpr int RSTEP = G::NT / CPR;
+                    constexpr int RPT = (ER + RSTEP - 1) / RSTEP;
+                    const int rbase = tid / CPR;
+                    float xin[RPT][8];
+#pragma unroll
+                    for (int k = 0; k < RPT; ++k) {
+                        const int rr = rbase + k * RSTEP;
+                        const int row = m0 + pass * ER + rr;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) xin[k][e] = 0.0f;
+                        if (rr >= ER || row >= p.M) continue;
+                        bool gathered = false;
+                        if constexpr (CONV == 2) {
+                            if (p.up_src) {
+                                // the residual starts as the pixel-shuffled channel-repeat
+                                // shortcut of the low-resolution input
+                                const int hw = p.conv_h * p.conv_w;
+                                const int img = row / hw, rem = row - img * hw;
+                                const int Y = rem / p.conv_w, X = rem - Y * p.conv_w;
+                                const float * src =
+                                    p.up_src + ((int64_t)(img * (p.conv_h / 2) + (Y >> 1)) * (p.conv_w / 2) + (X >> 1)) *
+                                                   p.up_c;
+                                const int q = 2 * (Y & 1) + (X & 1);
+#pragma unroll
+                                for (int e = 0; e < 8; ++e)
+                                    if (e < nc) xin[k][e] = src[((col + e) * 4 + q) / p.up_rep];
+                                gathered = true;
+                            }
+                        }
+                        if (!gathered) {
+                            const float * xr = p.out32 + (int64_t)row * p.ldo32 + col;
+                            if (vec8) {
+                                const float4 x0 = *reinterpret_cast<const float4 *>(xr);
+                                const float4 x1 = *reinterpret_cast<const float4 *>(xr + 4);
+                                xin[k][0] = x0.x; xin[k][1] = x0.y; xin[k][2] = x0.z; xin[k][3] = x0.w;
+                                xin[k][4] = x1.x; xin[k][5] = x1.y; xin[k][6] = x1.z; xin[k][7] = x1.w;
+                            } else {
+#pragma unroll
+                                for (int e = 0; e < 8; ++e)
+                                    if (e < nc) xin[k][e] = xr[e];
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int k = 0; k < RPT; ++k) {
+                        const int rr = rbase + k * RSTEP;
+                        const int row = m0 + pass * ER + rr;
+                        if (rr >= ER || row >= p.M) continue;
+                        const float4 v0 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8]);
+                        const float4 v1 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8 + 4]);
+                        float v[8] = {v0.x + bv[0], v0.y + bv[1], v0.z + bv[2], v0.w + bv[3],
+                                      v1.x + bv[4], v1.y + bv[5], v1.z + bv[6], v1.w + bv[7]};
+                        if constexpr (CONV != 0) {
+                            if (p.rn_w) {
+                                const float inv = ct[rr * LDC + BN];
+#pragma unroll
+                                for (int e = 0; e < 8; ++e)
+                                    if (e < nc) v[e] = v[e] * inv * p.rn_w[col + e] + (p.rn_b ? p.rn_b[col + e] : 0.0f);
+                            }
+                        }
                         const int b = row / p.rows_per_batch;
                         float g[8];
                         if (p.gate_a && vec8) {
@@ -473,13 +558,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                                 }
                             }
                         }
+                        float x[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) x[e] = xin[k][e] + g[e] * v[e];
                         float * xr = p.out32 + (int64_t)row * p.ldo32 + col;
                         if (vec8) {
-                            const float4 x0 = *reinterpret_cast<const float4 *>(xr);
-                            const float4 x1 = *reinterpret_cast<const float4 *>(xr + 4);
-                            float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) x[e] = x[e] + g[e] * v[e];
                             *reinterpret_cast<float4 *>(xr) = make_float4(x[0], x[1], x[2], x[3]);
                             *reinterpret_cast<float4 *>(xr + 4) = make_float4(x[4], x[5], x[6], x[7]);
                             if (p.out16) {
@@ -489,15 +572,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                                 *reinterpret_cast<f16x8 *>(reinterpret_cast<f16 *>(p.out16) + orow16(row) * p.ldo16 + col) = h;
                             }
                         } else {
-                            for (int e = 0; e < nc; ++e) {
-                                const float nx = xr[e] + g[e] * v[e];
-                                xr[e] = nx;
-                                if (p.out16) reinterpret_cast<f16 *>(p.out16)[orow16(row) * p.ldo16 + col + e] = (f16)nx;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {
+                                if (e >= nc) continue;
+                                xr[e] = x[e];
+                                if (p.out16) reinterpret_cast<f16 *>(p.out16)[orow16(row) * p.ldo16 + col + e] = (f16)x[e];
                             }
                         }
                     }
                 }
-
             }
         }
     }
@@ -565,6 +648,10 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     if (!p.A || !p.W || p.ldw < p.K || p.lda % 8 || p.ldw % 8) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(p.A) | reinterpret_cast<uintptr_t>(p.W)) & 15) return hipErrorInvalidValue;
     if (p.mode == kGemmResidual && !p.out32) return hipErrorInvalidValue;
+    if (p.rn_w && (p.mode != kGemmResidual || !p.conv || p.N > 128 || p.gate_a)) return hipErrorInvalidValue;
+    if (p.up_src && (p.conv != 2 || p.mode != kGemmResidual || p.up_c <= 0 || p.up_rep <= 0 ||
+                     ((int64_t)p.N * 4 + p.up_rep - 1) / p.up_rep > p.up_c))
+        return hipErrorInvalidValue;
     if (p.mode == kGemmVT && (!p.out16 || p.vt_rows <= 0 || p.vt_cols <= 0 || p.vt_batch <= 0 ||
                               p.vt_ld < p.vt_cols || p.N != p.vt_batch * p.vt_cols || p.M % p.vt_rows))
         return hipErrorInvalidValue;

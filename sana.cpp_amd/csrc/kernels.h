@@ -61,6 +61,18 @@ struct GemmParams {
     // lda + c].  With out16_pad the fp16 output goes to the interior of a
     // bordered [B][(conv_h + 2) * (conv_w + 2)][ldo16] buffer.
     int conv = 0, conv_h = 0, conv_w = 0, out16_pad = 0;
+    // conv = 2, residual mode: with up_src set, the residual is not read from
+    // out32 but starts as the pixel-shuffled channel-repeat shortcut of the
+    // low-resolution input up_src (fp32 NHWC, up_c channels): output pixel
+    // (y, x), channel n takes up_src[(y/2, x/2)][(4n + 2(y%2) + x%2) / up_rep].
+    const float * up_src = nullptr;
+    int up_c = 0, up_rep = 1;
+    // conv modes, residual mode, N <= 128 (one tile spans the row): with rn_w
+    // set, x += rmsnorm(acc + bias) * rn_w + rn_b over each row's N channels
+    // (eps rn_eps) instead of x += acc + bias.
+    const float * rn_w = nullptr;
+    const float * rn_b = nullptr;
+    float rn_eps = 1e-5f;
     // Launches of this shape that run concurrently with this one (on other
     // streams or graph branches); the tile choice sizes its grid for the CUs
     // it shares with them.

@@ -10,7 +10,7 @@
 //   1x1 input  fp16 [P, C].
 // Every 1x1 and 3x3 convolution is an MFMA GEMM (3x3: K = 9 taps x C,
 // tap-major weights; the nearest-2x upsample is folded into the A addressing);
-// the RMSNorm + residual, the shortcuts, the depthwise 5x5 and the grouped
+// the RMSNorm + residual, the conv_in shortcut, the depthwise 5x5 and the grouped
 // 1x1 of the multiscale attention are the kernels below; the ReLU linear
 // attention and the depthwise 3x3 + GLU of GLUMBConv are the DiT's kernels.
 //
@@ -99,21 +99,6 @@ __global__ void vae_zero_border_kernel(f16 * __restrict__ buf, int B, int H, int
 #pragma unroll
     for (int e = 0; e < 8; ++e) z[e] = (f16)0.0f;
     *reinterpret_cast<f16x8 *>(buf + (((int64_t)b * (H + 2) + y) * (W + 2) + x) * ld + c8 * 8) = z;
-}
-
-// Pixel-shuffled channel-repeat shortcut of the upsample block
-// (add_upsample_shortcut_2x_inplace, src/vae_ops.cpp:386-445) as the initial
-// value of the new residual: out[b, 2y+i, 2x+j][oc] = in[b, y, x][(4 oc + 2i + j) / rep].
-__global__ void vae_shortcut_up_kernel(const float * __restrict__ in, int Cin, float * __restrict__ out, int Cout,
-                                       int B, int H2, int W2, int rep) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t n = (int64_t)B * H2 * W2 * Cout;
-    if (i >= n) return;
-    const int oc = (int)(i % Cout);
-    const int64_t p = i / Cout;
-    const int X = (int)(p % W2), Y = (int)((p / W2) % H2), b = (int)(p / ((int64_t)W2 * H2));
-    const int ic = (oc * 4 + 2 * (Y & 1) + (X & 1)) / rep;
-    out[i] = in[(((int64_t)b * (H2 / 2) + Y / 2) * (W2 / 2) + X / 2) * Cin + ic];
 }
 
 // Per-pixel RMSNorm over channels (rms_norm_4d_channelwise,
@@ -508,7 +493,8 @@ void gemm_plain(const half_t * A, int64_t lda, const DevMem & W, int64_t M, int6
 // nearest-2x upsample (conv = 2).  Residual mode: x += acc + bias.
 void gemm_conv(int conv, const half_t * A, int64_t cin, const DevMem & W, int64_t B, int64_t H, int64_t Wd,
                int64_t N, const float * bias, int act, bool residual, float * x32, half_t * out16, bool pad16,
-               float * out32, hipStream_t s) {
+               float * out32, hipStream_t s, const float * up_src = nullptr, int64_t up_c = 0,
+               const DevMem * rn_w = nullptr, const DevMem * rn_b = nullptr) {
     sana::GemmParams p;
     p.conv = conv;
     p.conv_h = (int)H;
@@ -529,6 +515,16 @@ void gemm_conv(int conv, const half_t * A, int64_t cin, const DevMem & W, int64_
         p.mode = sana::kGemmResidual;
         p.out32 = x32;
         p.ldo32 = N;
+        if (up_src) {
+            p.up_src = up_src;
+            p.up_c = (int)up_c;
+            p.up_rep = (int)(N * 4 / up_c);
+        }
+        if (rn_w) {
+            p.rn_w = rn_w->as<float>();
+            p.rn_b = rn_b ? rn_b->as<float>() : nullptr;
+            p.rn_eps = 1e-5f;
+        }
     } else {
         p.out32 = out32;
         p.ldo32 = N;
@@ -626,15 +622,13 @@ void decode(sana_vae * v, const float * lat, int64_t B, int64_t h, int64_t w, fl
     for (int64_t li = L - 1; li >= 0; --li) {
         LevelDev & lvd = *v->lv[li];
         if (li + 1 < L) {
-            // upsample block: shortcut into xs32, then xs32 += conv(upsample(cur)) + bias
+            // upsample block: xs32 = shortcut(x32) + conv(upsample(cur)) + bias, the
+            // shortcut gathered from the low-resolution residual in the epilogue
             const int64_t Co = lvd.C, H2 = 2 * H, W2 = 2 * W;
-            const int64_t n = B * H2 * W2 * Co;
-            hipLaunchKernelGGL(vae_shortcut_up_kernel, dim3(blocks_for(n)), dim3(256), 0, s, v->x32.as<float>(), (int)C,
-                               v->xs32.as<float>(), (int)Co, (int)B, (int)H2, (int)W2, (int)(Co * 4 / C));
-            launch_check(hipGetLastError(), "vae shortcut");
             if (!lvd.attn) zero_border(*oth, B, H2, W2, Co, s);
             gemm_conv(2, cur->as<half_t>(), C, lvd.up_w, B, H2, W2, Co, lvd.up_b.as<float>(), sana::kActNone, true,
-                      v->xs32.as<float>(), lvd.attn ? v->a16.as<half_t>() : oth->as<half_t>(), !lvd.attn, nullptr, s);
+                      v->xs32.as<float>(), lvd.attn ? v->a16.as<half_t>() : oth->as<half_t>(), !lvd.attn, nullptr, s,
+                      v->x32.as<float>(), C);
             std::swap(v->x32.p, v->xs32.p);
             std::swap(v->x32.bytes, v->xs32.bytes);
             std::swap(cur, oth);
@@ -656,10 +650,16 @@ void decode(sana_vae * v, const float * lat, int64_t B, int64_t h, int64_t w, fl
                 ResDev & r = lvd.res[k];
                 gemm_conv(1, cur->as<half_t>(), C, r.w1, B, H, W, C, r.b1.as<float>(), sana::kActSilu, false, nullptr,
                           oth->as<half_t>(), true, nullptr, s);
-                gemm_conv(1, oth->as<half_t>(), C, r.w2, B, H, W, C, nullptr, sana::kActNone, false, nullptr, nullptr,
-                          false, v->t32.as<float>(), s);
                 // next: conv1 of the next ResBlock, the next upsample, or (level 0, last) the final norm
-                rmsnorm(v->t32.as<float>(), C, P, r.nw, &r.nb, x, false, x, cur->as<half_t>(), true, H, W, s);
+                if (C <= 128) {
+                    // x += rmsnorm(conv2) in the conv's epilogue (one tile spans the channels)
+                    gemm_conv(1, oth->as<half_t>(), C, r.w2, B, H, W, C, nullptr, sana::kActNone, true, x,
+                              cur->as<half_t>(), true, nullptr, s, nullptr, 0, &r.nw, &r.nb);
+                } else {
+                    gemm_conv(1, oth->as<half_t>(), C, r.w2, B, H, W, C, nullptr, sana::kActNone, false, nullptr,
+                              nullptr, false, v->t32.as<float>(), s);
+                    rmsnorm(v->t32.as<float>(), C, P, r.nw, &r.nb, x, false, x, cur->as<half_t>(), true, H, W, s);
+                }
             } else {
                 AttnDev & a = lvd.att[k];
                 const int64_t heads = C / kVaeHead;
