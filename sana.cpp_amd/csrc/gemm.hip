@@ -389,22 +389,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                     }
             }
             __syncthreads();
-            if constexpr (MODE == kGemmResidual && CONV != 0) {
-                if (p.rn_w) {
-                    // row RMSNorm (the tile spans all N columns): 1 / sqrt(mean(v^2) + eps)
-                    // of v = acc + bias, two threads per row, kept in the row's padding
-                    for (int rr = tid >> 1; rr < ER; rr += G::NT / 2) {
-                        float ss = 0.0f;
-                        for (int c = tid & 1; c < p.N; c += 2) {
-                            const float v = ct[rr * LDC + c] + (p.bias ? p.bias[c] : 0.0f);
-                            ss += v * v;
-                        }
-                        ss += __shfl_xor(ss, 1, 64);
-                        if ((tid & 1) == 0) ct[rr * LDC + BN] = 1.0f / sqrtf(ss / (float)p.N + p.rn_eps);
-                    }
-                    __syncthreads();
-                }
-            }
             if constexpr (MODE == kGemmQKV) {
                 // k and v sections: items (column, 8-row octet), consecutive lanes on
                 // consecutive octets of one column, so each column's 16-byte stores
@@ -471,7 +455,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
             }
             if constexpr (MODE == kGemmResidual) {
                 if (active) {
-                    // x += gate * (acc + bias), or x += rmsnorm(acc + bias).  All of this
+                    // x += gate * (acc + bias).  All of this
                     // thread's residual rows are loaded first (one batch of loads in
                     // flight), then updated and stored.
                     constexpr int RSTEP = G::NT / CPR;
@@ -526,14 +510,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                         const float4 v1 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8 + 4]);
                         float v[8] = {v0.x + bv[0], v0.y + bv[1], v0.z + bv[2], v0.w + bv[3],
                                       v1.x + bv[4], v1.y + bv[5], v1.z + bv[6], v1.w + bv[7]};
-                        if constexpr (CONV != 0) {
-                            if (p.rn_w) {
-                                const float inv = ct[rr * LDC + BN];
-#pragma unroll
-                                for (int e = 0; e < 8; ++e)
-                                    if (e < nc) v[e] = v[e] * inv * p.rn_w[col + e] + (p.rn_b ? p.rn_b[col + e] : 0.0f);
-                            }
-                        }
                         const int b = row / p.rows_per_batch;
                         float g[8];
                         if (p.gate_a && vec8) {
@@ -648,7 +624,6 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     if (!p.A || !p.W || p.ldw < p.K || p.lda % 8 || p.ldw % 8) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(p.A) | reinterpret_cast<uintptr_t>(p.W)) & 15) return hipErrorInvalidValue;
     if (p.mode == kGemmResidual && !p.out32) return hipErrorInvalidValue;
-    if (p.rn_w && (p.mode != kGemmResidual || !p.conv || p.N > 128 || p.gate_a)) return hipErrorInvalidValue;
     if (p.up_src && (p.conv != 2 || p.mode != kGemmResidual || p.up_c <= 0 || p.up_rep <= 0 ||
                      ((int64_t)p.N * 4 + p.up_rep - 1) / p.up_rep > p.up_c))
         return hipErrorInvalidValue;

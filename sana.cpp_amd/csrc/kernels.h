@@ -67,12 +67,6 @@ struct GemmParams {
     // (y, x), channel n takes up_src[(y/2, x/2)][(4n + 2(y%2) + x%2) / up_rep].
     const float * up_src = nullptr;
     int up_c = 0, up_rep = 1;
-    // conv modes, residual mode, N <= 128 (one tile spans the row): with rn_w
-    // set, x += rmsnorm(acc + bias) * rn_w + rn_b over each row's N channels
-    // (eps rn_eps) instead of x += acc + bias.
-    const float * rn_w = nullptr;
-    const float * rn_b = nullptr;
-    float rn_eps = 1e-5f;
     // Launches of this shape that run concurrently with this one (on other
     // streams or graph branches); the tile choice sizes its grid for the CUs
     // it shares with them.
