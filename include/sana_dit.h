@@ -185,6 +185,37 @@ int sana_vae_decoder_input(sana_vae * vae, const float * latent, int64_t B, int6
 int sana_vae_decode_device(sana_vae * vae, const float * latent, int64_t B, int64_t H, int64_t W, float * image,
                            void * stream);
 
+/* ---- Gemma-2 text encoder (the stage before the denoiser) ----
+ * The decoder forward that src/gemma_encoder.cpp:95-152 runs through
+ * llama.cpp in embeddings mode: token ids in, the per-token hidden states
+ * after the final RMSNorm out.  Causal attention with grouped kv heads, NeoX
+ * RoPE, logit soft-cap, a sliding window on the even layers, GELU-tanh gated
+ * FFN, pre- and post-norms.  Sizes: hidden, head_dim and ffn multiples of 64
+ * (hidden <= 4096), heads a multiple of kv_heads, up to 8192 tokens. */
+typedef struct sana_gemma sana_gemma;
+typedef struct {
+    int64_t vocab, hidden, layers, heads, kv_heads, head_dim, ffn;  /* Gemma-2 2B: 256000 2304 26 8 4 256 9216 */
+    int64_t sliding_window;                                           /* 4096; 0 = none */
+    float rms_eps;                                                    /* 1e-6 */
+    float rope_theta;                                                 /* 10000 */
+    float attn_softcap;                                               /* 50 */
+    float query_scale;                                                /* 1 / sqrt(head_dim) */
+    int device;
+} sana_gemma_config;
+int sana_gemma_create(const sana_gemma_config * cfg, sana_gemma ** out);
+int sana_gemma_destroy(sana_gemma * g);
+/* One tensor by its GGUF name (token_embd, output_norm, blk.N.{attn_norm,
+ * attn_q, attn_k, attn_v, attn_output, post_attention_norm, ffn_norm,
+ * ffn_gate, ffn_up, ffn_down, post_ffw_norm}.weight) and PyTorch-order shape.
+ * RMSNorm weights as the GGUF stores them (1 + w). fp32 host data. */
+int sana_gemma_set_weight(sana_gemma * g, const char * name, const float * data, const int64_t * shape, int ndim);
+/* SANA_ERR_STATE naming the first missing tensor, else SANA_OK. */
+int sana_gemma_check_weights(sana_gemma * g);
+/* All tensors from one GGUF (F32, F16 or BF16 payloads). */
+int sana_gemma_load_gguf(sana_gemma * g, const char * path);
+/* tokens [n] -> hidden [n, hidden] fp32 (host pointers). */
+int sana_gemma_encode(sana_gemma * g, const int32_t * tokens, int64_t n, float * hidden);
+
 /* Measured MFMA ceiling for roofline reports (no counterpart in the reference):
  * `workgroups` x 256 threads run `iters` steps of 8 independent fp16
  * v_mfma_f32_32x32x16 chains with no memory traffic, asynchronously on `stream`;

@@ -1,0 +1,496 @@
+// Gemma-2 text encoder (the stage before the denoiser: src/gemma_encoder.cpp,
+// which runs llama.cpp's Gemma-2 graph in embeddings mode) on one MI355X,
+// and its C ABI.
+//
+// Per layer, with T tokens (rows), hidden H, nh query heads and nkv kv heads
+// of dimension d, FFN width F:
+//   a16  = rmsnorm(x) * attn_norm                        gemma_norm_kernel
+//   qkv  = a16 [Wq; Wk; Wv]^T                            one MFMA GEMM, fp32 out
+//   q16, k16 = rope(q) * query_scale, rope(k); V^T       gemma_qkv_kernel
+//   S_h  = q16_h k16_kv(h)^T                             one GEMM per head
+//   P_h  = softmax(causal / window mask, soft-cap)       gemma_softmax_kernel
+//   o16_h = P_h V_kv(h)                                  one GEMM per head (B = V^T)
+//   x   += rmsnorm(o16 Wo^T) * post_attention_norm       GEMM + gemma_norm_kernel
+//   a16  = rmsnorm(x) * ffn_norm
+//   gu   = a16 [Wgate; Wup]^T; g16 = gelu_tanh(gate) up  GEMM + gemma_geglu_kernel
+//   x   += rmsnorm(g16 Wdown^T) * post_ffw_norm
+// out = rmsnorm(x) * output_norm.  Activations are token-major; GEMM operands
+// fp16 with fp32 accumulation; the residual stream, norms, softmax and RoPE
+// in fp32.  RMSNorm weights are taken as stored in the GGUF (1 + w).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/sana_dit.h"
+#include "gguf.h"
+#include "hip_common.h"
+#include "host_util.h"
+#include "kernels.h"
+
+using sana::half_t;
+using namespace sana_host;
+
+namespace {
+
+unsigned blocks_for(int64_t n, int per = 256) { return (unsigned)((n + per - 1) / per); }
+
+// x32[t][c] = embed[token[t]][c] * scale (token ids checked on the host).
+__global__ void gemma_embed_kernel(const int32_t * __restrict__ tok, const f16 * __restrict__ emb,
+                                   float * __restrict__ x, int T, int H, float scale) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)T * H) return;
+    const int t = (int)(i / H), c = (int)(i - (int64_t)t * H);
+    x[i] = (float)emb[(int64_t)tok[t] * H + c] * scale;
+}
+
+// One wave per row of C (<= 256 * NC4) channels: v = y / sqrt(mean(y^2) + eps) * w.
+// mode 0: out16 = fp16(v); 1: x += v (post-norm residual, out32 = x); 2: out32 = v.
+template <int NC4>
+__global__ __launch_bounds__(256) void gemma_norm_kernel(const float * __restrict__ y, int C, int M,
+                                                         const float * __restrict__ w, float eps, int mode,
+                                                         f16 * __restrict__ out16, float * __restrict__ out32) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const int n4 = C >> 2;
+    const float4 * yr = reinterpret_cast<const float4 *>(y + (int64_t)row * C);
+    float4 v[NC4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NC4; ++i) {
+        const int c4 = lane + 64 * i;
+        v[i] = c4 < n4 ? yr[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        ss += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)C + eps);
+#pragma unroll
+    for (int i = 0; i < NC4; ++i) {
+        const int c4 = lane + 64 * i;
+        if (c4 >= n4) continue;
+        const float4 g = reinterpret_cast<const float4 *>(w)[c4];
+        float o[4] = {v[i].x * inv * g.x, v[i].y * inv * g.y, v[i].z * inv * g.z, v[i].w * inv * g.w};
+        if (mode == 0) {
+            f16x4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = (f16)o[e];
+            *reinterpret_cast<f16x4 *>(out16 + (int64_t)row * C + 4 * c4) = h;
+        } else {
+            float4 * xr = reinterpret_cast<float4 *>(out32 + (int64_t)row * C) + c4;
+            if (mode == 1) {
+                const float4 x = *xr;
+                *xr = make_float4(x.x + o[0], x.y + o[1], x.z + o[2], x.w + o[3]);
+            } else {
+                *xr = make_float4(o[0], o[1], o[2], o[3]);
+            }
+        }
+    }
+}
+
+// qkv32 [T][(nh + 2 nkv) d] -> q16 [T][nh d] = rope(q) * qscale, k16 [T][nkv d]
+// = rope(k), vt16 [nkv][d][Tp] = V^T (tokens T..Tp-1 zero).  NeoX RoPE: pair
+// (i, i + d/2) of a head rotated by t * theta^(-2i/d).  One thread per
+// (token, rotation pair) of the q and k heads, and per (token, channel) of v.
+__global__ void gemma_qkv_kernel(const float * __restrict__ qkv, int T, int Tp, int nh, int nkv, int d,
+                                 float theta, float qscale, f16 * __restrict__ q16, f16 * __restrict__ k16,
+                                 f16 * __restrict__ vt16) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int half = d / 2, ld = (nh + 2 * nkv) * d;
+    const int64_t nrot = (int64_t)T * (nh + nkv) * half;
+    if (i < nrot) {
+        const int t = (int)(i / ((nh + nkv) * half));
+        const int r = (int)(i - (int64_t)t * (nh + nkv) * half);
+        const int head = r / half, p = r - head * half;  // heads 0..nh-1 are q, then k
+        const float inv = powf(theta, -2.0f * (float)p / (float)d);
+        float sn, cs;
+        sincosf((float)t * inv, &sn, &cs);
+        const float * src = qkv + (int64_t)t * ld + head * d;
+        const float a = src[p], b = src[p + half];
+        float oa = a * cs - b * sn, ob = b * cs + a * sn;
+        if (head < nh) {
+            f16 * dst = q16 + (int64_t)t * nh * d + head * d;
+            dst[p] = (f16)(oa * qscale);
+            dst[p + half] = (f16)(ob * qscale);
+        } else {
+            f16 * dst = k16 + (int64_t)t * nkv * d + (head - nh) * d;
+            dst[p] = (f16)oa;
+            dst[p + half] = (f16)ob;
+        }
+        return;
+    }
+    const int64_t j = i - nrot;
+    if (j >= (int64_t)nkv * d * Tp) return;
+    const int t = (int)(j % Tp), ch = (int)(j / Tp);  // ch = kvhead * d + dim
+    vt16[j] = t < T ? (f16)qkv[(int64_t)t * ld + (nh + nkv) * d + ch] : (f16)0.0f;
+}
+
+// Rows (head, t) of S [nh][T][Tp]: s = cap * tanh(S / cap) over keys j <= t
+// (and j > t - window when window > 0), softmax in fp32 -> P fp16 [nh][T][Tp]
+// with zeros for the masked and padding keys.  One wave per row.
+__global__ __launch_bounds__(256) void gemma_softmax_kernel(const float * __restrict__ S, f16 * __restrict__ P,
+                                                            int nh, int T, int Tp, float cap, int window) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= nh * T) return;
+    const int t = row % T;
+    const int j0 = window > 0 ? max(0, t - window + 1) : 0;
+    const float * sr = S + (int64_t)row * Tp;
+    f16 * pr = P + (int64_t)row * Tp;
+    float mx = -INFINITY;
+    for (int j = j0 + lane; j <= t; j += 64) mx = fmaxf(mx, cap * tanhf(sr[j] / cap));
+    mx = wave_max(mx);
+    float sum = 0.0f;
+    for (int j = j0 + lane; j <= t; j += 64) sum += expf(cap * tanhf(sr[j] / cap) - mx);
+    sum = wave_sum(sum);
+    const float rs = 1.0f / sum;
+    for (int j = lane; j < Tp; j += 64)
+        pr[j] = (j >= j0 && j <= t) ? (f16)(expf(cap * tanhf(sr[j] / cap) - mx) * rs) : (f16)0.0f;
+}
+
+// g16 [T][F] = gelu_tanh(gu[t][f]) * gu[t][F + f] (gate columns first).
+__global__ void gemma_geglu_kernel(const float * __restrict__ gu, int T, int F, f16 * __restrict__ g16) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)T * F) return;
+    const int64_t t = i / F, f = i - t * F;
+    const float g = gu[t * 2 * F + f], u = gu[t * 2 * F + F + f];
+    g16[i] = (f16)(gelu_tanh_f(g) * u);
+}
+
+struct LayerDev {
+    DevMem wqkv, wo, wgu, wdown;          // fp16, [out][in]
+    DevMem n_attn, n_post_attn, n_ffn, n_post_ffw;  // fp32
+};
+
+}  // namespace
+
+struct sana_gemma {
+    sana_gemma_config cfg{};
+    int64_t Dq = 0, Dkv = 0;
+    std::vector<std::unique_ptr<LayerDev>> layers;
+    DevMem emb16, out_norm;
+    std::map<std::string, bool> loaded;
+    std::vector<std::string> required;
+    hipStream_t stream = nullptr;
+    // workspace
+    int64_t ws_T = 0;
+    DevMem tok, x32, y32, a16, qkv32, q16, k16, vt16, s32, p16, o16, gu32, g16, out32;
+    ~sana_gemma() {
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+void upload_bytes(DevMem & d, const void * src, size_t bytes) {
+    d.ensure(bytes, false);
+    copy_to_device(d.p, src, bytes, "upload gemma weight");
+}
+
+void upload_f16_rows(DevMem & d, const float * src, size_t n, size_t total, size_t offset) {
+    if (!d.p) d.ensure(total * 2, false);
+    std::vector<_Float16> h(n);
+    for (size_t i = 0; i < n; ++i) h[i] = (_Float16)src[i];
+    copy_to_device(static_cast<_Float16 *>(d.p) + offset, h.data(), n * 2, "upload gemma weight");
+}
+
+void expect(const std::string & name, const int64_t * shape, int ndim, std::vector<int64_t> want) {
+    bool ok = ndim == (int)want.size();
+    for (int i = 0; ok && i < ndim; ++i) ok = shape[i] == want[i];
+    if (!ok) {
+        std::string got, exp;
+        for (int i = 0; i < ndim; ++i) got += (i ? "," : "") + std::to_string(shape[i]);
+        for (size_t i = 0; i < want.size(); ++i) exp += (i ? "," : "") + std::to_string(want[i]);
+        throw_err(SANA_ERR_SHAPE, "gemma weight " + name + " has shape [" + got + "], expected [" + exp + "]");
+    }
+}
+
+std::vector<std::string> required_names(const sana_gemma * g) {
+    std::vector<std::string> r = {"token_embd.weight", "output_norm.weight"};
+    for (int64_t l = 0; l < g->cfg.layers; ++l)
+        for (const char * s : {"attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "post_attention_norm",
+                               "ffn_norm", "ffn_gate", "ffn_up", "ffn_down", "post_ffw_norm"})
+            r.push_back("blk." + std::to_string(l) + "." + s + ".weight");
+    return r;
+}
+
+void set_weight(sana_gemma * g, const std::string & n, const float * d, const int64_t * sh, int nd) {
+    const sana_gemma_config & c = g->cfg;
+    const int64_t H = c.hidden, F = c.ffn, Dq = g->Dq, Dkv = g->Dkv;
+    if (n == "token_embd.weight") {
+        expect(n, sh, nd, {c.vocab, H});
+        upload_f16_rows(g->emb16, d, (size_t)(c.vocab * H), (size_t)(c.vocab * H), 0);
+    } else if (n == "output_norm.weight") {
+        expect(n, sh, nd, {H});
+        upload_bytes(g->out_norm, d, (size_t)H * 4);
+    } else {
+        const std::string pre = "blk.";
+        const size_t dot = n.find('.', pre.size());
+        if (n.compare(0, pre.size(), pre) != 0 || dot == std::string::npos)
+            throw_err(SANA_ERR_INVALID_ARGUMENT, "unknown gemma weight " + n);
+        const int64_t l = std::stoll(n.substr(pre.size(), dot - pre.size()));
+        if (l < 0 || l >= c.layers) throw_err(SANA_ERR_INVALID_ARGUMENT, "gemma layer index out of range: " + n);
+        const std::string s = n.substr(dot + 1);
+        LayerDev & L = *g->layers[l];
+        const size_t qkv_rows = (size_t)(Dq + 2 * Dkv);
+        if (s == "attn_q.weight") {
+            expect(n, sh, nd, {Dq, H});
+            upload_f16_rows(L.wqkv, d, (size_t)(Dq * H), qkv_rows * H, 0);
+        } else if (s == "attn_k.weight") {
+            expect(n, sh, nd, {Dkv, H});
+            upload_f16_rows(L.wqkv, d, (size_t)(Dkv * H), qkv_rows * H, (size_t)(Dq * H));
+        } else if (s == "attn_v.weight") {
+            expect(n, sh, nd, {Dkv, H});
+            upload_f16_rows(L.wqkv, d, (size_t)(Dkv * H), qkv_rows * H, (size_t)((Dq + Dkv) * H));
+        } else if (s == "attn_output.weight") {
+            expect(n, sh, nd, {H, Dq});
+            upload_f16_rows(L.wo, d, (size_t)(H * Dq), (size_t)(H * Dq), 0);
+        } else if (s == "ffn_gate.weight") {
+            expect(n, sh, nd, {F, H});
+            upload_f16_rows(L.wgu, d, (size_t)(F * H), (size_t)(2 * F * H), 0);
+        } else if (s == "ffn_up.weight") {
+            expect(n, sh, nd, {F, H});
+            upload_f16_rows(L.wgu, d, (size_t)(F * H), (size_t)(2 * F * H), (size_t)(F * H));
+        } else if (s == "ffn_down.weight") {
+            expect(n, sh, nd, {H, F});
+            upload_f16_rows(L.wdown, d, (size_t)(H * F), (size_t)(H * F), 0);
+        } else {
+            DevMem * dst = s == "attn_norm.weight"             ? &L.n_attn
+                           : s == "post_attention_norm.weight" ? &L.n_post_attn
+                           : s == "ffn_norm.weight"            ? &L.n_ffn
+                           : s == "post_ffw_norm.weight"       ? &L.n_post_ffw
+                                                               : nullptr;
+            if (!dst) throw_err(SANA_ERR_INVALID_ARGUMENT, "unknown gemma weight " + n);
+            expect(n, sh, nd, {H});
+            upload_bytes(*dst, d, (size_t)H * 4);
+        }
+    }
+    g->loaded[n] = true;
+}
+
+void check_ready(const sana_gemma * g) {
+    for (const std::string & n : g->required)
+        if (!g->loaded.count(n)) throw_err(SANA_ERR_STATE, "gemma weight not set: " + n);
+}
+
+void ensure_workspace(sana_gemma * g, int64_t T) {
+    if (T <= g->ws_T) return;
+    const sana_gemma_config & c = g->cfg;
+    const int64_t H = c.hidden, Tp = round_up(T, 64);
+    g->tok.ensure((size_t)T * 4, false);
+    g->x32.ensure((size_t)T * H * 4, false);
+    g->y32.ensure((size_t)T * H * 4, false);
+    g->a16.ensure((size_t)T * H * 2, false);
+    g->qkv32.ensure((size_t)T * (g->Dq + 2 * g->Dkv) * 4, false);
+    g->q16.ensure((size_t)T * g->Dq * 2, false);
+    g->k16.ensure((size_t)T * g->Dkv * 2, false);
+    g->vt16.ensure((size_t)g->Dkv * Tp * 2, false);
+    g->s32.ensure((size_t)c.heads * T * Tp * 4, false);
+    g->p16.ensure((size_t)c.heads * T * Tp * 2, false);
+    g->o16.ensure((size_t)T * g->Dq * 2, false);
+    g->gu32.ensure((size_t)T * 2 * c.ffn * 4, false);
+    g->g16.ensure((size_t)T * c.ffn * 2, false);
+    g->out32.ensure((size_t)T * H * 4, false);
+    g->ws_T = T;
+}
+
+void gemm(const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
+          half_t * o16, int64_t ldo16, float * o32, int64_t ldo32, hipStream_t s) {
+    sana::GemmParams p;
+    p.A = A;
+    p.lda = lda;
+    p.W = W;
+    p.ldw = ldw;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.out16 = o16;
+    p.ldo16 = ldo16;
+    p.out32 = o32;
+    p.ldo32 = ldo32;
+    launch_check(sana::gemm(p, s), "gemma gemm");
+}
+
+void norm(const sana_gemma * g, const float * y, int64_t M, const DevMem & w, int mode, half_t * o16, float * o32,
+          hipStream_t s) {
+    const int64_t C = g->cfg.hidden;
+    const dim3 grid((unsigned)((M + 3) / 4)), blk(256);
+    f16 * h = reinterpret_cast<f16 *>(o16);
+    const float eps = g->cfg.rms_eps;
+#define SANA_GEMMA_NORM(n4) \
+    hipLaunchKernelGGL((gemma_norm_kernel<n4>), grid, blk, 0, s, y, (int)C, (int)M, w.as<float>(), eps, mode, h, o32)
+    if (C <= 1024) SANA_GEMMA_NORM(4);
+    else if (C <= 2048) SANA_GEMMA_NORM(8);
+    else SANA_GEMMA_NORM(16);
+#undef SANA_GEMMA_NORM
+    launch_check(hipGetLastError(), "gemma norm");
+}
+
+// decode_embeddings (src/gemma_encoder.cpp:95-152) on device token ids.
+void encode(sana_gemma * g, int64_t T, hipStream_t s) {
+    const sana_gemma_config & c = g->cfg;
+    const int64_t H = c.hidden, F = c.ffn, d = c.head_dim, nh = c.heads, nkv = c.kv_heads, Tp = round_up(T, 64);
+    const int64_t Dq = g->Dq, Dkv = g->Dkv, Dqkv = Dq + 2 * Dkv, grp = nh / nkv;
+    hipLaunchKernelGGL(gemma_embed_kernel, dim3(blocks_for(T * H)), dim3(256), 0, s, g->tok.as<int32_t>(),
+                       g->emb16.as<f16>(), g->x32.as<float>(), (int)T, (int)H, std::sqrt((float)H));
+    launch_check(hipGetLastError(), "gemma embed");
+    half_t * a16 = g->a16.as<half_t>();
+    for (int64_t l = 0; l < c.layers; ++l) {
+        LayerDev & L = *g->layers[l];
+        norm(g, g->x32.as<float>(), T, L.n_attn, 0, a16, nullptr, s);
+        gemm(a16, H, L.wqkv.as<half_t>(), H, T, Dqkv, H, nullptr, 0, g->qkv32.as<float>(), Dqkv, s);
+        {
+            const int64_t n = T * (nh + nkv) * (d / 2) + nkv * d * Tp;
+            hipLaunchKernelGGL(gemma_qkv_kernel, dim3(blocks_for(n)), dim3(256), 0, s, g->qkv32.as<float>(), (int)T,
+                               (int)Tp, (int)nh, (int)nkv, (int)d, c.rope_theta, c.query_scale, g->q16.as<f16>(),
+                               g->k16.as<f16>(), g->vt16.as<f16>());
+            launch_check(hipGetLastError(), "gemma qkv");
+        }
+        for (int64_t h = 0; h < nh; ++h)
+            gemm(g->q16.as<half_t>() + h * d, Dq, g->k16.as<half_t>() + (h / grp) * d, Dkv, T, T, d, nullptr, 0,
+                 g->s32.as<float>() + h * T * Tp, Tp, s);
+        const int window = (c.sliding_window > 0 && l % 2 == 0) ? (int)c.sliding_window : 0;
+        hipLaunchKernelGGL(gemma_softmax_kernel, dim3((unsigned)((nh * T + 3) / 4)), dim3(256), 0, s,
+                           g->s32.as<float>(), g->p16.as<f16>(), (int)nh, (int)T, (int)Tp, c.attn_softcap, window);
+        launch_check(hipGetLastError(), "gemma softmax");
+        for (int64_t h = 0; h < nh; ++h)
+            gemm(g->p16.as<half_t>() + h * T * Tp, Tp, g->vt16.as<half_t>() + (h / grp) * d * Tp, Tp, T, d, Tp,
+                 g->o16.as<half_t>() + h * d, Dq, nullptr, 0, s);
+        gemm(g->o16.as<half_t>(), Dq, L.wo.as<half_t>(), Dq, T, H, Dq, nullptr, 0, g->y32.as<float>(), H, s);
+        norm(g, g->y32.as<float>(), T, L.n_post_attn, 1, nullptr, g->x32.as<float>(), s);
+        norm(g, g->x32.as<float>(), T, L.n_ffn, 0, a16, nullptr, s);
+        gemm(a16, H, L.wgu.as<half_t>(), H, T, 2 * F, H, nullptr, 0, g->gu32.as<float>(), 2 * F, s);
+        hipLaunchKernelGGL(gemma_geglu_kernel, dim3(blocks_for(T * F)), dim3(256), 0, s, g->gu32.as<float>(), (int)T,
+                           (int)F, g->g16.as<f16>());
+        launch_check(hipGetLastError(), "gemma geglu");
+        gemm(g->g16.as<half_t>(), F, L.wdown.as<half_t>(), F, T, H, F, nullptr, 0, g->y32.as<float>(), H, s);
+        norm(g, g->y32.as<float>(), T, L.n_post_ffw, 1, nullptr, g->x32.as<float>(), s);
+    }
+    norm(g, g->x32.as<float>(), T, g->out_norm, 2, nullptr, g->out32.as<float>(), s);
+}
+
+void validate_config(const sana_gemma_config * c) {
+    auto bad = [](const char * m) { throw_err(SANA_ERR_INVALID_ARGUMENT, m); };
+    if (c->vocab <= 0 || c->layers <= 0 || c->heads <= 0 || c->kv_heads <= 0) bad("gemma sizes must be positive");
+    if (c->heads % c->kv_heads) bad("gemma query heads must be a multiple of the kv heads");
+    if (c->hidden <= 0 || c->hidden % 64 || c->hidden > 4096) bad("gemma hidden size must be a multiple of 64 up to 4096");
+    if (c->head_dim <= 0 || c->head_dim % 64) bad("gemma head dim must be a multiple of 64");
+    if (c->ffn <= 0 || c->ffn % 64) bad("gemma FFN width must be a multiple of 64");
+    if (!(c->rms_eps > 0.0f) || !(c->rope_theta > 0.0f) || !(c->attn_softcap > 0.0f) || !(c->query_scale > 0.0f))
+        bad("gemma eps, rope theta, soft-cap and query scale must be positive");
+    if (c->sliding_window < 0) bad("gemma sliding window must be >= 0");
+}
+
+}  // namespace
+
+extern "C" {
+
+int sana_gemma_create(const sana_gemma_config * cfg, sana_gemma ** out) {
+    if (!cfg || !out) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    return guarded([&] {
+        validate_config(cfg);
+        int ndev = 0;
+        hip_check(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+        if (cfg->device < 0 || cfg->device >= ndev) throw_err(SANA_ERR_INVALID_ARGUMENT, "no such device");
+        hip_check(hipSetDevice(cfg->device), "hipSetDevice");
+        auto g = std::make_unique<sana_gemma>();
+        g->cfg = *cfg;
+        g->Dq = cfg->heads * cfg->head_dim;
+        g->Dkv = cfg->kv_heads * cfg->head_dim;
+        for (int64_t l = 0; l < cfg->layers; ++l) g->layers.push_back(std::make_unique<LayerDev>());
+        g->required = required_names(g.get());
+        hip_check(hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking), "hipStreamCreate");
+        *out = g.release();
+    });
+}
+
+int sana_gemma_destroy(sana_gemma * g) {
+    if (!g) return SANA_OK;
+    (void)hipSetDevice(g->cfg.device);
+    (void)hipDeviceSynchronize();
+    delete g;
+    return SANA_OK;
+}
+
+int sana_gemma_set_weight(sana_gemma * g, const char * name, const float * data, const int64_t * shape, int ndim) {
+    if (!g || !name || !data || !shape) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] {
+        hip_check(hipSetDevice(g->cfg.device), "hipSetDevice");
+        set_weight(g, name, data, shape, ndim);
+    });
+}
+
+int sana_gemma_check_weights(sana_gemma * g) {
+    if (!g) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] { check_ready(g); });
+}
+
+int sana_gemma_load_gguf(sana_gemma * g, const char * path) {
+    if (!g || !path) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] {
+        using namespace sana::gguf;
+        hip_check(hipSetDevice(g->cfg.device), "hipSetDevice");
+        Index idx;
+        try {
+            idx = read_index(path);
+        } catch (const std::exception & e) {
+            throw_err(SANA_ERR_IO, e.what());
+        }
+        MappedFile f(path);
+        std::map<std::string, const TensorInfo *> by;
+        for (const auto & t : idx.tensors) by[t.name] = &t;
+        std::vector<float> tmp;
+        for (const std::string & n : g->required) {
+            auto it = by.find(n);
+            if (it == by.end()) throw_err(SANA_ERR_INVALID_ARGUMENT, "weight name not found in weight index: " + n);
+            const TensorInfo & t = *it->second;
+            size_t cnt = 1;
+            for (int64_t dd : t.shape) cnt *= (size_t)dd;
+            const float * src;
+            if (t.type == kF32) {
+                src = reinterpret_cast<const float *>(f.data() + t.offset);
+            } else if (t.type == kF16 || t.type == kBF16) {
+                tmp.resize(cnt);
+                const uint16_t * h = reinterpret_cast<const uint16_t *>(f.data() + t.offset);
+                for (size_t i = 0; i < cnt; ++i) {
+                    if (t.type == kF16) {
+                        _Float16 x;
+                        std::memcpy(&x, h + i, 2);
+                        tmp[i] = (float)x;
+                    } else {
+                        const uint32_t u = (uint32_t)h[i] << 16;
+                        std::memcpy(&tmp[i], &u, 4);
+                    }
+                }
+                src = tmp.data();
+            } else {
+                throw_err(SANA_ERR_FORMAT, "unsupported gguf tensor type for " + t.name);
+            }
+            set_weight(g, n, src, t.shape.data(), (int)t.shape.size());
+        }
+    });
+}
+
+int sana_gemma_encode(sana_gemma * g, const int32_t * tokens, int64_t n, float * hidden) {
+    if (!g || !tokens || !hidden) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] {
+        hip_check(hipSetDevice(g->cfg.device), "hipSetDevice");
+        check_ready(g);
+        if (n <= 0 || n > 8192) throw_err(SANA_ERR_INVALID_ARGUMENT, "gemma token count must be in [1, 8192]");
+        for (int64_t i = 0; i < n; ++i)
+            if (tokens[i] < 0 || tokens[i] >= g->cfg.vocab)
+                throw_err(SANA_ERR_INVALID_ARGUMENT, "gemma token id out of range at position " + std::to_string(i));
+        ensure_workspace(g, n);
+        hip_check(hipMemcpyAsync(g->tok.p, tokens, (size_t)n * 4, hipMemcpyHostToDevice, g->stream), "upload tokens");
+        encode(g, n, g->stream);
+        hip_check(hipMemcpyAsync(hidden, g->out32.p, (size_t)n * g->cfg.hidden * 4, hipMemcpyDeviceToHost, g->stream),
+                  "download hidden");
+        hip_check(hipStreamSynchronize(g->stream), "gemma encode");
+    });
+}
+
+}  // extern "C"

@@ -40,6 +40,13 @@ class VaeConfig(ctypes.Structure):
                 ("scaling_factor", ctypes.c_float), ("device", ctypes.c_int)]
 
 
+class GemmaConfig(ctypes.Structure):
+    _fields_ = [("vocab", _i64), ("hidden", _i64), ("layers", _i64), ("heads", _i64), ("kv_heads", _i64),
+                ("head_dim", _i64), ("ffn", _i64), ("sliding_window", _i64), ("rms_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float), ("attn_softcap", ctypes.c_float), ("query_scale", ctypes.c_float),
+                ("device", ctypes.c_int)]
+
+
 # name -> (restype, argtypes); exactly the entry points of include/sana_dit.h
 PROTOTYPES = {
     "sana_dit_last_error": (ctypes.c_char_p, []),
@@ -88,6 +95,12 @@ PROTOTYPES = {
     "sana_vae_load_gguf": (ctypes.c_int, [_vp, ctypes.c_char_p]),
     "sana_vae_decode": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp]),
     "sana_vae_decoder_input": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
+    "sana_gemma_create": (ctypes.c_int, [ctypes.POINTER(GemmaConfig), ctypes.POINTER(_vp)]),
+    "sana_gemma_destroy": (ctypes.c_int, [_vp]),
+    "sana_gemma_set_weight": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, ctypes.POINTER(_i64), ctypes.c_int]),
+    "sana_gemma_check_weights": (ctypes.c_int, [_vp]),
+    "sana_gemma_load_gguf": (ctypes.c_int, [_vp, ctypes.c_char_p]),
+    "sana_gemma_encode": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "sana_vae_decode_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "sana_op_gemm_f32": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, ctypes.c_int, _vp, _i64,
                                         _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
@@ -396,3 +409,63 @@ class Vae:
     def decode_device(self, latent, shape, image, stream):
         B, _, H, W = shape
         check(lib().sana_vae_decode_device(self.h, ptr(latent), B, H, W, ptr(image), stream))
+
+
+GEMMA2_2B = dict(vocab=256000, hidden=2304, layers=26, heads=8, kv_heads=4, head_dim=256, ffn=9216,
+                 sliding_window=4096, rms_eps=1e-6, rope_theta=10000.0, softcap=50.0, query_scale=1.0 / 16.0)
+
+
+def gemma_manifest(vocab, hidden, layers, heads, kv_heads, head_dim, ffn, **_):
+    """{GGUF tensor name: PyTorch-order shape} of a Gemma-2 encoder as llama.cpp names it."""
+    Dq, Dkv = heads * head_dim, kv_heads * head_dim
+    m = {"token_embd.weight": (vocab, hidden), "output_norm.weight": (hidden,)}
+    for l in range(layers):
+        p = f"blk.{l}."
+        m.update({p + "attn_norm.weight": (hidden,), p + "attn_q.weight": (Dq, hidden),
+                  p + "attn_k.weight": (Dkv, hidden), p + "attn_v.weight": (Dkv, hidden),
+                  p + "attn_output.weight": (hidden, Dq), p + "post_attention_norm.weight": (hidden,),
+                  p + "ffn_norm.weight": (hidden,), p + "ffn_gate.weight": (ffn, hidden),
+                  p + "ffn_up.weight": (ffn, hidden), p + "ffn_down.weight": (hidden, ffn),
+                  p + "post_ffw_norm.weight": (hidden,)})
+    return m
+
+
+class Gemma:
+    """One device context of the Gemma-2 text encoder.  cfg keys as GEMMA2_2B."""
+
+    def __init__(self, cfg, device=0):
+        c = GemmaConfig()
+        c.vocab, c.hidden, c.layers, c.heads = cfg["vocab"], cfg["hidden"], cfg["layers"], cfg["heads"]
+        c.kv_heads, c.head_dim, c.ffn = cfg["kv_heads"], cfg["head_dim"], cfg["ffn"]
+        c.sliding_window, c.rms_eps, c.rope_theta = cfg["sliding_window"], cfg["rms_eps"], cfg["rope_theta"]
+        c.attn_softcap, c.query_scale, c.device = cfg["softcap"], cfg["query_scale"], device
+        self.cfg = dict(cfg)
+        h = _vp()
+        check(lib().sana_gemma_create(ctypes.byref(c), ctypes.byref(h)))
+        self.h = h
+        self._destroy = lib().sana_gemma_destroy
+
+    def close(self):
+        if getattr(self, "h", None):
+            self._destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def set_weight(self, name, arr):
+        arr = _f32(arr)
+        shape = (_i64 * arr.ndim)(*arr.shape)
+        check(lib().sana_gemma_set_weight(self.h, name.encode(), ptr(arr), shape, arr.ndim))
+
+    def check_weights(self):
+        check(lib().sana_gemma_check_weights(self.h))
+
+    def load_gguf(self, path):
+        check(lib().sana_gemma_load_gguf(self.h, str(path).encode()))
+
+    def encode(self, tokens):
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty((tokens.size, self.cfg["hidden"]), np.float32)
+        check(lib().sana_gemma_encode(self.h, ptr(tokens), tokens.size, ptr(out)))
+        return out

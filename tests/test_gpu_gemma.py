@@ -1,0 +1,111 @@
+"""Gemma-2 text encoder on the GPU (sana_gemma_* C ABI) against the oracle.
+
+The oracle (oracle/gemma_oracle.py) restates the Gemma-2 forward that the
+reference runs through llama.cpp and is pinned against transformers'
+Gemma2Model (tests/test_oracle_gemma.py).  The HIP path (fp16 GEMM operands,
+fp32 accumulation, residual, norms and softmax) is held to a relative L2 of
+2e-3 on the hidden states, the per-forward bar of the DiT.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from gguf_writer import GGML_F16, write_gguf
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle"))
+import gemma_oracle as G  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+CONFIGS = {
+    "gqa_window": dict(vocab=300, hidden=256, layers=2, heads=4, kv_heads=2, head_dim=64, ffn=512, sliding_window=8,
+                       rms_eps=1e-6, rope_theta=10000.0, softcap=50.0, query_scale=1 / 8),
+    "mqa_softcap": dict(vocab=200, hidden=192, layers=3, heads=2, kv_heads=1, head_dim=128, ffn=320,
+                        sliding_window=0, rms_eps=1e-6, rope_theta=10000.0, softcap=2.0, query_scale=128 ** -0.5),
+    # the Gemma-2 2B layer shapes, two layers and a small vocabulary
+    "gemma2_2b_2layers": dict(G.GEMMA2_2B, vocab=1024, layers=2),
+}
+
+
+def build(cfg, seed=5, scale=0.05):
+    import sana_dit
+    w = G.random_weights(cfg, seed=seed, scale=scale)
+    dev = sana_dit.Gemma(cfg)
+    for name, arr in w.items():
+        dev.set_weight(name, arr)
+    dev.check_weights()
+    return w, dev
+
+
+@pytest.mark.parametrize("name,T", [("gqa_window", 37), ("gqa_window", 64), ("mqa_softcap", 19),
+                                    ("gemma2_2b_2layers", 438)])
+def test_encode_vs_oracle(name, T):
+    cfg = CONFIGS[name]
+    w, dev = build(cfg)
+    try:
+        tokens = np.random.default_rng(T).integers(0, cfg["vocab"], size=T)
+        print(f"{name} T={T}: oracle forward on the host ...", flush=True)
+        ref = G.forward(w, cfg, tokens)
+        got = dev.encode(tokens)
+        err = rel_l2(got, ref)
+        print(f"{name} T={T}: hidden rel_l2 {err:.3e}")
+        assert got.shape == (T, cfg["hidden"])
+        assert np.isfinite(got).all()
+        assert err < TOL
+        assert np.array_equal(dev.encode(tokens), got)
+    finally:
+        dev.close()
+
+
+def test_prefix_positions_are_causal():
+    """Causal attention: the hidden states of a prefix do not depend on the
+    tokens after it (the reference pads prompts at the end for this reason)."""
+    cfg = CONFIGS["gqa_window"]
+    w, dev = build(cfg)
+    try:
+        tokens = np.random.default_rng(3).integers(0, cfg["vocab"], size=40)
+        a = dev.encode(tokens)
+        b = dev.encode(np.concatenate([tokens[:25], np.zeros(15, np.int64)]))
+        assert rel_l2(b[:25], a[:25]) < 1e-6
+    finally:
+        dev.close()
+
+
+def test_load_gguf(tmp_path):
+    cfg = CONFIGS["gqa_window"]
+    w = G.random_weights(cfg, seed=5, scale=0.05)
+    path = str(tmp_path / "gemma.gguf")
+    write_gguf(path, w, ggml_type=GGML_F16)
+    import sana_dit
+    dev = sana_dit.Gemma(cfg)
+    try:
+        dev.load_gguf(path)
+        dev.check_weights()
+        tokens = np.random.default_rng(9).integers(0, cfg["vocab"], size=21)
+        w16 = {k: v.astype(np.float16).astype(np.float32) for k, v in w.items()}
+        assert rel_l2(dev.encode(tokens), G.forward(w16, cfg, tokens)) < TOL
+    finally:
+        dev.close()
+
+
+def test_rejects_bad_input():
+    import sana_dit
+    with pytest.raises(sana_dit.SanaError):
+        sana_dit.Gemma(dict(CONFIGS["gqa_window"], heads=3))       # heads % kv_heads
+    with pytest.raises(sana_dit.SanaError):
+        sana_dit.Gemma(dict(CONFIGS["gqa_window"], head_dim=48))   # head dim % 64
+    cfg = CONFIGS["gqa_window"]
+    w, dev = build(cfg)
+    try:
+        with pytest.raises(sana_dit.SanaError) as e:
+            dev.encode(np.array([1, cfg["vocab"]]))
+        assert e.value.code == sana_dit.SANA_ERR_INVALID_ARGUMENT
+        with pytest.raises(sana_dit.SanaError) as e:
+            dev.set_weight("blk.0.attn_q.weight", np.zeros((3, 3), np.float32))
+        assert e.value.code == sana_dit.SANA_ERR_SHAPE
+    finally:
+        dev.close()
