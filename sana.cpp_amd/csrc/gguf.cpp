@@ -43,6 +43,46 @@ struct Reader {
         pos += len;
         return s;
     }
+    double number(uint32_t t) {
+        switch (t) {
+            case kU8: return get<uint8_t>();
+            case kI8: return get<int8_t>();
+            case kBool: return get<uint8_t>() ? 1.0 : 0.0;
+            case kU16: return get<uint16_t>();
+            case kI16: return get<int16_t>();
+            case kU32: return get<uint32_t>();
+            case kI32: return get<int32_t>();
+            case kF32v: return get<float>();
+            case kU64: return (double)get<uint64_t>();
+            case kI64: return (double)get<int64_t>();
+            case kF64: return get<double>();
+            default: throw std::runtime_error("not a numeric gguf metadata type in " + path);
+        }
+    }
+    // Reads one value into v (arrays of scalars and strings; nested arrays skipped).
+    void value(uint32_t t, MetaValue & v) {
+        v.type = t;
+        if (t == kString) {
+            v.str = str();
+        } else if (t == kArray) {
+            const uint32_t et = get<uint32_t>();
+            const uint64_t cnt = get<uint64_t>();
+            v.elem_type = et;
+            if (et == kArray) {
+                for (uint64_t i = 0; i < cnt; ++i) skip_value(et, 1);
+            } else if (et == kString) {
+                if (cnt > n) throw std::runtime_error("implausible gguf array length in " + path);
+                v.strs.reserve(cnt);
+                for (uint64_t i = 0; i < cnt; ++i) v.strs.push_back(str());
+            } else {
+                if (cnt > n) throw std::runtime_error("implausible gguf array length in " + path);
+                v.nums.reserve(cnt);
+                for (uint64_t i = 0; i < cnt; ++i) v.nums.push_back(number(et));
+            }
+        } else {
+            v.num = number(t);
+        }
+    }
     void skip_value(uint32_t t, int depth = 0) {
         switch (t) {
             case kU8: case kI8: case kBool: need(1); pos += 1; break;
@@ -109,7 +149,7 @@ Index read_index(const std::string & path) {
             if (idx.alignment == 0 || (idx.alignment & (idx.alignment - 1)))
                 throw std::runtime_error("general.alignment must be a power of two: " + path);
         } else {
-            r.skip_value(t);
+            r.value(t, idx.meta[key]);
         }
     }
     std::set<std::string> seen;

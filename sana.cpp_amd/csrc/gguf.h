@@ -11,6 +11,7 @@
 #pragma once
 
 #include <cstdint>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -27,8 +28,20 @@ struct TensorInfo {
     uint64_t nbytes = 0;         // payload size (F32/F16/BF16), 0 for other types
 };
 
+// One metadata value: a scalar (number in `num`, text in `str`) or an array
+// of scalars (`nums` / `strs`, element type in `elem_type`).
+struct MetaValue {
+    uint32_t type = 0;       // GGUF value type; 9 = array
+    uint32_t elem_type = 0;  // arrays
+    double num = 0.0;
+    std::string str;
+    std::vector<double> nums;
+    std::vector<std::string> strs;
+};
+
 struct Index {
     std::string path;
+    std::map<std::string, MetaValue> meta;  // every key except arrays of arrays
     uint32_t version = 0;
     uint64_t alignment = 32;
     uint64_t data_offset = 0;

@@ -19,6 +19,16 @@
 //                            small synthetic DC-AE decoder) against the oracle's
 //                            tensors; with `run`, run_vae_decode and
 //                            run_vae_decoder_input on the GPU against the oracle
+//   dropin_test gemma-tok FILE CASES
+//                            gemma_encoder.h tokenizer on FILE (a GGUF with
+//                            SentencePiece vocabulary metadata) against the ids in
+//                            CASES (u32 length, text, u32 count, int32 ids ...);
+//                            select_rows_first_and_last known answers; no GPU
+//   dropin_test gemma FILE CASES OUT
+//                            encode_prompt_pair on FILE (vocabulary + weights) for
+//                            CASES (u32 length + prompt, u32 length + negative,
+//                            u32 max_sequence_length); writes embeddings then
+//                            attention bias (fp32) to OUT
 //   dropin_test full-loop CAPTION LATENT STEPS OUT
 //                            the denoise stage of sana_infer on the seeded
 //                            Sana-0.6B model (28 blocks, 36/16 heads, guidance
@@ -36,6 +46,7 @@
 #include <vector>
 
 #include "common_ops.h"
+#include "gemma_encoder.h"
 #include "oracle.h"
 #include "scheduler.h"
 #include "tensor.h"
@@ -833,6 +844,88 @@ void vae_tests(const std::string & path, bool run) {
     oracle_vae_destroy(o);
 }
 
+// ---------------------------------------------------------------- Gemma encoder (gemma_encoder.h)
+
+bool read_u32(std::ifstream & f, uint32_t & v) { return static_cast<bool>(f.read(reinterpret_cast<char *>(&v), 4)); }
+
+std::string read_text(std::ifstream & f) {
+    uint32_t n = 0;
+    if (!read_u32(f, n)) throw std::runtime_error("truncated cases file");
+    std::string s(n, '\0');
+    f.read(&s[0], n);
+    return s;
+}
+
+// select_rows_first_and_last: the reference's known answers (tests/test_gemma_encoder.cpp:7-33).
+void gemma_host_tests() {
+    Tensor input({10, 2});
+    for (size_t r = 0; r < 10; ++r) {
+        input.at({r, 0}) = static_cast<float>(2 * r);
+        input.at({r, 1}) = static_cast<float>(2 * r + 1);
+    }
+    const Tensor kept = select_rows_first_and_last(input, 4);
+    check(kept.shape() == std::vector<size_t>({4, 2}), "select_rows shape");
+    const float want[8] = {0, 1, 14, 15, 16, 17, 18, 19};
+    for (size_t i = 0; i < 8; ++i) check(kept.data()[i] == want[i], "select_rows value " + std::to_string(i));
+    check(select_rows_first_and_last(input, 10).data() == input.data(), "select_rows keep == rows");
+    check(select_rows_first_and_last(input, 1).data() == std::vector<float>({0, 1}), "select_rows keep == 1");
+    throws<std::invalid_argument>([&] { select_rows_first_and_last(input, 0); }, "select_rows keep 0");
+    throws<std::invalid_argument>([&] { select_rows_first_and_last(input, 11); }, "select_rows keep > rows");
+    throws<std::invalid_argument>([&] { select_rows_first_and_last(Tensor({2, 2, 2}), 1); }, "select_rows rank 3");
+}
+
+void gemma_tok_tests(const std::string & gguf, const std::string & cases) {
+    gemma_host_tests();
+    std::ifstream f(cases, std::ios::binary);
+    uint32_t n = 0;
+    int k = 0;
+    for (; f.peek() != EOF; ++k) {
+        const std::string text = read_text(f);
+        if (!read_u32(f, n)) throw std::runtime_error("truncated cases file");
+        std::vector<int32_t> want(n);
+        f.read(reinterpret_cast<char *>(want.data()), 4 * (std::streamsize)n);
+        const std::vector<int32_t> got = gemma_tokenize_gguf(gguf, text);
+        bool same = got == want;
+        if (!same) {
+            std::printf("  case %d: %zu ids, want %zu; first difference at", k, got.size(), want.size());
+            for (size_t i = 0; i < std::min(got.size(), want.size()); ++i)
+                if (got[i] != want[i]) {
+                    std::printf(" %zu (%d vs %d)", i, got[i], want[i]);
+                    break;
+                }
+            std::printf("\n");
+        }
+        check(same, "tokenization of case " + std::to_string(k));
+    }
+    std::printf("  %d tokenizer cases\n", k);
+}
+
+void gemma_tests(const std::string & gguf, const std::string & cases, const std::string & out_path) {
+    std::ifstream f(cases, std::ios::binary);
+    const std::string prompt = read_text(f), negative = read_text(f);
+    uint32_t L = 0;
+    if (!read_u32(f, L)) throw std::runtime_error("truncated cases file");
+    GemmaEncoderConfig cfg;
+    cfg.gguf_path = gguf;
+    GemmaEncoder enc(cfg);
+    const GemmaPromptPair pp = encode_prompt_pair(enc, prompt, negative, L);
+    check(pp.embeddings.rank() == 3 && pp.embeddings.dim_size(0) == 2 && pp.embeddings.dim_size(1) == L,
+          "prompt pair embeddings shape");
+    check(pp.attention_bias.shape() == std::vector<size_t>({2, 1, L}), "prompt pair bias shape");
+    std::ofstream o(out_path, std::ios::binary);
+    o.write(reinterpret_cast<const char *>(pp.embeddings.data().data()), (std::streamsize)(pp.embeddings.numel() * 4));
+    o.write(reinterpret_cast<const char *>(pp.attention_bias.data().data()),
+            (std::streamsize)(pp.attention_bias.numel() * 4));
+    check(static_cast<bool>(o), "prompt pair written");
+    throws<std::invalid_argument>([&] { encode_prompt_pair(enc, std::string(4 * L, 'x') + " y z", "", L); },
+                                  "prompt longer than the padded length");
+    throws<std::runtime_error>([&] {
+        GemmaEncoderConfig bad;
+        bad.gguf_path = gguf + ".missing";
+        GemmaEncoder e(bad);
+    }, "missing gguf");
+}
+
 }  // namespace
 
 int main(int argc, char ** argv) {
@@ -852,12 +945,16 @@ int main(int argc, char ** argv) {
             ops_random_tests();
         } else if (mode == "gguf" && argc > 2) {
             gguf_tests(argv[2], argc > 3 && std::string(argv[3]) == "run");
+        } else if (mode == "gemma-tok" && argc > 3) {
+            gemma_tok_tests(argv[2], argv[3]);
+        } else if (mode == "gemma" && argc > 4) {
+            gemma_tests(argv[2], argv[3], argv[4]);
         } else if (mode == "vae" && argc > 2) {
             vae_tests(argv[2], argc > 3 && std::string(argv[3]) == "run");
         } else if (mode == "full-loop" && argc > 5) {
             full_loop(argv[2], argv[3], std::strtoul(argv[4], nullptr, 10), argv[5]);
         } else {
-            std::fprintf(stderr, "usage: dropin_test cpu | gpu | ops | gguf FILE [run] | vae FILE [run] | full-loop CAPTION LATENT STEPS OUT\n");
+            std::fprintf(stderr, "usage: dropin_test cpu | gpu | ops | gguf FILE [run] | vae FILE [run] | gemma-tok FILE CASES | gemma FILE CASES OUT | full-loop CAPTION LATENT STEPS OUT\n");
             return 2;
         }
     } catch (const std::exception & e) {
