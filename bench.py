@@ -34,6 +34,9 @@ Prints ONE JSON line (rank 0, N = 1 only):
   vae_decode_1024px        the DC-AE decode of one 32x32x32 latent to a
                            1024x1024 image (the stage after the denoising
                            loop), ms and TFLOP/s
+  gemma_encode_prompt_pair the Gemma-2 2B text encoder over the prompt
+                           pair's two sequences (the stage before the loop),
+                           ms and TFLOP/s
 
 --pmc-calib adds, before the timed region, three launches of a plain copy
 kernel over 256 MiB (torch.neg: 256 MiB read + 256 MiB written), the known
@@ -294,6 +297,48 @@ def vae_decode_1024px(sana_dit, torch, dev, stream, rng):
                      "512/1024/1024 EfficientViT)"}
 
 
+def gemma_flops(T, c):
+    """2 x multiply-adds of one Gemma-2 encoder pass over T tokens: the q|k|v,
+    output, gate|up and down projections, and the causal score and P.V
+    products (full T x T, as computed)."""
+    H, Dq, Dkv, F = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["ffn"]
+    per_layer = 2 * T * (H * (Dq + 2 * Dkv) + Dq * H + 3 * H * F) + 2 * 2 * T * T * Dq
+    return c["layers"] * per_layer
+
+
+def gemma_prompt_pair(sana_dit, rng, pos_tokens=438, neg_tokens=300):
+    """Gemma-2 2B encoder (26 layers, 256000-token vocabulary) on the two
+    sequences encode_prompt_pair runs: the instruction-prefixed positive
+    prompt (instruction + 300 - 2 tokens) and the negative prompt (300).
+    Seeded N(0, 0.02) weights, one draw per tensor shape shared by the 26
+    layers; mean of 3 pairs after one warm-up."""
+    import numpy as np
+    c = sana_dit.GEMMA2_2B
+    g = sana_dit.Gemma(c)
+    by_shape = {}
+    for name, shape in sana_dit.gemma_manifest(**c).items():
+        if shape not in by_shape:
+            z = rng.standard_normal(shape, dtype=np.float32)
+            by_shape[shape] = 1 + np.float32(0.1) * z if len(shape) == 1 else z * np.float32(0.02)
+        g.set_weight(name, by_shape[shape])
+    g.check_weights()
+    pos = rng.integers(0, c["vocab"], size=pos_tokens)
+    neg = rng.integers(0, c["vocab"], size=neg_tokens)
+    g.encode(pos)
+    g.encode(neg)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        h = g.encode(pos)
+        g.encode(neg)
+    ms = (time.perf_counter() - t0) * 1e3 / 3
+    if not np.isfinite(h).all():
+        raise RuntimeError("non-finite Gemma hidden states")
+    g.close()
+    fl = gemma_flops(pos_tokens, c) + gemma_flops(neg_tokens, c)
+    return {"ms": round(ms, 3), "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "gflop": round(fl / 1e9, 1),
+            "shape": f"Gemma-2 2B, {pos_tokens} + {neg_tokens} tokens, host token ids in, host hidden states out"}
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (None when it is absent)."""
@@ -414,6 +459,7 @@ def main():
                                     "tokens": 128 * 128, "note": "28 blocks, CFG batch 2, context resident"}
         extras["microbench_4096_tokens"] = microbench_4096(sana_dit, torch, dev, stream)
         extras["vae_decode_1024px"] = vae_decode_1024px(sana_dit, torch, dev, stream, rng)
+        extras["gemma_encode_prompt_pair"] = gemma_prompt_pair(sana_dit, rng)
 
     peaks = measured_peaks(sana_dit, torch, dev, stream)
     lb_spec = step_lower_bound_ms(B, N, L, PEAK_MFMA_TFLOPS, PEAK_HBM_GBS)
