@@ -34,7 +34,19 @@
 //                            Sana-0.6B model (28 blocks, 36/16 heads, guidance
 //                            4.5): CAPTION [2,300,2304] and LATENT [1,32,32,32]
 //                            raw fp32 in, final latent raw fp32 out
+//   dropin_test pipeline GEMMA DIT VAE CASES OUT
+//                            the three stages of sana_infer chained through the
+//                            drop-in API (src/infer_main.cpp:152-181,341-398):
+//                            encode_prompt_pair on GEMMA, the seeded initial
+//                            latent, run_full_denoising_loop_with_cfg with the
+//                            encoder's attention bias on the weights of DIT (one
+//                            GGUF for the three indexes), run_vae_decode on VAE.
+//                            CASES: prompt, negative (u32 length + bytes), then
+//                            u32 max_sequence_length, steps, seed, latent side,
+//                            self heads, cross heads.  OUT: embeddings, bias,
+//                            initial latent, final latent, image (fp32)
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -926,6 +938,52 @@ void gemma_tests(const std::string & gguf, const std::string & cases, const std:
     }, "missing gguf");
 }
 
+// ---------------------------------------------------------------- the sana_infer chain
+
+void pipeline_tests(const std::string & gemma, const std::string & dit, const std::string & vae,
+                    const std::string & cases, const std::string & out_path) {
+    std::ifstream f(cases, std::ios::binary);
+    const std::string prompt = read_text(f), negative = read_text(f);
+    uint32_t p[6] = {};
+    for (uint32_t & v : p)
+        if (!read_u32(f, v)) throw std::runtime_error("truncated cases file");
+    const size_t L = p[0], steps = p[1], seed = p[2], side = p[3];
+    using clock = std::chrono::steady_clock;
+    auto ms = [](clock::time_point a, clock::time_point b) {
+        return std::chrono::duration<double, std::milli>(b - a).count();
+    };
+    // loading (untimed, as bench_full_pipeline loads before its timed runs)
+    GemmaEncoderConfig gc;
+    gc.gguf_path = gemma;
+    GemmaEncoder enc(gc);
+    const auto di = load_weight_index(dit);
+    const SanaDenoiserWeights dw = load_denoiser_weights(dit, di, dit, di, dit, di, p[4], p[5]);
+    const auto vi = load_weight_index(vae);
+    const SanaVaeWeights vw = load_vae_weights(vae, vi, 0.41407f, 32);
+    validate_vae_weights(vw);
+
+    const auto t0 = clock::now();
+    const GemmaPromptPair pp = encode_prompt_pair(enc, prompt, negative, L);
+    const Tensor latent = randn_torch_cpu({1, 32, side, side}, seed);
+    const auto t1 = clock::now();
+    const SanaSchedulerConfig cfg = make_sana_scheduler_config();
+    SanaSchedulerState st = init_sana_scheduler_state(steps, cfg);
+    const Tensor fin = run_full_denoising_loop_with_cfg(latent, pp.embeddings, 4.5f, st, cfg, dw, &pp.attention_bias);
+    const auto t2 = clock::now();
+    const Tensor img = run_vae_decode(fin, vw);
+    const auto t3 = clock::now();
+    std::printf("  stages (ms): encode %.2f  denoise (%zu steps) %.2f  vae %.2f  total %.2f\n", ms(t0, t1), steps,
+                ms(t1, t2), ms(t2, t3), ms(t0, t3));
+    check(pp.embeddings.shape() == std::vector<size_t>({2, L, pp.embeddings.dim_size(2)}), "embeddings shape");
+    check(st.step_index == steps, "loop consumed the schedule");
+    check(fin.shape() == latent.shape(), "final latent shape");
+    check(img.shape() == std::vector<size_t>({1, 3, 8 * side, 8 * side}), "image shape");
+    std::ofstream o(out_path, std::ios::binary);
+    for (const Tensor * t : {&pp.embeddings, &pp.attention_bias, &latent, &fin, &img})
+        o.write(reinterpret_cast<const char *>(t->data().data()), static_cast<std::streamsize>(t->numel() * 4));
+    check(static_cast<bool>(o), "pipeline outputs written");
+}
+
 }  // namespace
 
 int main(int argc, char ** argv) {
@@ -951,10 +1009,12 @@ int main(int argc, char ** argv) {
             gemma_tests(argv[2], argv[3], argv[4]);
         } else if (mode == "vae" && argc > 2) {
             vae_tests(argv[2], argc > 3 && std::string(argv[3]) == "run");
+        } else if (mode == "pipeline" && argc > 6) {
+            pipeline_tests(argv[2], argv[3], argv[4], argv[5], argv[6]);
         } else if (mode == "full-loop" && argc > 5) {
             full_loop(argv[2], argv[3], std::strtoul(argv[4], nullptr, 10), argv[5]);
         } else {
-            std::fprintf(stderr, "usage: dropin_test cpu | gpu | ops | gguf FILE [run] | vae FILE [run] | gemma-tok FILE CASES | gemma FILE CASES OUT | full-loop CAPTION LATENT STEPS OUT\n");
+            std::fprintf(stderr, "usage: dropin_test cpu | gpu | ops | gguf FILE [run] | vae FILE [run] | gemma-tok FILE CASES | gemma FILE CASES OUT | pipeline GEMMA DIT VAE CASES OUT | full-loop CAPTION LATENT STEPS OUT\n");
             return 2;
         }
     } catch (const std::exception & e) {
