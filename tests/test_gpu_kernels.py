@@ -219,7 +219,8 @@ def _xattn(L, q, k, v, H, bias):
 
 @pytest.mark.parametrize("B,N,Lk,H,D,masked", [(2, 1024, 300, 16, 72, False), (2, 256, 300, 16, 72, True),
                                                (1, 70, 33, 4, 32, False), (1, 2, 2, 1, 2, False),
-                                               (1, 17, 5, 3, 12, True)])
+                                               (1, 17, 5, 3, 12, True), (1, 130, 150, 2, 64, True),
+                                               (2, 200, 100, 4, 72, False)])
 def test_cross_attention(L, B, N, Lk, H, D, masked):
     rng = np.random.default_rng(N + Lk)
     C = H * D
