@@ -1127,12 +1127,10 @@ hipError_t cross_attention(const half_t * q, int64_t ldq, const half_t * k, int6
     const bool out_vec = ldo % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;  // 8-byte output stores
     if (vec && out_vec && D <= 96 && lt32 <= 10 && ldvt >= (int64_t)lt32 * 32) {
         // key-split kernel by default (1024 queries x 300 keys x 16 heads of 72: 12.8 us
-        // against 17.3 us for one wave per query group); SANA_XATTN_SPLIT=0 selects the latter
-        static const int split = [] {
-            const char * e = std::getenv("SANA_XATTN_SPLIT");
-            return e ? std::atoi(e) : 1;
-        }();
-        if (split) {
+        // against 17.3 us for one wave per query group); SANA_XATTN_SPLIT=0 selects the
+        // latter (read at every launch, so a process can compare both)
+        const char * split_env = std::getenv("SANA_XATTN_SPLIT");
+        if (!split_env || std::atoi(split_env) != 0) {
             if (lt32 <= 2) return launch_xattn_split<2>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
             if (lt32 <= 4) return launch_xattn_split<4>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
             return launch_xattn_split<10>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);

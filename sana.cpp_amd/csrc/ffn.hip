@@ -150,10 +150,9 @@ hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const flo
     if (vec) {
         // row segments of 4 tokens (1024 tokens x 2880 channels: 10.0 us against 10.8 us with
         // segments of 8, inputs cycled through 8 buffers); SANA_DWGLU_XS selects 2, 8 or 16
-        static const int xs_env = [] {
-            const char * e = std::getenv("SANA_DWGLU_XS");
-            return e ? std::atoi(e) : 4;
-        }();
+        // (read at every launch)
+        const char * xs_str = std::getenv("SANA_DWGLU_XS");
+        const int xs_env = xs_str ? std::atoi(xs_str) : 4;
         auto run = [&](auto xs_tag) {
             constexpr int XS = decltype(xs_tag)::value;
             const int nseg = (Ww + XS - 1) / XS;

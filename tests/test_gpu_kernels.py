@@ -221,7 +221,12 @@ def _xattn(L, q, k, v, H, bias):
                                                (1, 70, 33, 4, 32, False), (1, 2, 2, 1, 2, False),
                                                (1, 17, 5, 3, 12, True), (1, 130, 150, 2, 64, True),
                                                (2, 200, 100, 4, 72, False)])
-def test_cross_attention(L, B, N, Lk, H, D, masked):
+@pytest.mark.parametrize("variant", ["split", "single"])
+def test_cross_attention(L, B, N, Lk, H, D, masked, variant, monkeypatch):
+    # "split": 8 waves per 128 queries, one key half each (the default);
+    # "single": one wave per 32 queries over all keys (SANA_XATTN_SPLIT=0)
+    if variant == "single":
+        monkeypatch.setenv("SANA_XATTN_SPLIT", "0")
     rng = np.random.default_rng(N + Lk)
     C = H * D
     q = f16(rng.standard_normal((B, N, C)))
@@ -239,7 +244,10 @@ def test_cross_attention(L, B, N, Lk, H, D, masked):
 
 
 @pytest.mark.parametrize("B,S,F", [(2, 32, 2880), (2, 64, 2880), (1, 37, 40), (1, 16, 64), (1, 3, 5), (2, 1, 8)])
-def test_dwconv_glu(L, B, S, F):
+@pytest.mark.parametrize("xs", ["4", "2", "8", "16"])
+def test_dwconv_glu(L, B, S, F, xs, monkeypatch):
+    # xs: tokens per row segment of a thread (SANA_DWGLU_XS; 4 is the default)
+    monkeypatch.setenv("SANA_DWGLU_XS", xs)
     rng = np.random.default_rng(S + F)
     E = 2 * F
     x = f16(rng.standard_normal((B, S, S, E)))
