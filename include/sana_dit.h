@@ -132,7 +132,9 @@ int sana_dit_denoise_loop_device(sana_dit * ctx, const float * d_latent, int64_t
 /* The converted model outputs (x0 = sample - sigma * guided prediction) of the
  * last two steps of the last denoise loop on this context, [Bl, Cl, H, W]
  * each: the previous_model_outputs a host scheduler state holds after the loop
- * (src/scheduler.cpp:286-290).  x0_prev is left untouched after a one-step loop. */
+ * (src/scheduler.cpp:286-290).  x0_prev is left untouched after a one-step loop.
+ * The copies wait for the loop's last step on whatever stream the loop was
+ * queued on, then return (blocking). */
 int sana_dit_loop_model_outputs(sana_dit * ctx, float * x0_prev, float * x0_last);
 /* Time MLP of the forward (src/transformer.cpp:638-656): B timesteps ->
  * embedded [B, C] (pre-SiLU) and t_mod [B, 6C]. */

@@ -2,8 +2,6 @@
 #include <algorithm>
 #include <cmath>
 
-#include <cstdlib>
-
 #include "hip_common.h"
 #include "kernels.h"
 
@@ -596,290 +594,146 @@ __global__ __launch_bounds__(256) void xattn_kernel(const f16 * __restrict__ q, 
     }
 }
 
-// Fast path of K4 for L <= 32 * LT (<= 320 keys) and D <= 96, D % 8 == 0.
-// One workgroup per (b, h, 128 queries); the head's K [keys][d] and V^T
-// [d][keys] are staged in LDS once and shared by the 4 waves (32 queries
-// each).  Scores are computed transposed, S^T = K . Q^T on
-// v_mfma_f32_32x32x16_f16, so each lane holds one query column: the softmax
-// max and sum over keys are in-lane plus one cross-half shuffle.  exp(S^T) in
-// fp16 then feeds O^T = V^T . P^T directly from registers as the B operand; the
-// key order inside each 16-key MFMA step is permuted identically in both
-// operands (lane half h supplies keys 4h..4h+3 and 8+4h..8+4h+3), which leaves
-// the sum over keys unchanged.
+// Fast path of K4 for L <= 32 * LT (<= 320 keys), D <= 96, D % 8 == 0.
 //
-// With 1024 queries per (b, h) there are only four waves per CU, so the
-// kernel is latency-bound and written for instruction-level parallelism: the
-// query fragments and all staging loads are issued before the first wait,
-// key masking is branch-free (keys >= L carry a -inf bias in LDS, so their
-// probability is exactly 0), the exponent is one v_exp_f32 on log2-scaled
-// scores, and the P.V product keeps one accumulator per 32-dim tile so the
-// MFMA chains are independent.
+// One workgroup of 8 waves per (head, 128 queries, batch row).  The grid is
+// head-major (blockIdx.x = head): consecutive workgroup ids go to different
+// XCDs, so each XCD's L2 holds the K/V of H/8 heads instead of all of them.
+//
+// The head's K [keys][KROW] and V^T [dims][VROW] are staged in LDS once and
+// shared by the 8 waves; wave w takes query group w & 3 (32 queries) and key
+// half w >> 2.  Scores are computed transposed, S^T = K . Q^T on
+// v_mfma_f32_32x32x16_f16, so each lane holds one query column and the
+// softmax max is in-lane plus one cross-half shuffle.  exp(S^T) in fp16 feeds
+// O^T = V^T . P^T straight from registers as the B operand: in each 16-key
+// step lane half hh holds keys 4hh..4hh+3 and 8+4hh..8+4hh+3 (the rows the
+// score MFMA leaves in it), and V^T is staged with its keys permuted the same
+// way inside every 16-key group, so the A operand is one 16-byte LDS read.
+// When D is not a multiple of 32, the last staged V^T row (a padding row of
+// the last 32-dim tile) holds 1 for every key < L, so the same MFMA also
+// produces the softmax denominator sum_k p_k.  The two key halves' (max, O^T) are merged
+// through LDS: O = O_0 2^(m_0 - m) + O_1 2^(m_1 - m), m = max(m_0, m_1).
+//
+// Staging issues every 16-byte load before the first use, with a
+// power-of-two thread -> (row, chunk) map; chunks outside the head are
+// written as zeros instead of loaded, so no load waits behind a branch.
 constexpr int kXaQ = 128;  // queries per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
-template <int LT>
-__global__ __launch_bounds__(256) void xattn_fast_kernel(const f16 * __restrict__ q, int64_t ldq,
-                                                         const f16 * __restrict__ k, int64_t ldk,
-                                                         const f16 * __restrict__ vt, int64_t ldvt,
-                                                         const float * __restrict__ bias, f16 * __restrict__ out,
-                                                         int64_t ldo, int N, int L, int H, int D, float scale) {
-    constexpr int LP = LT * 32;
-    constexpr int KROW = 96 + 8;    // halves per K row (d padded, 208 B rows)
-    constexpr int VROW = LP + 8;    // halves per V^T row
-    constexpr int KCH = KROW / 8;   // 16-byte chunks per staged K row
-    constexpr int VCH = VROW / 8;
-    constexpr int KN = (LP * KCH + 255) / 256;  // K chunks per thread
-    constexpr int VN = (96 * VCH + 255) / 256;  // V^T chunks per thread
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    f16 * Ks = reinterpret_cast<f16 *>(smem);                       // [LP][KROW]
-    f16 * Vs = Ks + LP * KROW;                                       // [96][VROW]
-    float * bs = reinterpret_cast<float *>(Vs + 96 * VROW);          // [LP], log2-scaled bias, -inf past L
-    const int h = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int hh = lane >> 5;
-    const int KS = (D + 15) / 16;   // 16-deep steps over head dims (<= 6)
-    const int DT = (D + 31) / 32;   // 32-wide output dim tiles (<= 3)
-    const int q0 = blockIdx.x * kXaQ + w * 32;
 
-    // query fragments of this lane's column (issued first; independent of LDS)
-    const int qcol = min(q0 + (lane & 31), N - 1);
-    const f16 * qr = q + ((int64_t)b * N + qcol) * ldq + (int64_t)h * D;
-    f16x8 qf[6];
-#pragma unroll
-    for (int ks = 0; ks < 6; ++ks) {
-        const int d0 = ks * 16 + 8 * hh;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[ks][e] = (f16)0.0f;
-        if (ks < KS && d0 + 8 <= D) qf[ks] = *reinterpret_cast<const f16x8 *>(qr + d0);
-    }
+template <int LT, int KS>
+struct XaCfg {
+    static constexpr int LP = LT * 32;              // keys, padded to the score tile
+    static constexpr int KROW = KS * 16 + 8;        // halves per staged K row (72, 88, 104: conflict-free reads)
+    static constexpr int DT = (KS * 16 + 31) / 32;  // 32-wide output dim tiles
+    static constexpr int DP = DT * 32;              // staged V^T rows
+    static constexpr int VROW = LP + 8;             // halves per staged V^T row
+    static constexpr int K_BYTES = LP * KROW * 2;
+    static constexpr int V_BYTES = DP * VROW * 2;
+    static constexpr int MERGE_BYTES = 4 * (DT * 16 + 2) * 64 * 4;
+    static constexpr int STAGE_BYTES = K_BYTES + V_BYTES + LP * 4;
+    static constexpr int LDS_BYTES = STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES;
+};
 
-    // stage K rows (zero past D and past L) and V^T rows (zero past D and past
-    // L, whatever the padding of vt holds): all loads in flight before the LDS
-    // stores
-    const f16 * kb = k + (int64_t)b * L * ldk + (int64_t)h * D;
-    const f16 * vb = vt + ((int64_t)b * H * D + (int64_t)h * D) * ldvt;
-    f16x8 kreg[KN], vreg[VN];
-#pragma unroll
-    for (int j = 0; j < KN; ++j) {
-        const int idx = tid + 256 * j;
-        const int key = idx / KCH, c8 = (idx - key * KCH) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kreg[j][e] = (f16)0.0f;
-        if (idx < LP * KCH && key < L && c8 < D) kreg[j] = *reinterpret_cast<const f16x8 *>(kb + (int64_t)key * ldk + c8);
-    }
-#pragma unroll
-    for (int j = 0; j < VN; ++j) {
-        const int idx = tid + 256 * j;
-        const int dim = idx / VCH, c8 = (idx - dim * VCH) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vreg[j][e] = (f16)0.0f;
-        if (idx < 96 * VCH && dim < D && c8 < L) vreg[j] = *reinterpret_cast<const f16x8 *>(vb + (int64_t)dim * ldvt + c8);
-        if (c8 + 8 > L) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (c8 + e >= L) vreg[j][e] = (f16)0.0f;
-        }
-    }
-    for (int key = tid; key < LP; key += 256)
-        bs[key] = key < L ? (bias ? bias[(int64_t)b * L + key] * kLog2e : 0.0f) : -INFINITY;
-#pragma unroll
-    for (int j = 0; j < KN; ++j) {
-        const int idx = tid + 256 * j;
-        if (idx < LP * KCH) *reinterpret_cast<f16x8 *>(Ks + idx * 8) = kreg[j];
-    }
-#pragma unroll
-    for (int j = 0; j < VN; ++j) {
-        const int idx = tid + 256 * j;
-        if (idx < 96 * VCH) *reinterpret_cast<f16x8 *>(Vs + idx * 8) = vreg[j];
-    }
-    __syncthreads();
-    if (q0 >= N) return;
-
-    // S^T[key][q] (log2-scaled): tile t holds keys 32t + 8*(i/4) + 4*hh + i%4 for the lane's query.
-    f32x16 st[LT];
-#pragma unroll
-    for (int t = 0; t < LT; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st[t][i] = 0.0f;
-#pragma unroll
-    for (int ks = 0; ks < 6; ++ks) {
-        if (ks >= KS) break;
-        const int d0 = ks * 16 + 8 * hh;
-#pragma unroll
-        for (int t = 0; t < LT; ++t) {
-            const f16x8 kf = *reinterpret_cast<const f16x8 *>(Ks + (t * 32 + (lane & 31)) * KROW + d0);
-            st[t] = mfma_32x32x16(kf, qf[ks], st[t]);
-        }
-    }
-    const float scale2 = scale * kLog2e;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < LT; ++t)
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-            const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bs + t * 32 + 8 * i4 + 4 * hh);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float sv = st[t][4 * i4 + u] * scale2 + b4[u];
-                st[t][4 * i4 + u] = sv;
-                mx = fmaxf(mx, sv);
-            }
-        }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    float sum = 0.0f;
-    f16x8 pf[LT][2];  // P^T as the B operand: [tile][16-key step], slot u -> i = 8*step + u
-#pragma unroll
-    for (int t = 0; t < LT; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float e = __builtin_amdgcn_exp2f(st[t][i] - mx);
-            sum += e;
-            pf[t][i >> 3][i & 7] = (f16)e;
-        }
-    sum += __shfl_xor(sum, 32, 64);
-    const float rs = 1.0f / sum;
-
-    // O^T[dim][q] = V^T . P^T, one accumulator per 32-dim tile; A lane (dim, hh)
-    // supplies keys 16s + 4hh + {0..3} and 16s + 8 + 4hh + {0..3}.
-    f32x16 o[3];
-#pragma unroll
-    for (int dt = 0; dt < 3; ++dt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
-#pragma unroll
-    for (int t = 0; t < LT; ++t)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            const int kbase = t * 32 + 16 * s2 + 4 * hh;
-#pragma unroll
-            for (int dt = 0; dt < 3; ++dt) {
-                if (dt >= DT) break;
-                const f16 * vrow = Vs + (dt * 32 + (lane & 31)) * VROW;
-                const f16x4 lo4 = *reinterpret_cast<const f16x4 *>(vrow + kbase);
-                const f16x4 hi4 = *reinterpret_cast<const f16x4 *>(vrow + kbase + 8);
-                f16x8 af;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    af[e] = lo4[e];
-                    af[4 + e] = hi4[e];
-                }
-                o[dt] = mfma_32x32x16(af, pf[t][s2], o[dt]);
-            }
-        }
-    // lane holds query column (lane & 31), dims dt*32 + 8*(i/4) + 4*hh + i%4:
-    // four consecutive dims per 8-byte store (D % 8 == 0, rows 16-byte aligned)
-    const int qq = q0 + (lane & 31);
-    if (qq < N) {
-        f16 * orow = out + ((int64_t)b * N + qq) * ldo + (int64_t)h * D;
-#pragma unroll
-        for (int dt = 0; dt < 3; ++dt) {
-            if (dt >= DT) break;
-#pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {
-                const int dim = dt * 32 + 8 * i4 + 4 * hh;
-                if (dim < D) {
-                    f16x4 v4;
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) v4[u] = (f16)(o[dt][4 * i4 + u] * rs);
-                    *reinterpret_cast<f16x4 *>(orow + dim) = v4;
-                }
-            }
-        }
-    }
-}
-
-template <int LT>
-hipError_t launch_xattn_fast(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
-                             const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D,
-                             float scale, hipStream_t s) {
-    constexpr int LP = LT * 32;
-    const size_t lds = (size_t)LP * (96 + 8) * 2 + (size_t)96 * (LP + 8) * 2 + (size_t)LP * 4;
-    static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&xattn_fast_kernel<LT>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
-    (void)attr;
-    hipLaunchKernelGGL((xattn_fast_kernel<LT>), dim3((N + kXaQ - 1) / kXaQ, H, B), dim3(256), lds, s, q, ldq, k, ldk,
-                       vt, ldvt, bias, out, ldo, N, L, H, D, scale);
-    return hipGetLastError();
-}
-
-// Key-split variant of the fast path: 8 waves per workgroup of 128 queries;
-// wave w takes query group w & 3 and key half w >> 2 (tiles [kh*LT/2,
-// (kh+1)*LT/2)).  Each half keeps its own running max m, sum l and O^T
-// partial; the second half hands (m, l, O^T) to the first through LDS, which
-// merges them as l = l0*2^(m0-m) + l1*2^(m1-m) (same for O^T), m = max(m0, m1).
-// Two waves per SIMD let one wave's softmax overlap the other's MFMAs.
-template <int LT>
-__global__ __launch_bounds__(512) void xattn_split_kernel(const f16 * __restrict__ q, int64_t ldq,
-                                                          const f16 * __restrict__ k, int64_t ldk,
-                                                          const f16 * __restrict__ vt, int64_t ldvt,
-                                                          const float * __restrict__ bias, f16 * __restrict__ out,
-                                                          int64_t ldo, int N, int L, int H, int D, float scale) {
+template <int LT, int KS, bool ONES>
+__global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__ q, int64_t ldq,
+                                                        const f16 * __restrict__ k, int64_t ldk,
+                                                        const f16 * __restrict__ vt, int64_t ldvt,
+                                                        const float * __restrict__ bias, f16 * __restrict__ out,
+                                                        int64_t ldo, int N, int L, int D, float scale) {
+    using X = XaCfg<LT, KS>;
     static_assert(LT % 2 == 0, "key tiles split in two halves");
+    static_assert(X::DP <= 128 && X::LP / 8 <= 64, "staging map");
     constexpr int LTH = LT / 2;
-    constexpr int LP = LT * 32;
-    constexpr int KROW = 96 + 8;
-    constexpr int VROW = LP + 8;
-    constexpr int KCH = KROW / 8;
-    constexpr int VCH = VROW / 8;
-    constexpr int KN = (LP * KCH + 511) / 512;
-    constexpr int VN = (96 * VCH + 511) / 512;
+    constexpr int LP = X::LP, KROW = X::KROW, VROW = X::VROW, DT = X::DT, DP = X::DP;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    f16 * Ks = reinterpret_cast<f16 *>(smem);
-    f16 * Vs = Ks + LP * KROW;
-    float * bs = reinterpret_cast<float *>(Vs + 96 * VROW);
-    const int h = blockIdx.y, b = blockIdx.z;
+    f16 * Ks = reinterpret_cast<f16 *>(smem);                          // [LP][KROW]
+    f16 * Vs = reinterpret_cast<f16 *>(smem + X::K_BYTES);             // [DP][VROW], keys permuted
+    float * bs = reinterpret_cast<float *>(smem + X::K_BYTES + X::V_BYTES);  // [LP] log2-scaled bias, -inf past L
+    const int h = blockIdx.x, b = blockIdx.z, H = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = w & 3, kh = w >> 2;
     const int hh = lane >> 5;
-    const int KS = (D + 15) / 16;
-    const int DT = (D + 31) / 32;
-    const int q0 = blockIdx.x * kXaQ + g * 32;
+    const int q0 = blockIdx.y * kXaQ + g * 32;
+    constexpr bool ones_row = ONES;  // D < DP: the last V^T row carries the denominator
 
+    // query fragments (B operand of the score MFMA): query (lane & 31), dims 16 ks + 8 hh ..
     const int qcol = min(q0 + (lane & 31), N - 1);
     const f16 * qr = q + ((int64_t)b * N + qcol) * ldq + (int64_t)h * D;
-    f16x8 qf[6];
+    f16x8 qf[KS];
 #pragma unroll
-    for (int ks = 0; ks < 6; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
         const int d0 = ks * 16 + 8 * hh;
+        const f16x8 v = *reinterpret_cast<const f16x8 *>(qr + (d0 < D ? d0 : 0));
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qf[ks][e] = (f16)0.0f;
-        if (ks < KS && d0 + 8 <= D) qf[ks] = *reinterpret_cast<const f16x8 *>(qr + d0);
+        for (int e = 0; e < 8; ++e) qf[ks][e] = d0 < D ? v[e] : (f16)0.0f;
     }
 
-    const f16 * kb = k + (int64_t)b * L * ldk + (int64_t)h * D;
-    const f16 * vb = vt + ((int64_t)b * H * D + (int64_t)h * D) * ldvt;
-    f16x8 kreg[KN], vreg[VN];
+    // K staging: thread -> chunk kc = tid & 15 (8 dims), rows kr0 + 32 j.  Chunks
+    // past D and rows past L are written as zeros; lanes load only what exists.
+    const int kc = tid & 15, kr0 = tid >> 4;
+    const bool kc_live = kc < KS * 2;  // chunks 0 .. 2 KS - 1 are staged
+    const bool kc_data = kc * 8 < D;
+    const f16 * kp = k + ((int64_t)b * L + kr0) * ldk + (int64_t)h * D + kc * 8;
+    f16x8 kreg[LT];
+    if (kc_data) {
 #pragma unroll
-    for (int j = 0; j < KN; ++j) {
-        const int idx = tid + 512 * j;
-        const int key = idx / KCH, c8 = (idx - key * KCH) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kreg[j][e] = (f16)0.0f;
-        if (idx < LP * KCH && key < L && c8 < D) kreg[j] = *reinterpret_cast<const f16x8 *>(kb + (int64_t)key * ldk + c8);
+        for (int j = 0; j < LT; ++j)
+            if (kr0 + 32 * j < L) kreg[j] = *reinterpret_cast<const f16x8 *>(kp + (int64_t)(32 * j) * ldk);
     }
+    // V^T staging: thread -> 8-key chunk vc = tid & 63, dims vd0 + 8 j (vd0 = the
+    // wave index, so the dim of a step is uniform over the wave)
+    constexpr int VJ = DP / 8;
+    const int vc = tid & 63, vd0 = tid >> 6;
+    const bool vc_live = vc < LP / 8;
+    const int vkeys = min(max(L - vc * 8, 0), 8);  // keys of this chunk below L
+    const f16 * vp = vt + ((int64_t)b * H * D + (int64_t)h * D + vd0) * ldvt + vc * 8;
+    f16x8 vreg[VJ];
+    if (vkeys > 0) {
 #pragma unroll
-    for (int j = 0; j < VN; ++j) {
-        const int idx = tid + 512 * j;
-        const int dim = idx / VCH, c8 = (idx - dim * VCH) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vreg[j][e] = (f16)0.0f;
-        if (idx < 96 * VCH && dim < D && c8 < L) vreg[j] = *reinterpret_cast<const f16x8 *>(vb + (int64_t)dim * ldvt + c8);
-        if (c8 + 8 > L) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (c8 + e >= L) vreg[j][e] = (f16)0.0f;
-        }
+        for (int j = 0; j < VJ; ++j)
+            if (vd0 + 8 * j < D) vreg[j] = *reinterpret_cast<const f16x8 *>(vp + (int64_t)(8 * j) * ldvt);
     }
     for (int key = tid; key < LP; key += 512)
         bs[key] = key < L ? (bias ? bias[(int64_t)b * L + key] * kLog2e : 0.0f) : -INFINITY;
+    const f16x8 zero8 = {(f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f};
+    if (kc_live) {
 #pragma unroll
-    for (int j = 0; j < KN; ++j) {
-        const int idx = tid + 512 * j;
-        if (idx < LP * KCH) *reinterpret_cast<f16x8 *>(Ks + idx * 8) = kreg[j];
+        for (int j = 0; j < LT; ++j) {
+            f16 * dst = Ks + (kr0 + 32 * j) * KROW + kc * 8;
+            if (kc_data && kr0 + 32 * j < L)
+                *reinterpret_cast<f16x8 *>(dst) = kreg[j];
+            else
+                *reinterpret_cast<f16x8 *>(dst) = zero8;
+        }
     }
+    if (vc_live) {
+        // keys 8 vc .. 8 vc + 7: the first four go to positions 16 (vc >> 1) + 4 (vc & 1),
+        // the last four 8 positions further
+        const int pos = 16 * (vc >> 1) + 4 * (vc & 1);
 #pragma unroll
-    for (int j = 0; j < VN; ++j) {
-        const int idx = tid + 512 * j;
-        if (idx < 96 * VCH) *reinterpret_cast<f16x8 *>(Vs + idx * 8) = vreg[j];
+        for (int j = 0; j < VJ; ++j) {
+            const int d = vd0 + 8 * j;
+            f16x8 v = zero8;
+            if (d < D) {
+                if (vkeys == 8) {
+                    v = vreg[j];
+                } else if (vkeys > 0) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = e < vkeys ? vreg[j][e] : (f16)0.0f;
+                }
+            } else if (d == DP - 1 && ones_row) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = e < vkeys ? (f16)1.0f : (f16)0.0f;
+            }
+            f16x4 lo, hi;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                lo[e] = v[e];
+                hi[e] = v[4 + e];
+            }
+            *reinterpret_cast<f16x4 *>(Vs + d * VROW + pos) = lo;
+            *reinterpret_cast<f16x4 *>(Vs + d * VROW + pos + 8) = hi;
+        }
     }
     __syncthreads();
 
@@ -891,8 +745,7 @@ __global__ __launch_bounds__(512) void xattn_split_kernel(const f16 * __restrict
 #pragma unroll
         for (int i = 0; i < 16; ++i) st[t][i] = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < 6; ++ks) {
-        if (ks >= KS) break;
+    for (int ks = 0; ks < KS; ++ks) {
         const int d0 = ks * 16 + 8 * hh;
 #pragma unroll
         for (int t = 0; t < LTH; ++t) {
@@ -917,58 +770,56 @@ __global__ __launch_bounds__(512) void xattn_split_kernel(const f16 * __restrict
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     // a half whose keys are all past L has mx = -inf: its probabilities are exp2(-inf) = 0
     const float mref = mx == -INFINITY ? 0.0f : mx;
-    float sum = 0.0f;
     f16x8 pf[LTH][2];
+    float sum = 0.0f;
 #pragma unroll
     for (int t = 0; t < LTH; ++t)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const float e = __builtin_amdgcn_exp2f(st[t][i] - mref);
-            sum += e;
+            if constexpr (!ones_row) sum += e;
             pf[t][i >> 3][i & 7] = (f16)e;
         }
-    sum += __shfl_xor(sum, 32, 64);
 
-    f32x16 o[3];
+    f32x16 o[DT];
 #pragma unroll
-    for (int dt = 0; dt < 3; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
 #pragma unroll
     for (int t = 0; t < LTH; ++t)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-            const int kbase = (tb + t) * 32 + 16 * s2 + 4 * hh;
+            const int kpos = (tb + t) * 32 + 16 * s2 + 8 * hh;
 #pragma unroll
-            for (int dt = 0; dt < 3; ++dt) {
-                if (dt >= DT) break;
-                const f16 * vrow = Vs + (dt * 32 + (lane & 31)) * VROW;
-                const f16x4 lo4 = *reinterpret_cast<const f16x4 *>(vrow + kbase);
-                const f16x4 hi4 = *reinterpret_cast<const f16x4 *>(vrow + kbase + 8);
-                f16x8 af;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    af[e] = lo4[e];
-                    af[4 + e] = hi4[e];
-                }
+            for (int dt = 0; dt < DT; ++dt) {
+                const f16x8 af = *reinterpret_cast<const f16x8 *>(Vs + (dt * 32 + (lane & 31)) * VROW + kpos);
                 o[dt] = mfma_32x32x16(af, pf[t][s2], o[dt]);
             }
         }
+    // denominator of this half: the last row (31) of the last O^T tile, held by
+    // the upper lane half in register 15 -- or the in-lane sum
+    if constexpr (ones_row) {
+        sum = __shfl(o[DT - 1][15], (lane & 31) + 32, 64);
+    } else {
+        sum += __shfl_xor(sum, 32, 64);
+    }
 
     // merge the two key halves through LDS (the staged K/V are no longer read)
     __syncthreads();
-    float * part = reinterpret_cast<float *>(smem) + g * 50 * 64 + lane;  // [g][50 values][64 lanes]
+    constexpr int NV = DT * 16 + 2;
+    float * part = reinterpret_cast<float *>(smem) + g * NV * 64 + lane;  // [g][NV values][64 lanes]
     if (kh == 1) {
 #pragma unroll
-        for (int dt = 0; dt < 3; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) part[(dt * 16 + i) * 64] = o[dt][i];
-        part[48 * 64] = mx;
-        part[49 * 64] = sum;
+        part[DT * 16 * 64] = mx;
+        part[(DT * 16 + 1) * 64] = sum;
     }
     __syncthreads();
     if (kh == 1) return;
-    const float m1 = part[48 * 64], l1 = part[49 * 64];
+    const float m1 = part[DT * 16 * 64], l1 = part[(DT * 16 + 1) * 64];
     const float m = fmaxf(mx, m1);
     const float a0 = __builtin_amdgcn_exp2f(mx - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
     const float rs = 1.0f / (sum * a0 + l1 * a1);
@@ -978,8 +829,7 @@ __global__ __launch_bounds__(512) void xattn_split_kernel(const f16 * __restrict
     if (qq < N) {
         f16 * orow = out + ((int64_t)b * N + qq) * ldo + (int64_t)h * D;
 #pragma unroll
-        for (int dt = 0; dt < 3; ++dt) {
-            if (dt >= DT) break;
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
                 const int dim = dt * 32 + 8 * i4 + 4 * hh;
@@ -993,24 +843,44 @@ __global__ __launch_bounds__(512) void xattn_split_kernel(const f16 * __restrict
                     *reinterpret_cast<f16x4 *>(orow + dim) = v4;
                 }
             }
-        }
     }
 }
 
+template <int LT, int KS, bool ONES>
+hipError_t launch_xattn_lds1(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
+                             const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D,
+                             float scale, hipStream_t s) {
+    using X = XaCfg<LT, KS>;
+    static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&xattn_lds_kernel<LT, KS, ONES>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, X::LDS_BYTES) ==
+                             hipSuccess;
+    (void)attr;
+    hipLaunchKernelGGL((xattn_lds_kernel<LT, KS, ONES>), dim3(H, (N + kXaQ - 1) / kXaQ, B), dim3(512), X::LDS_BYTES,
+                       s, q, ldq, k, ldk, vt, ldvt, bias, out, ldo, N, L, D, scale);
+    return hipGetLastError();
+}
+
+template <int LT, int KS>
+hipError_t launch_xattn_lds(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
+                            const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D,
+                            float scale, hipStream_t s) {
+    if (D < XaCfg<LT, KS>::DP)
+        return launch_xattn_lds1<LT, KS, true>(q, ldq, k, ldk, vt, ldvt, bias, out, ldo, B, N, L, H, D, scale, s);
+    return launch_xattn_lds1<LT, KS, false>(q, ldq, k, ldk, vt, ldvt, bias, out, ldo, B, N, L, H, D, scale, s);
+}
+
 template <int LT>
-hipError_t launch_xattn_split(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
+hipError_t launch_xattn_lds_d(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
                               const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D,
                               float scale, hipStream_t s) {
-    constexpr int LP = LT * 32;
-    const size_t stage = (size_t)LP * (96 + 8) * 2 + (size_t)96 * (LP + 8) * 2 + (size_t)LP * 4;
-    const size_t merge = (size_t)4 * 50 * 64 * 4;
-    const size_t lds = stage > merge ? stage : merge;
-    static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&xattn_split_kernel<LT>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
-    (void)attr;
-    hipLaunchKernelGGL((xattn_split_kernel<LT>), dim3((N + kXaQ - 1) / kXaQ, H, B), dim3(512), lds, s, q, ldq, k,
-                       ldk, vt, ldvt, bias, out, ldo, N, L, H, D, scale);
-    return hipGetLastError();
+    switch ((D + 15) / 16) {
+        case 1:
+        case 2: return launch_xattn_lds<LT, 2>(q, ldq, k, ldk, vt, ldvt, bias, out, ldo, B, N, L, H, D, scale, s);
+        case 3:
+        case 4: return launch_xattn_lds<LT, 4>(q, ldq, k, ldk, vt, ldvt, bias, out, ldo, B, N, L, H, D, scale, s);
+        case 5: return launch_xattn_lds<LT, 5>(q, ldq, k, ldk, vt, ldvt, bias, out, ldo, B, N, L, H, D, scale, s);
+        default: return launch_xattn_lds<LT, 6>(q, ldq, k, ldk, vt, ldvt, bias, out, ldo, B, N, L, H, D, scale, s);
+    }
 }
 
 template <int LT>
@@ -1122,22 +992,14 @@ hipError_t cross_attention(const half_t * q, int64_t ldq, const half_t * k, int6
     const f16 * kk = reinterpret_cast<const f16 *>(k);
     const f16 * vv = reinterpret_cast<const f16 *>(vt);
     f16 * oo = reinterpret_cast<f16 *>(out);
-    // fast path: LDS-staged head, transposed scores (ldvt >= the 32-padded key count)
+    // LDS-staged head, transposed scores (ldvt >= the 32-padded key count)
     const int lt32 = (L + 31) / 32;
     const bool out_vec = ldo % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;  // 8-byte output stores
     if (vec && out_vec && D <= 96 && lt32 <= 10 && ldvt >= (int64_t)lt32 * 32) {
-        // key-split kernel by default (1024 queries x 300 keys x 16 heads of 72: 12.8 us
-        // against 17.3 us for one wave per query group); SANA_XATTN_SPLIT=0 selects the
-        // latter (read at every launch, so a process can compare both)
-        const char * split_env = std::getenv("SANA_XATTN_SPLIT");
-        if (!split_env || std::atoi(split_env) != 0) {
-            if (lt32 <= 2) return launch_xattn_split<2>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
-            if (lt32 <= 4) return launch_xattn_split<4>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
-            return launch_xattn_split<10>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
-        }
-        if (lt32 <= 2) return launch_xattn_fast<2>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
-        if (lt32 <= 4) return launch_xattn_fast<4>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
-        return launch_xattn_fast<10>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
+        if (lt32 <= 2) return launch_xattn_lds_d<2>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
+        if (lt32 <= 4) return launch_xattn_lds_d<4>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
+        if (lt32 <= 6) return launch_xattn_lds_d<6>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
+        return launch_xattn_lds_d<10>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, s);
     }
     const int lt = (L + 15) / 16;
     if (lt <= 2) return launch_xattn<2>(qq, ldq, kk, ldk, vv, ldvt, bias, oo, ldo, B, N, L, H, D, scale, vec, s);

@@ -90,6 +90,9 @@ struct sana_dit {
     // its fork / join events; same (default) priority as `stream`
     hipStream_t stream2 = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    // recorded on the stream of the last denoise loop after its last step, so
+    // sana_dit_loop_model_outputs reads loop_x0 only once the loop has written it
+    hipEvent_t ev_loop = nullptr;
     std::vector<std::unique_ptr<BlockDev>> blocks;
     DevMem w_k_all, b_k_all, w_v_all, b_v_all, sst_all;  // stacked over blocks
     DevMem w_cap1, b_cap1, w_cap2, b_cap2, cap_norm;
@@ -111,12 +114,17 @@ struct sana_dit {
         graphs;
     int64_t last_M = 0, last_B = 0, last_N = 0;
     int64_t loop_steps = 0, loop_n = 0;  // shape of the last denoise loop (its converted outputs stay in loop_x0)
+    // Execution switches, read from the environment once by sana_dit_create:
+    // SANA_DIT_CFG_BRANCHES=0 runs the CFG pair as one chain, SANA_DIT_NO_GRAPH=1
+    // launches the forward's kernels directly instead of replaying a graph.
+    bool cfg_branches = true, use_graphs = true;
 
     ~sana_dit() {
         for (auto & kv : graphs)
             if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
         if (ev_fork) (void)hipEventDestroy(ev_fork);
         if (ev_join) (void)hipEventDestroy(ev_join);
+        if (ev_loop) (void)hipEventDestroy(ev_loop);
         if (stream2) (void)hipStreamDestroy(stream2);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -428,14 +436,6 @@ void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * 
     if (hook) hook(hook_ctx, 2);
 }
 
-// Whether a forward over the CFG pair runs its two batch rows as two
-// concurrent chains (graph branches): each kernel then covers half the rows,
-// and the two chains fill each other's launch gaps and tails and share the
-// weights through the caches.
-bool cfg_branches_enabled() {
-    const char * e = std::getenv("SANA_DIT_CFG_BRANCHES");
-    return !(e && e[0] == '0');
-}
 
 void enqueue_forward(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh, int64_t Ww, const float * xbias,
                      float * out, hipStream_t s) {
@@ -444,7 +444,10 @@ void enqueue_forward(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh,
                                    c->b_patch.as<float>(), c->x32.as<float>(), (int)c->C, s),
                  "patch_embed");
     enqueue_time(c, B, s);
-    if (B == 2 && cfg_branches_enabled()) {
+    // The CFG pair runs its two batch rows as two concurrent chains (graph
+    // branches): each kernel then covers half the rows, and the two chains fill
+    // each other's launch gaps and tails and share the weights through the caches.
+    if (B == 2 && c->cfg_branches) {
         // batch row 0 on s, row 1 on stream2, forked after the time embedding
         // and joined before the final layer
         hip_check(hipEventRecord(c->ev_fork, s), "hipEventRecord");
@@ -514,10 +517,6 @@ void set_t(sana_dit * c, int64_t B, float t, hipStream_t s) {
     hip_check(hipGetLastError(), "fill");
 }
 
-bool graphs_enabled() {
-    const char * e = std::getenv("SANA_DIT_NO_GRAPH");
-    return !(e && e[0] == '1');
-}
 
 // Run `body` on stream s through a cached HIP graph (captured on the context
 // stream on first use for this key).
@@ -526,7 +525,7 @@ void run_graph(sana_dit * c,
                const std::tuple<int, int64_t, int64_t, int64_t, int64_t, const void *, const void *, const void *,
                                 const void *> & key,
                hipStream_t s, Body body) {
-    if (!graphs_enabled()) {
+    if (!c->use_graphs) {
         body(s);
         return;
     }
@@ -592,11 +591,16 @@ int sana_dit_create(const sana_dit_config * cfg, sana_dit ** out) {
         c->Cp = round_up(c->C, 64);
         c->Fp = round_up(c->F, 64);
         c->Ccap_p = round_up(c->Ccap, 64);
+        const char * eb = std::getenv("SANA_DIT_CFG_BRANCHES");
+        c->cfg_branches = !(eb && eb[0] == '0');
+        const char * eg = std::getenv("SANA_DIT_NO_GRAPH");
+        c->use_graphs = !(eg && eg[0] == '1');
         hip_check(hipSetDevice(cfg->device), "hipSetDevice");
         hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
         hip_check(hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking), "hipStreamCreate");
         hip_check(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "hipEventCreate");
         hip_check(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "hipEventCreate");
+        hip_check(hipEventCreateWithFlags(&c->ev_loop, hipEventDisableTiming), "hipEventCreate");
         for (int64_t i = 0; i < c->L_; ++i) c->blocks.emplace_back(new BlockDev());
         // sinusoid frequencies exactly as the reference computes them in fp32
         // (src/transformer.cpp:89,97-99)
@@ -997,6 +1001,7 @@ float * enqueue_loop(sana_dit * c, const float * d_latent, int64_t Bl, int64_t H
                            guidance, s0_v, ca, cb, cc, inv_r0, first ? 0 : 1);
         hip_check(hipGetLastError(), "cfg_dpm");
     }
+    hip_check(hipEventRecord(c->ev_loop, s), "hipEventRecord");
     c->loop_steps = steps;
     c->loop_n = n;
     return c->loop_lat[steps & 1].as<float>();
@@ -1054,6 +1059,8 @@ int sana_dit_loop_model_outputs(sana_dit * c, float * x0_prev, float * x0_last) 
     return guarded([&] {
         const int64_t st = c->loop_steps;
         const size_t bytes = (size_t)c->loop_n * 4;
+        // the loop may have been queued on a caller's stream
+        hip_check(hipStreamWaitEvent(c->stream, c->ev_loop, 0), "hipStreamWaitEvent");
         // step i writes its converted output to loop_x0[i & 1] (cfg_dpm_kernel's x0_out)
         hip_check(hipMemcpyAsync(x0_last, c->loop_x0[(st - 1) & 1].p, bytes, hipMemcpyDeviceToHost, c->stream),
                   "x0");

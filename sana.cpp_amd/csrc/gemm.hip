@@ -35,8 +35,6 @@
 //   residual: x += gate * (acc + bias), optional fp16 copy of the new x
 //             (mul_inplace_broadcast_lastdim + add_inplace, src/tensor.cpp:101-160)
 //   V^T     : transposed per-batch store of the cross-attention values.
-#include <cstdlib>
-
 #include "hip_common.h"
 #include "kernels.h"
 
@@ -648,42 +646,6 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     if (p.conv) {
         if (p.N <= 64) return launch_conv<128, 64, 2, 2, 2, 3>(p, s);
         return launch_conv<128, 128, 2, 2, 2, 1>(p, s);
-    }
-    static const int forced = [] {
-        const char * e = std::getenv("SANA_GEMM_VARIANT");
-        return e ? std::atoi(e) : -1;
-    }();
-    switch (forced) {
-        case 0: return launch<128, 128, 2, 2, 2, 0>(p, s);
-        case 1: return launch<128, 128, 2, 2, 2, 1>(p, s);
-        case 2: return launch<128, 128, 2, 2, 2, 2>(p, s);
-        case 3: return launch<128, 128, 2, 2, 3, 0>(p, s);
-        case 4: return launch<128, 128, 2, 2, 3, 1>(p, s);
-        case 5: return launch<128, 128, 2, 2, 3, 2>(p, s);
-        case 6: return launch<128, 64, 2, 2, 2, 0>(p, s);
-        case 7: return launch<128, 64, 2, 2, 2, 1>(p, s);
-        case 8: return launch<128, 64, 2, 2, 3, 1>(p, s);
-        case 9: return launch<64, 64, 2, 2, 2, 0>(p, s);
-        case 10: return launch<64, 64, 2, 2, 2, 1>(p, s);
-        case 11: return launch<64, 64, 2, 2, 4, 1>(p, s);
-        case 12: return launch<256, 128, 2, 2, 3, 1>(p, s);
-        case 13: return launch<256, 128, 2, 2, 3, 2>(p, s);
-        case 14: return launch<128, 256, 2, 2, 3, 1>(p, s);
-        case 15: return launch<128, 128, 2, 2, 4, 1>(p, s);
-        case 16: return launch<128, 128, 2, 2, 4, 2>(p, s);
-        case 17: return launch<128, 64, 2, 2, 4, 1>(p, s);
-        case 18: return launch<128, 128, 2, 4, 2, 1>(p, s);
-        case 19: return launch<128, 128, 4, 2, 2, 1>(p, s);
-        case 22: return launch<256, 128, 4, 2, 2, 1>(p, s);
-        case 23: return launch<128, 256, 2, 4, 2, 1>(p, s);
-        case 24: return launch<128, 128, 2, 4, 2, 0>(p, s);
-        case 25: return launch<64, 64, 2, 2, 3, 1>(p, s);
-        case 26: return launch<128, 192, 2, 2, 2, 3>(p, s);
-        case 27: return launch<128, 64, 2, 2, 2, 3>(p, s);
-        case 28: return launch<64, 64, 2, 2, 2, 3>(p, s);
-        case 29: return launch<128, 128, 2, 2, 2, 3>(p, s);
-        case 30: return launch<64, 64, 2, 2, 3, 3>(p, s);
-        default: break;
     }
     // Tile choice from sweeps on MI355X with cold weights (each GEMM's weights
     // come from HBM, as in the 28-block forward).  Every CU pulls at most

@@ -168,3 +168,58 @@ def test_small_forward_masked_vs_oracle(small_model):
     d.set_context(caption, projected=False, bias=bias)
     got = d.forward(latent, 733.0)
     assert rel_l2(got, ref) < TOL_FORWARD
+
+
+def test_small_forward_batch2_vs_oracle(small_model):
+    """A latent batch of 2 (context batch 4): the single-chain forward, patch
+    embed reading latent row b % 2, uncond rows first."""
+    m, d = small_model
+    latent = O.randn((2, 8, 8, 8), 11)
+    caption = O.randn((4, 16, 96), 12)
+    ctx = m.project_caption(caption)
+    ref = m.forward(latent, ctx, 610.0)
+    d.set_context(caption, projected=False)
+    got = d.forward(latent, 610.0)
+    err = rel_l2(got, ref)
+    print(f"small forward, latent batch 2: rel_l2 {err:.2e}")
+    assert err < TOL_FORWARD
+
+
+def test_small_loop_batch2_vs_oracle(small_model):
+    """The fused device loop on a latent batch of 2: CFG combines rows b and
+    b + 2 of the noise prediction."""
+    m, d = small_model
+    latent = O.randn((2, 8, 8, 8), 13)
+    caption = O.randn((4, 16, 96), 14)
+    ref = m.loop(latent, caption, 5, 4.5)
+    d.set_context(caption, projected=False)
+    ts, sg = O.scheduler_timesteps(5)
+    got = d.denoise_loop(latent, ts, sg, 4.5)
+    err = rel_l2(got, ref)
+    print(f"small loop, latent batch 2: rel_l2 {err:.2e}")
+    assert err < TOL_LOOP
+
+
+def test_small_forward_one_chain_no_graph_vs_oracle(monkeypatch):
+    """SANA_DIT_CFG_BRANCHES=0 (the CFG pair as one chain) and
+    SANA_DIT_NO_GRAPH=1 (direct launches), both read at context creation."""
+    import sana_dit
+    monkeypatch.setenv("SANA_DIT_CFG_BRANCHES", "0")
+    monkeypatch.setenv("SANA_DIT_NO_GRAPH", "1")
+    m = O.Model(**SMALL)
+    d = sana_dit.Dit(layers=2, hidden=128, ffn=256, caption_dim=96, latent_channels=8, self_heads=4, cross_heads=2)
+    try:
+        for name, shape in sana_dit.manifest(2, 128, 256, 96, 8).items():
+            d.set_weight(name, m.get(name, shape))
+        latent = O.randn((1, 8, 8, 8), 15)
+        caption = O.randn((2, 16, 96), 16)
+        ref = m.forward(latent, m.project_caption(caption), 999.0)
+        d.set_context(caption, projected=False)
+        got = d.forward(latent, 999.0)
+        again = d.forward(latent, 999.0)
+        err = rel_l2(got, ref)
+        print(f"small forward, one chain, no graph: rel_l2 {err:.2e}")
+        assert err < TOL_FORWARD
+        assert np.array_equal(got, again)
+    finally:
+        d.close()

@@ -218,15 +218,16 @@ def _xattn(L, q, k, v, H, bias):
 
 
 @pytest.mark.parametrize("B,N,Lk,H,D,masked", [(2, 1024, 300, 16, 72, False), (2, 256, 300, 16, 72, True),
-                                               (1, 70, 33, 4, 32, False), (1, 2, 2, 1, 2, False),
-                                               (1, 17, 5, 3, 12, True), (1, 130, 150, 2, 64, True),
-                                               (2, 200, 100, 4, 72, False)])
-@pytest.mark.parametrize("variant", ["split", "single"])
-def test_cross_attention(L, B, N, Lk, H, D, masked, variant, monkeypatch):
-    # "split": 8 waves per 128 queries, one key half each (the default);
-    # "single": one wave per 32 queries over all keys (SANA_XATTN_SPLIT=0)
-    if variant == "single":
-        monkeypatch.setenv("SANA_XATTN_SPLIT", "0")
+                                               (2, 129, 300, 16, 72, True), (1, 64, 320, 2, 96, False),
+                                               (1, 100, 161, 3, 48, True), (1, 70, 33, 4, 32, False),
+                                               (1, 2, 2, 1, 2, False), (1, 17, 5, 3, 12, True),
+                                               (1, 130, 150, 2, 64, True), (2, 200, 100, 4, 72, False),
+                                               (1, 40, 5, 2, 72, False)])
+def test_cross_attention(L, B, N, Lk, H, D, masked):
+    # D % 8 == 0 with <= 320 keys runs the LDS-staged kernel: D = 72 and 48
+    # take the softmax denominator from the ones row of V^T, D = 32, 64 and 96
+    # (multiples of 32, no padding row) sum it in registers; 5 and 33 keys
+    # leave the second key half (nearly) empty.  D = 2 and 12 run the generic kernel.
     rng = np.random.default_rng(N + Lk)
     C = H * D
     q = f16(rng.standard_normal((B, N, C)))
@@ -243,11 +244,11 @@ def test_cross_attention(L, B, N, Lk, H, D, masked, variant, monkeypatch):
     assert rel_l2(got, ref) < 2e-3, rel_l2(got, ref)
 
 
-@pytest.mark.parametrize("B,S,F", [(2, 32, 2880), (2, 64, 2880), (1, 37, 40), (1, 16, 64), (1, 3, 5), (2, 1, 8)])
-@pytest.mark.parametrize("xs", ["4", "2", "8", "16"])
-def test_dwconv_glu(L, B, S, F, xs, monkeypatch):
-    # xs: tokens per row segment of a thread (SANA_DWGLU_XS; 4 is the default)
-    monkeypatch.setenv("SANA_DWGLU_XS", xs)
+@pytest.mark.parametrize("B,S,F", [(2, 32, 2880), (2, 64, 2880), (1, 37, 40), (1, 16, 64), (1, 3, 5), (2, 1, 8),
+                                   (1, 6, 16), (1, 7, 24)])
+def test_dwconv_glu(L, B, S, F):
+    # 4-token row segments: S = 6 and 7 leave a partial last segment, S = 1 and 3
+    # a row shorter than a segment; F = 5 takes the scalar kernel
     rng = np.random.default_rng(S + F)
     E = 2 * F
     x = f16(rng.standard_normal((B, S, S, E)))
