@@ -76,8 +76,10 @@ int sana_dit_set_block_norm(sana_dit * ctx, int64_t block, int which, const floa
 /* Checks that every tensor has been uploaded (validate_denoiser_weights,
  * src/transformer.cpp:807-884 checks the shapes; set_* already did). */
 int sana_dit_check_weights(sana_dit * ctx);
-/* Loads the three GGUF files of download_weights.sh (model, caption, denoiser),
- * F32 tensors only (src/weights_io.cpp:134-164, :325-365). */
+/* Loads the three GGUF files of download_weights.sh (model, caption, denoiser)
+ * (src/weights_io.cpp:134-164, :325-365).  Payloads may be F32, F16 or BF16;
+ * 16-bit payloads are widened exactly to fp32 before the upload (the reference
+ * reads every payload as F32).  Other ggml types fail with SANA_ERR_FORMAT. */
 int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * caption_path,
                        const char * denoiser_path);
 

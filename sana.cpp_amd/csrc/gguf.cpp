@@ -211,5 +211,46 @@ std::vector<std::string> block_prefixes(const std::vector<std::string> & names) 
     return v;
 }
 
+// IEEE binary16 -> binary32, exact (written out so the host compiler needs no
+// half type).
+static float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const uint32_t ex = (h >> 10) & 31, man = h & 1023;
+    uint32_t u;
+    if (ex == 0) {
+        // zero or subnormal: man * 2^-24 (exact in fp32)
+        float v = (float)man * 5.9604644775390625e-08f;
+        std::memcpy(&u, &v, 4);
+        u |= sign;
+    } else if (ex == 31) {
+        u = sign | 0x7f800000u | (man << 13);  // inf / nan
+    } else {
+        u = sign | ((ex + 112) << 23) | (man << 13);
+    }
+    float out;
+    std::memcpy(&out, &u, 4);
+    return out;
+}
+
+const float * payload_f32(const MappedFile & f, const TensorInfo & t, std::vector<float> & tmp) {
+    if (t.offset + t.nbytes > f.size() || (t.nbytes == 0 && t.type != kF32))
+        throw std::runtime_error("unsupported or truncated gguf tensor: " + t.name);
+    if (t.type == kF32) return reinterpret_cast<const float *>(f.data() + t.offset);
+    const size_t n = t.nbytes / 2;
+    tmp.resize(n);
+    const unsigned char * p = f.data() + t.offset;
+    for (size_t i = 0; i < n; ++i) {
+        uint16_t h;
+        std::memcpy(&h, p + 2 * i, 2);
+        if (t.type == kF16) {
+            tmp[i] = half_to_float(h);
+        } else {
+            const uint32_t u = (uint32_t)h << 16;  // bf16 is the top half of an fp32
+            std::memcpy(&tmp[i], &u, 4);
+        }
+    }
+    return tmp.data();
+}
+
 }  // namespace gguf
 }  // namespace sana

@@ -68,6 +68,11 @@ private:
     uint64_t size_ = 0;
 };
 
+// The payload of tensor t as fp32: F32 is returned in place (pointer into the
+// mapping); F16 and BF16 are widened into `tmp` (exactly: both are subsets of
+// fp32).  Throws std::runtime_error naming the tensor for any other type.
+const float * payload_f32(const MappedFile & f, const TensorInfo & t, std::vector<float> & tmp);
+
 // Block prefixes as find_block_prefixes (src/transformer.cpp:401-426): the
 // names ending in ".scale_shift_table", minus that suffix, ordered by trailing
 // integer when two prefixes share a stem, else lexicographically.

@@ -43,10 +43,19 @@ struct Err {
     std::string msg;
 };
 
-const float * payload(const sana::gguf::MappedFile & f, const sana::gguf::TensorInfo & t) {
-    if (t.type != sana::gguf::kF32)
-        throw Err{SANA_ERR_FORMAT, "only float32 gguf tensors are supported: " + t.name};
-    return reinterpret_cast<const float *>(f.data() + t.offset);
+// F32 payloads are read in place; F16 and BF16 are widened to fp32 first (the
+// reference reads every payload as raw F32 whatever its ggml type,
+// src/weights_io.cpp:155, :340-355, which misreads 16-bit files).  Other types
+// are refused.
+const float * payload(const sana::gguf::MappedFile & f, const sana::gguf::TensorInfo & t, std::vector<float> & tmp) {
+    using namespace sana::gguf;
+    if (t.type != kF32 && t.type != kF16 && t.type != kBF16)
+        throw Err{SANA_ERR_FORMAT, "gguf tensor type must be F32, F16 or BF16: " + t.name};
+    try {
+        return payload_f32(f, t, tmp);
+    } catch (const std::runtime_error & e) {
+        throw Err{SANA_ERR_FORMAT, e.what()};
+    }
 }
 
 const sana::gguf::TensorInfo & find(const sana::gguf::Index & idx, const std::string & n) {
@@ -105,12 +114,13 @@ int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * cap
             std::vector<std::string> names;
             for (const auto & t : idx.tensors) names.push_back(t.name);
             const std::vector<std::string> pre = block_prefixes(names);
+            std::vector<float> tmp;
             if (pre.empty()) throw Err{SANA_ERR_INVALID_ARGUMENT, "weight index does not contain any prefixed model blocks"};
             for (size_t b = 0; b < pre.size(); ++b) {
                 for (const char * s : kBlockSuffixes) {
                     const std::string full = pre[b].empty() ? std::string(s) : pre[b] + "." + s;
                     const TensorInfo & t = find(idx, full);
-                    int rc = sana_dit_set_block_weight(ctx, (int64_t)b, s, payload(f, t), t.shape.data(),
+                    int rc = sana_dit_set_block_weight(ctx, (int64_t)b, s, payload(f, t, tmp), t.shape.data(),
                                                        (int)t.shape.size(), 0);
                     if (rc == SANA_ERR_INVALID_ARGUMENT && b > 0)
                         throw Err{SANA_ERR_SHAPE, "gguf holds more blocks than the model's layer count"};
@@ -122,12 +132,13 @@ int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * cap
             const char * path = which == 0 ? caption_path : denoiser_path;
             const Index idx = read_index(path);
             MappedFile f(path);
+            std::vector<float> tmp;
             const size_t n = which == 0 ? sizeof(kCaptionNames) / sizeof(kCaptionNames[0])
                                         : sizeof(kDenoiserNames) / sizeof(kDenoiserNames[0]);
             for (size_t i = 0; i < n; ++i) {
                 const char * name = which == 0 ? kCaptionNames[i] : kDenoiserNames[i];
                 const TensorInfo & t = find(idx, name);
-                call(sana_dit_set_weight(ctx, name, payload(f, t), t.shape.data(), (int)t.shape.size(), 0));
+                call(sana_dit_set_weight(ctx, name, payload(f, t, tmp), t.shape.data(), (int)t.shape.size(), 0));
             }
         }
         call(sana_dit_check_weights(ctx));

@@ -749,26 +749,14 @@ void validate_config(const sana_vae_config * c) {
 const float * gguf_payload(const sana::gguf::MappedFile & f, const sana::gguf::TensorInfo & t,
                            std::vector<float> & tmp) {
     using namespace sana::gguf;
-    if (t.type == kF32) return reinterpret_cast<const float *>(f.data() + t.offset);
-    size_t n = 1;
-    for (int64_t d : t.shape) n *= (size_t)d;
-    tmp.resize(n);
-    const uint16_t * h = reinterpret_cast<const uint16_t *>(f.data() + t.offset);
-    if (t.type == kF16) {
-        for (size_t i = 0; i < n; ++i) {
-            _Float16 x;
-            std::memcpy(&x, h + i, 2);
-            tmp[i] = (float)x;
-        }
-    } else if (t.type == kBF16) {
-        for (size_t i = 0; i < n; ++i) {
-            const uint32_t u = (uint32_t)h[i] << 16;
-            std::memcpy(&tmp[i], &u, 4);
-        }
-    } else {
+    if (t.type != kF32 && t.type != kF16 && t.type != kBF16)
         throw_err(SANA_ERR_FORMAT, "unsupported gguf tensor type for " + t.name);
+    try {
+        return payload_f32(f, t, tmp);
+    } catch (const std::runtime_error & e) {
+        throw_err(SANA_ERR_FORMAT, e.what());
     }
-    return tmp.data();
+    return nullptr;
 }
 
 }  // namespace

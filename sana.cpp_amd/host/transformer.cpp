@@ -549,6 +549,18 @@ SanaBlockModulation compute_sana_block_modulation(const Tensor & timestep, const
             std::get<3>(parts), std::get<4>(parts), std::get<5>(parts)};
 }
 
+namespace {
+void drop_device_models(const void * key) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    for (auto it = g_models.begin(); it != g_models.end();)
+        it = (!key || it->first.second == key) ? g_models.erase(it) : std::next(it);
+}
+}  // namespace
+
+void invalidate_device_weights(const SanaDenoiserWeights & weights) { drop_device_models(&weights); }
+void invalidate_device_weights(const SanaBlockWeights & weights) { drop_device_models(&weights); }
+void invalidate_all_device_weights() { drop_device_models(nullptr); }
+
 SanaBlockStageOutputs block_forward(const Tensor & input, const Tensor & context, const Tensor & timestep,
                                     const SanaBlockWeights & weights, const Tensor * bias) {
     if (timestep.rank() != 2) throw std::invalid_argument("timestep must be rank 2");

@@ -123,3 +123,17 @@ Tensor run_full_denoising_loop_with_cfg(const Tensor & initial_latents, const Te
                                         const Tensor * encoder_attention_bias = nullptr);
 SanaBlockStageOutputs block_forward(const Tensor & input, const Tensor & context, const Tensor & timestep,
                                     const SanaBlockWeights & weights, const Tensor * encoder_attention_bias = nullptr);
+
+// Device residency of the drop-in (no counterpart in the reference, which
+// reads the host weights on every call).  The first call with a weights
+// object uploads it to the GPU; later calls reuse that copy while the object
+// has the same address and fingerprint (every tensor's storage address and
+// shape, and its values: all of them up to 4096, else 65 spread samples).  A
+// reallocated or refilled object is therefore uploaded again, but an in-place
+// edit of values that misses the samples (same storage, e.g. merging a LoRA
+// delta into a weight) is not seen: call invalidate_device_weights on the
+// object after such an edit, and the next call uploads it again.
+void invalidate_device_weights(const SanaDenoiserWeights & weights);
+void invalidate_device_weights(const SanaBlockWeights & weights);
+// Drops every device copy the drop-in holds (denoisers and blocks).
+void invalidate_all_device_weights();

@@ -357,6 +357,13 @@ Tensor run_vae_decoder_input(const Tensor & latents, const SanaVaeDecoderWeights
     return out;
 }
 
+void invalidate_device_weights(const SanaVaeDecoderWeights & weights) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    g_vaes.erase(&weights);
+}
+
+void invalidate_device_weights(const SanaVaeWeights & weights) { invalidate_device_weights(weights.decoder); }
+
 Tensor run_vae_decode(const Tensor & latents, const SanaVaeWeights & weights) {
     validate_vae_weights(weights);
     if (latents.rank() != 4) throw std::invalid_argument("vae decode latents must be rank 4");

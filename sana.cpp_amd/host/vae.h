@@ -84,3 +84,11 @@ void validate_vae_weights(const SanaVaeWeights & weights);
 Tensor run_vae_decoder_input(const Tensor & latents, const SanaVaeDecoderWeights & weights, bool in_shortcut = true);
 // latents [B, Cl, H, W] -> image [B, 3, H * 2^(blocks-1), W * 2^(blocks-1)].
 Tensor run_vae_decode(const Tensor & latents, const SanaVaeWeights & weights);
+
+// Device residency of the drop-in (no counterpart in the reference): a
+// decoder's weights are uploaded on first use and reused while its address and
+// fingerprint (tensor storage addresses, shapes, all values up to 4096 else 65
+// spread samples) are unchanged.  After an in-place edit of tensor values,
+// call invalidate_device_weights so the next decode uploads them again.
+void invalidate_device_weights(const SanaVaeWeights & weights);
+void invalidate_device_weights(const SanaVaeDecoderWeights & weights);

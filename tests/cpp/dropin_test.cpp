@@ -508,6 +508,28 @@ void gpu_small_model_tests() {
     Tensor mid = run_full_denoising_step_with_cfg(latent, ctx, 4.5f, s_mid, cfg, w, &bias);
     mid = run_full_denoising_loop_with_cfg(mid, caption, 4.5f, s_mid, cfg, w, &bias);
     close_l2(mid.data(), ref, 1e-2, "loop resumed after one step");
+
+    // In-place edits and invalidate_device_weights.  Element 1 of the FFN
+    // inverted weight (256 x 128 values, sampled every 512th) is outside the
+    // fingerprint's samples: the resident copy is reused until the object is
+    // invalidated, then the edit is uploaded and matches a fresh object.
+    SanaDenoiserWeights we = sm.weights();
+    const Tensor r0 = run_model_blocks(x, ctx, tmod, we, 0, 2);
+    const SanaBlockStageOutputs b0 = block_forward(x, ctx, tmod, we.blocks[1]);
+    we.blocks[1].ff_inverted_weight.data()[1] += 4.0f;
+    check(run_model_blocks(x, ctx, tmod, we, 0, 2).data() == r0.data(), "unsampled in-place edit: resident copy used");
+    invalidate_device_weights(we);
+    const Tensor r1 = run_model_blocks(x, ctx, tmod, we, 0, 2);
+    check(r1.data() != r0.data(), "after invalidate_device_weights the edit is uploaded");
+    const SanaDenoiserWeights fresh = we;  // the edited values at new storage addresses
+    check(run_model_blocks(x, ctx, tmod, fresh, 0, 2).data() == r1.data(), "invalidated object == fresh upload");
+    check(block_forward(x, ctx, tmod, we.blocks[1]).after_ff.data() == b0.after_ff.data(),
+          "block-level copy still resident");
+    invalidate_device_weights(we.blocks[1]);
+    check(block_forward(x, ctx, tmod, we.blocks[1]).after_ff.data() != b0.after_ff.data(),
+          "block-level invalidate uploads the edit");
+    invalidate_all_device_weights();
+    check(run_model_blocks(x, ctx, tmod, we, 0, 2).data() == r1.data(), "re-upload after invalidate_all");
 }
 
 // ---------------------------------------------------------------- op-level API

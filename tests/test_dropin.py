@@ -211,6 +211,34 @@ def test_load_gguf_abi_forward(tmp_path):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("ggml_type", [GGML_F16, GGML_BF16])
+def test_load_gguf_abi_16bit_forward(tmp_path, ggml_type):
+    """sana_dit_load_gguf on F16 and BF16 payloads: the forward matches the
+    oracle run on the same weights rounded to that format."""
+    path = str(tmp_path / "small16.gguf")
+    m, names = small_gguf(path, ggml_type)
+    for n, shape in names.items():
+        w = m.get(n, shape)
+        if ggml_type == GGML_F16:
+            r = w.astype(np.float16).astype(np.float32)
+        else:
+            r = ((w.view(np.uint32) >> 16) << 16).view(np.float32)  # the writer truncates to bf16
+        m.set(n, r)
+    d = sana_dit.Dit(layers=2, hidden=128, ffn=256, caption_dim=96, latent_channels=8, self_heads=4, cross_heads=2)
+    try:
+        d.load_gguf(path, path, path)
+        latent = O.randn((1, 8, 8, 8), 42)
+        caption = O.randn((2, 16, 96), 43)
+        ref = m.forward(latent, m.project_caption(caption), 999.0)
+        d.set_context(caption, projected=False)
+        err = rel_l2(d.forward(latent, 999.0), ref)
+        print(f"gguf type {ggml_type}: forward rel_l2 {err:.2e}")
+        assert err < 2e-3
+    finally:
+        d.close()
+
+
+@pytest.mark.gpu
 def test_dropin_full_loop_1024px_vs_reference(tmp_path):
     path = os.path.join(GOLDEN, "cfg3.npz")
     if not os.path.exists(path):
