@@ -14,23 +14,38 @@ the context kept resident (sana_dit_forward_device) is reported beside it.
 
 Prints ONE JSON line (rank 0, N = 1 only):
   value / ms_per_step      ms per step (lower is better)
-  roofline                 the dominant kernel (Mix-FFN inverted 1x1 GEMM,
-                           2048 x 5760 x 1152) timed with HIP events on the
-                           stream it is launched on, against the dense fp16
-                           MFMA peak; `traffic` is its HBM bytes per launch
-                           from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-                           summarised in profiles/ (null when absent)
-  cpu_baseline             the reference's own CPU block_forward (compiled
-                           from source into oracle/_ref, 1 thread) on one
-                           block of the same workload, median of 6, x28
-  peaks_measured           the dense fp16 MFMA rate of independent MFMA chains
-                           (sana_hip_mfma_peak) and the HBM rate of a 1 GiB
-                           device copy, on this GPU
+  kernels                  every kernel class of a block, timed with HIP events
+                           on the stream it runs on, launched exactly as the
+                           forward launches it (sana_dit_time_kernel: same
+                           instantiation and per-CFG-branch shape, weights
+                           cycled over the 28 blocks), with its algorithmic
+                           flops / bytes, the bound, the achieved rate against
+                           the MI355X peak and the HBM bytes per launch from the
+                           rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/
+  roofline                 the forward's dominant kernel (largest total time
+                           per forward; roles that share one kernel
+                           instantiation are one kernel, as in a trace)
+  cpu_baseline             the reference's own CPU code (compiled from source
+                           into oracle/_ref, 1 thread): one full CFG step at
+                           this workload (caption projection + 28-block
+                           forward); beside it the single-block configuration
+                           (B=1, 256 tokens, 16x72 heads, median of 3) and the
+                           4096-token linear attention + Mix-FFN
+                           microbenchmark (median of 3)
+  peaks_measured           the dense fp16 MFMA rate of independent MFMA
+                           accumulators (sana_hip_mfma_peak, one workgroup per
+                           CU) and the HBM rate of 4 GiB streaming reads and
+                           copies (sana_hip_hbm_peak), on this GPU
   forward_roofline         lower bound of the step, sum over kernels of
                            max(flops / MFMA peak, bytes / HBM peak), with the
-                           spec and the measured peaks, and the measured step
-                           as a fraction of it
+                           spec (headline) and the measured peaks, and the
+                           measured step as a fraction of it
 
+  forward_4096px           the same forward at latent 128x128 (16384 tokens,
+                           CFG batch 2), context resident
+  kernels_4096px           the kernel table at 16384 tokens per branch, where
+                           the working sets exceed the 256 MB last-level cache
+  microbench_4096_tokens   linear attention and Mix-FFN at 4096 tokens
   vae_decode_1024px        the DC-AE decode of one 32x32x32 latent to a
                            1024x1024 image (the stage after the denoising
                            loop), ms and TFLOP/s
@@ -57,10 +72,9 @@ sys.path.insert(0, os.path.join(ROOT, "sana.cpp_amd"))
 PEAK_MFMA_TFLOPS = 2516.6   # MI355X dense fp16/bf16
 PEAK_HBM_GBS = 8000.0
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ffn_inverted_gemm_1024px_hbm_traffic.md")
-CPU_REPS = 6
-# operands and output of the Mix-FFN inverted GEMM, fp16: A 2048x1152, W 5760x1152, out 2048x5760, bias fp32
-GEMM_BYTES = 2 * (2048 * 1152 + 5760 * 1152 + 2048 * 5760) + 4 * 5760
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dit_kernels_1024px_hbm_traffic.md")
+TRAFFIC_FILE_4096 = os.path.join(ROOT, "profiles", "dit_kernels_4096px_hbm_traffic.md")
+CPU_REPS = 3
 
 DIMS = dict(layers=28, hidden=1152, ffn=5760, caption_dim=2304, latent_channels=32, self_heads=36, cross_heads=16)
 SIDE = 32          # 1024 px / 32 (DC-AE f32 latent)
@@ -113,76 +127,115 @@ def step_lower_bound_ms(B, N, L, p_mfma_tflops, p_hbm_gbs, d=DIMS):
 
 
 def measured_peaks(sana_dit, torch, dev, stream):
-    """MFMA ceiling from sana_hip_mfma_peak and HBM rate from a 1 GiB copy, both
-    timed with HIP events on `stream`."""
+    """MFMA ceilings from sana_hip_mfma_peak (1024 workgroups of 4 waves, 8
+    independent accumulators per wave; fp16 operands spread over [-1, 1), and
+    all zero) and HBM rates from sana_hip_hbm_peak over 4 GiB (read only, and
+    copy), timed with HIP events on `stream`."""
     import ctypes
     L = sana_dit.lib()
-    wg, iters = 2048, 64
+    sp = stream.cuda_stream
+    wg, iters = 1024, 2000
     sink = torch.empty(wg * 256, device=dev, dtype=torch.float32)
     fl = ctypes.c_double()
-    sp = stream.cuda_stream
-    sana_dit.check(L.sana_hip_mfma_peak(wg, iters, sink.data_ptr(), sp, ctypes.byref(fl)))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(3):
-        sana_dit.check(L.sana_hip_mfma_peak(wg, iters, sink.data_ptr(), sp, ctypes.byref(fl)))
-    e1.record(stream)
-    torch.cuda.synchronize()
-    mfma = fl.value * 3 / (e0.elapsed_time(e1) * 1e-3) / 1e12
-    n = 1 << 28                                      # 1 GiB of fp32
-    src = torch.ones(n, device=dev, dtype=torch.float32)
-    dst = torch.empty_like(src)
-    with torch.cuda.stream(stream):
-        dst.copy_(src)
+    mfma = {}
+    for zero in (0, 1):
+        sana_dit.check(L.sana_hip_mfma_peak(wg, iters, zero, sink.data_ptr(), sp, ctypes.byref(fl)))
         e0.record(stream)
-        for _ in range(5):
-            dst.copy_(src)
+        for _ in range(3):
+            sana_dit.check(L.sana_hip_mfma_peak(wg, iters, zero, sink.data_ptr(), sp, ctypes.byref(fl)))
         e1.record(stream)
-    torch.cuda.synchronize()
-    hbm = 5 * 2 * n * 4 / (e0.elapsed_time(e1) * 1e-3) / 1e9
-    del src, dst, sink
-    return {"mfma_tflops": round(mfma, 1), "hbm_gbs": round(hbm, 1),
-            "how": "8 independent fp16 32x32x16 MFMA chains x 2048 workgroups; 1 GiB device copy (read + write)"}
+        torch.cuda.synchronize()
+        mfma[zero] = fl.value * 3 / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    nbytes = 4 << 30
+    nsink = ctypes.c_int64()
+    sana_dit.check(L.sana_hip_hbm_peak(None, None, 0, None, ctypes.byref(nsink), None))
+    hsink = torch.empty(nsink.value, device=dev, dtype=torch.float32)
+    src = torch.ones(nbytes // 4, device=dev, dtype=torch.float32)
+    dst = torch.empty_like(src)
+    rates = {}
+    for mode in ("read", "copy"):
+        def once():
+            sana_dit.check(L.sana_hip_hbm_peak(src.data_ptr(), dst.data_ptr() if mode == "copy" else None, nbytes,
+                                               hsink.data_ptr(), None, sp))
+        once()
+        e0.record(stream)
+        for _ in range(4):
+            once()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        moved = nbytes * (2 if mode == "copy" else 1)
+        rates[mode] = 4 * moved / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst, sink, hsink
+    return {"mfma_tflops": round(mfma[0], 1), "mfma_tflops_zero_operands": round(mfma[1], 1),
+            "hbm_read_gbs": round(rates["read"], 1), "hbm_copy_gbs": round(rates["copy"], 1),
+            "hbm_gbs": round(max(rates.values()), 1),
+            "how": "MFMA: 1024 workgroups x 4 waves, 8 independent fp16 32x32x16 accumulators per wave, no memory "
+                   "traffic, operands spread over [-1, 1) (mfma_tflops, the rate random weights see) and all zero "
+                   "(power-limited part: zeros run faster); HBM: 16-byte grid-stride streaming over 4 GiB, read only "
+                   "and copy (read + write)"}
 
 
-def cpu_baseline():
-    """The reference's own block_forward, 1 thread, one block of this workload."""
+def progress(msg):
+    """One line per finished phase on stderr (stdout carries only the JSON line)."""
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
+
+
+def _harness(*args, timeout=600):
     exe = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
-    B = 2
-    if os.path.exists(exe):
-        cmd = [exe, "time-block", str(DIMS["self_heads"]), str(DIMS["cross_heads"]), str(B), str(SIDE),
-               str(CPU_REPS)]
-        if shutil.which("taskset"):
-            cmd = ["taskset", "-c", "0"] + cmd
-        t0 = time.time()
-        out = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
-        if out.returncode != 0:
-            raise RuntimeError("reference CPU baseline failed: " + out.stderr[-500:])
-        block_ms = float([ln for ln in out.stdout.splitlines() if ln.startswith("median_block_ms")][0].split()[1])
-        kind = "reference"
-        wall = time.time() - t0
+    cmd = [exe] + [str(a) for a in args]
+    if shutil.which("taskset"):
+        cmd = ["taskset", "-c", "0"] + cmd
+    t0 = time.time()
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+    if out.returncode != 0:
+        raise RuntimeError("reference CPU baseline failed: " + out.stderr[-500:])
+    progress(f"cpu baseline: ref_harness {' '.join(str(a) for a in args)} done in {time.time() - t0:.1f} s")
+    vals = {}
+    for ln in out.stdout.splitlines():
+        parts = ln.split()
+        if len(parts) == 2:
+            try:
+                vals[parts[0]] = float(parts[1])
+            except ValueError:
+                pass
+    return vals
+
+
+def cpu_baseline(quick=False):
+    """The reference's own CPU code (oracle/_ref/ref_harness, built from the
+    reference's sources), 1 thread pinned to core 0: one full CFG step of this
+    workload (caption projection + 28-block forward), plus the single-block
+    configuration and the 4096-token microbenchmark.  quick: one block x 28
+    instead of the full step."""
+    exe = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
+    if not os.path.exists(exe):
+        return None
+    t0 = time.time()
+    res = {"unit": "ms/step", "cores": 1, "kind": "reference", "host_nproc": os.cpu_count()}
+    if quick:
+        blk = _harness("time-block", DIMS["self_heads"], DIMS["cross_heads"], 2, SIDE, CPU_REPS)["median_block_ms"]
+        res["value"] = round(blk * DIMS["layers"], 1)
+        res["sample"] = (f"extrapolated: one reference block_forward at B=2, N=1024, L=300, 36x32/16x72 heads, "
+                         f"median of {CPU_REPS} ({blk:.0f} ms), x28 blocks")
     else:
-        # Fallback: the oracle restatement of the same block, 1 thread.
-        sys.path.insert(0, os.path.join(ROOT, "tests"))
-        import numpy as np
-        import oracle_lib as O
-        O.lib().oracle_set_threads(1)
-        m = O.Model(layers=1, self_heads=DIMS["self_heads"], cross_heads=DIMS["cross_heads"])
-        x = O.randn((B, SIDE * SIDE, DIMS["hidden"]), 42) * np.float32(0.1)
-        tm = O.randn((B, 6 * DIMS["hidden"]), 44) * np.float32(0.05)
-        ctx = O.randn((B, CAPTION_LEN, DIMS["hidden"]), 43)
-        t0 = time.time()
-        m.block(0, x, ctx, tm)
-        block_ms = (time.time() - t0) * 1e3
-        kind = "port"
-        wall = block_ms / 1e3
-    ms = block_ms * DIMS["layers"]
-    return {"value": round(ms, 1), "unit": "ms/step", "cores": 1, "kind": kind,
-            "sample": (f"one DiT block (block_forward: self linear attention, cross attention incl. its K/V "
-                       f"projections, Mix-FFN) at B=2, N=1024, L=300, 36x32/16x72 heads, median of "
-                       f"{CPU_REPS if kind == 'reference' else 1} reps on 1 thread ({block_ms:.0f} ms), x28 blocks; "
-                       f"patch/time/final layers (<0.1% of FLOPs) untimed; {wall:.1f} s wall"),
-            "host_nproc": os.cpu_count()}
+        v = _harness("time-forward", DIMS["self_heads"], DIMS["cross_heads"], SIDE, timeout=900)
+        res["value"] = round(v["step_ms"], 1)
+        res["forward_ms"] = round(v["forward_ms"], 1)
+        res["caption_projection_ms"] = round(v["caption_projection_ms"], 1)
+        res["sample"] = ("one full CFG step as the reference runs it: caption projection (300x2304 -> 1152) + "
+                         "the 28-block forward of run_full_denoising_step_with_cfg at 1024 px, batch 2, t=999, "
+                         "36x32/16x72 heads, seeded N(0,0.02) weights, 1 thread")
+    c1 = _harness("time-block", 16, 16, 1, 16, CPU_REPS)
+    res["config1_block_ms"] = round(c1["median_block_ms"], 1)
+    c4 = _harness("time-micro", 64, CPU_REPS, timeout=900)
+    res["config4_linear_attention_ms"] = round(c4["median_linear_attention_ms"], 1)
+    res["config4_mixffn_ms"] = round(c4["median_mixffn_ms"], 1)
+    res["configs_note"] = ("config1: one block_forward, B=1, 16x16 latent (256 tokens), 16x72 self heads as "
+                           f"written, L=300, median of {CPU_REPS}; config4: linear_attention_4d on [2,16,4096,72] "
+                           f"and glumb_conv on [2,1152,64,64], median of {CPU_REPS}")
+    res["wall_s"] = round(time.time() - t0, 1)
+    return res
 
 
 def microbench_4096(sana_dit, torch, dev, stream):
@@ -339,15 +392,70 @@ def gemma_prompt_pair(sana_dit, rng, pos_tokens=438, neg_tokens=300):
             "shape": f"Gemma-2 2B, {pos_tokens} + {neg_tokens} tokens, host token ids in, host hidden states out"}
 
 
-def measured_traffic():
-    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (None when it is absent)."""
+def measured_traffic(path=TRAFFIC_FILE):
+    """Bytes per launch of each kernel role (qkv, attn_out, ...) from a
+    committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary of the same kernel
+    table ({role: bytes}; empty when absent)."""
     try:
-        text = open(TRAFFIC_FILE).read()
+        text = open(path).read()
     except OSError:
-        return None
-    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9]+)", text, re.M)
-    return int(m.group(1)) if m else None
+        return {}
+    return {m.group(1): int(m.group(2))
+            for m in re.finditer(r"^traffic_bytes_per_launch\s+(.+?):\s*([0-9]+)\s*$", text, re.M)}
+
+
+KERNEL_BOUND = {"qkv": "mfma", "attn_out": "mfma", "cross_q": "mfma", "cross_out": "mfma", "ffn_inverted": "mfma",
+                "ffn_point": "mfma", "ln_modulate": "hbm", "linear_attention": "hbm", "cross_attention": "hbm",
+                "dwconv_glu": "hbm"}
+LAUNCHES_PER_BLOCK = {"ln_modulate": 2}   # per batch-row chain; every other class runs once
+
+
+def kernel_table(d, branches, traffic):
+    """Every block kernel at its in-forward launch (sana_dit_time_kernel)."""
+    out = {}
+    chains = 2 if branches else 1
+    for which, cls in enumerate(d.KERNELS):
+        ms, fl, by, name = d.time_kernel(which, 2 * DIMS["layers"])
+        bound = KERNEL_BOUND[cls]
+        us = ms * 1e3
+        if bound == "mfma":
+            achieved, peak, unit = fl / (us * 1e-6) / 1e12, PEAK_MFMA_TFLOPS, "TFLOP/s"
+        else:
+            achieved, peak, unit = by / (us * 1e-6) / 1e9, PEAK_HBM_GBS, "GB/s"
+        out[cls] = {"kernel": name, "avg_us": round(us, 2),
+                    "launches_per_forward": DIMS["layers"] * chains * LAUNCHES_PER_BLOCK.get(cls, 1),
+                    "gflop": round(fl / 1e9, 4), "mbytes": round(by / 1e6, 3), "bound": bound,
+                    "achieved": round(achieved, 1), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+                    "traffic": traffic.get(cls)}
+    return out
+
+
+def dominant_roofline(kernels):
+    """The kernel (instantiation) with the largest total time per forward; the
+    roles that launch the same instantiation are one kernel, as in a trace."""
+    groups = {}
+    for cls, k in kernels.items():
+        g = groups.setdefault(k["kernel"], {"roles": [], "time": 0.0, "launches": 0, "flops": 0.0, "bytes": 0.0,
+                                             "bound": k["bound"], "traffic": 0.0})
+        n = k["launches_per_forward"]
+        g["roles"].append(cls)
+        # measured bytes per launch, averaged over the roles' launches like `bytes`
+        g["traffic"] = None if g["traffic"] is None or k["traffic"] is None else g["traffic"] + k["traffic"] * n
+        g["time"] += k["avg_us"] * n
+        g["launches"] += n
+        g["flops"] += k["gflop"] * 1e9 * n
+        g["bytes"] += k["mbytes"] * 1e6 * n
+    name, g = max(groups.items(), key=lambda kv: kv[1]["time"])
+    avg_us = g["time"] / g["launches"]
+    if g["bound"] == "mfma":
+        achieved, peak, unit = g["flops"] / (g["time"] * 1e-6) / 1e12, PEAK_MFMA_TFLOPS, "TFLOP/s"
+    else:
+        achieved, peak, unit = g["bytes"] / (g["time"] * 1e-6) / 1e9, PEAK_HBM_GBS, "GB/s"
+    return {"bound": g["bound"], "kernel": name, "roles": g["roles"], "achieved": round(achieved, 1), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4),
+            "traffic": None if g["traffic"] is None else round(g["traffic"] / g["launches"]),
+            "algorithmic_bytes": round(g["bytes"] / g["launches"]), "avg_us": round(avg_us, 2),
+            "launches_per_forward": g["launches"], "share_of_kernel_time": None}
 
 
 def main():
@@ -356,16 +464,20 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-quick", action="store_true",
+                    help="CPU baseline from one reference block x 28 instead of the full reference step")
     ap.add_argument("--pmc-calib", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the extra 4096 px forward and 4096-token microbenchmark lines (profiling runs)")
+    ap.add_argument("--extras-4096px-only", action="store_true",
+                    help="of the extras, run only the 4096 px forward and its kernel table (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for {args.gpus}); "
               "the multi-GPU sharding of the path is a design only", file=sys.stderr)
         sys.exit(2)
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline()   # before the GPU is touched
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_quick)   # before the GPU is touched
 
     import numpy as np
     import torch
@@ -418,6 +530,7 @@ def main():
     ev1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    progress(f"{args.steps} timed steps done")
     ev_ms = ev0.elapsed_time(ev1) / args.steps
     if not torch.isfinite(out).all():
         raise RuntimeError("non-finite velocity")
@@ -433,13 +546,13 @@ def main():
     torch.cuda.synchronize()
     fwd_ms = ev0.elapsed_time(ev1) / args.steps
 
-    # dominant kernel: Mix-FFN inverted 1x1 conv GEMM (2048 x 5760 x 1152), HIP events on its stream
-    gemm_ms, gemm_flops = d.time_gemm(4, 50)
-    gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
-    per_gemm = {}
-    for which, nm in enumerate(["qkv", "attn_out", "cross_q", "cross_out", "ffn_inverted", "ffn_point"]):
-        ms_w, fl_w = d.time_gemm(which, 20)
-        per_gemm[nm] = {"us": round(ms_w * 1e3, 2), "tflops": round(fl_w / (ms_w * 1e-3) / 1e12, 1)}
+    # every kernel class at its in-forward launch (the forward just ran), HIP events on its stream
+    branches = os.environ.get("SANA_DIT_CFG_BRANCHES", "1") != "0"
+    kernels = kernel_table(d, branches, measured_traffic())
+    progress("kernel table at 1024 px done")
+    roof = dominant_roofline(kernels)
+    total_kernel_us = sum(k["avg_us"] * k["launches_per_forward"] for k in kernels.values())
+    roof["share_of_kernel_time"] = round(roof["avg_us"] * roof["launches_per_forward"] / total_kernel_us, 4)
 
     extras = {}
     if not args.no_extras:
@@ -457,11 +570,16 @@ def main():
         c5_flops = forward_flops(B, 128 * 128, L, with_context=False)
         extras["forward_4096px"] = {"ms": round(c5_ms, 3), "tflops": round(c5_flops / (c5_ms * 1e-3) / 1e12, 1),
                                     "tokens": 128 * 128, "note": "28 blocks, CFG batch 2, context resident"}
-        extras["microbench_4096_tokens"] = microbench_4096(sana_dit, torch, dev, stream)
-        extras["vae_decode_1024px"] = vae_decode_1024px(sana_dit, torch, dev, stream, rng)
-        extras["gemma_encode_prompt_pair"] = gemma_prompt_pair(sana_dit, rng)
+        # the block kernels at 16384 tokens per batch row (working sets past the 256 MB last-level cache)
+        extras["kernels_4096px"] = kernel_table(d, branches, measured_traffic(TRAFFIC_FILE_4096))
+        progress("4096 px forward and kernel table done")
+        if not args.extras_4096px_only:
+            extras["microbench_4096_tokens"] = microbench_4096(sana_dit, torch, dev, stream)
+            extras["vae_decode_1024px"] = vae_decode_1024px(sana_dit, torch, dev, stream, rng)
+            extras["gemma_encode_prompt_pair"] = gemma_prompt_pair(sana_dit, rng)
 
     peaks = measured_peaks(sana_dit, torch, dev, stream)
+    progress("peaks measured")
     lb_spec = step_lower_bound_ms(B, N, L, PEAK_MFMA_TFLOPS, PEAK_HBM_GBS)
     lb_meas = step_lower_bound_ms(B, N, L, peaks["mfma_tflops"], peaks["hbm_gbs"])
 
@@ -489,20 +607,16 @@ def main():
         "step_mfma_frac": round(step_flops / (wall_ms * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 4),
         "step_gflop": round(step_flops / 1e9, 2),
         "forward_gflop_context_resident": round(fwd_flops / 1e9, 2),
-        "gemms": per_gemm,
-        "roofline": {"bound": "mfma",
-                     "kernel": "gemm_kernel (128x192 tiles, early stage release, bias+SiLU epilogue): "
-                               "Mix-FFN inverted 2048x5760x1152",
-                     "achieved": round(gemm_tflops, 1), "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tflops / PEAK_MFMA_TFLOPS, 4), "traffic": measured_traffic(),
-                     "algorithmic_bytes": GEMM_BYTES, "avg_us": round(gemm_ms * 1e3, 2)},
+        "kernels": kernels,
+        "roofline": roof,
         "cpu_baseline": cpu,
         "peaks_measured": peaks,
         "forward_roofline": {"lower_bound_ms_spec_peaks": round(lb_spec, 4), "frac_spec": round(lb_spec / wall_ms, 4),
                              "lower_bound_ms_measured_peaks": round(lb_meas, 4),
                              "frac_measured": round(lb_meas / wall_ms, 4),
                              "note": "sum over kernels of max(flops/MFMA peak, bytes/HBM peak) for one step; "
-                                     "frac = lower bound / measured ms_per_step"},
+                                     "frac = lower bound / measured ms_per_step; frac_spec (MI355X spec peaks "
+                                     "2516.6 TFLOP/s, 8000 GB/s) is the headline"},
         **extras,
     }
     d.close()

@@ -141,12 +141,22 @@ int sana_dit_loop_model_outputs(sana_dit * ctx, float * x0_prev, float * x0_last
 /* Time MLP of the forward (src/transformer.cpp:638-656): B timesteps ->
  * embedded [B, C] (pre-SiLU) and t_mod [B, 6C]. */
 int sana_dit_time_embed(sana_dit * ctx, const float * t, int64_t B, float * embedded, float * t_mod);
-/* Average duration (ms) over `iters` eager launches of one GEMM of the blocks
- * at the token count of the last forward (launch i uses block i mod layers, so
- * weights stream from HBM as in the forward): which = 0 QKV, 1 attn out,
- * 2 cross q, 3 cross out, 4 FFN inverted, 5 FFN point.  Also returns its
- * FLOPs.  Overwrites the forward's activation buffers. */
-int sana_dit_time_gemm(sana_dit * ctx, int which, int iters, float * avg_ms, double * flops);
+/* Measurement hook (no counterpart in the reference): average duration (ms)
+ * over `iters` back-to-back eager launches of one kernel of the blocks, launched
+ * exactly as the last forward launched it -- the same kernel instantiation and
+ * shape (one batch row of a CFG pair per launch when the forward ran the pair as
+ * two branches), on the forward's own buffers, which it overwrites.  Launch i
+ * uses block i mod layers, so weights stream from HBM as in the forward.
+ * which: 0 QKV GEMM, 1 attn-out GEMM (+ gated residual), 2 cross-q GEMM,
+ * 3 cross-out GEMM (+ residual), 4 FFN inverted GEMM (+ SiLU), 5 FFN point GEMM
+ * (+ gated residual), 6 LayerNorm + modulate, 7 linear attention, 8 cross
+ * attention, 9 depthwise 3x3 + GLU.  Also returns the launch's algorithmic
+ * flops (contractions) and bytes (interface tensors at their stored precision,
+ * GEMM weights included, no re-reads), and in `name` (when not NULL, up to
+ * name_cap bytes with the terminating 0) the launched kernel as rocprofv3
+ * names it.  Needs a context and a forward. */
+int sana_dit_time_kernel(sana_dit * ctx, int which, int iters, float * avg_ms, double * flops, double * bytes,
+                         char * name, size_t name_cap);
 
 /* ---- DC-AE VAE decoder: latent -> RGB (src/vae.h:11-92, src/vae.cpp) ----
  * Levels are indexed as the reference's decoder.up_blocks.{i} (level 0 = the
@@ -221,11 +231,24 @@ int sana_gemma_load_gguf(sana_gemma * g, const char * path);
 int sana_gemma_encode(sana_gemma * g, const int32_t * tokens, int64_t n, float * hidden);
 
 /* Measured MFMA ceiling for roofline reports (no counterpart in the reference):
- * `workgroups` x 256 threads run `iters` steps of 8 independent fp16
- * v_mfma_f32_32x32x16 chains with no memory traffic, asynchronously on `stream`;
- * `sink` (device, workgroups * 256 floats) receives the sums; *flops is the
- * work of the launch.  The caller times it (e.g. with events). */
-int sana_hip_mfma_peak(int64_t workgroups, int64_t iters, float * sink, void * stream, double * flops);
+ * `workgroups` x 256 threads (4 waves) run `iters` steps of 8 independent fp16
+ * v_mfma_f32_32x32x16 accumulators per wave (4 A x 2 B register fragments) with
+ * no memory traffic, asynchronously on `stream`; `sink` (device, workgroups *
+ * 256 floats) receives the sums; *flops is the work of the launch.  Operands
+ * are fp16 values spread over [-1, 1) (as random weights are), or all zero
+ * when `zero_operands` is nonzero: the part is power limited, and zeros run
+ * faster.  The caller times it (e.g. with events); 1024 workgroups (4 waves
+ * per SIMD) give the peak. */
+int sana_hip_mfma_peak(int64_t workgroups, int64_t iters, int zero_operands, float * sink, void * stream,
+                       double * flops);
+/* Measured HBM ceiling (no counterpart in the reference): streams `bytes` (a
+ * multiple of 16) from device buffer src into dst (copy: bytes read + bytes
+ * written) or, with dst NULL, into per-thread sums in sink (read only; sink
+ * holds *sink_floats floats, returned when sink is NULL and dst is NULL with
+ * bytes 0).  Asynchronous on `stream`; the caller times it.  Use buffers far
+ * larger than the 256 MB last-level cache. */
+int sana_hip_hbm_peak(const void * src, void * dst, int64_t bytes, float * sink, int64_t * sink_floats,
+                      void * stream);
 
 /* GGUF index inspection (no GPU needed): number of tensors, and the name,
  * PyTorch-order shape (up to 4 dims), ggml type and absolute payload offset of

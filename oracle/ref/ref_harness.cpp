@@ -284,6 +284,8 @@ int usage() {
         "  ref_harness forward SELF_HEADS CROSS_HEADS SIDE T MASK CHECK_STEP OUTDIR\n"
         "  ref_harness loop SELF_HEADS CROSS_HEADS SIDE STEPS GUIDANCE MASK OUTDIR\n"
         "  ref_harness time-block SELF_HEADS CROSS_HEADS BATCH SIDE REPS\n"
+        "  ref_harness time-forward SELF_HEADS CROSS_HEADS SIDE\n"
+        "  ref_harness time-micro SIDE REPS\n"
         "  ref_harness vae small|full SIDE OUTDIR\n"
         "  ref_harness vae-conv SIDE CIN COUT OUTDIR\n"
         "  ref_harness vae-digest small|full\n");
@@ -424,6 +426,59 @@ int main(int argc, char ** argv) {
             Tensor img = run_vae_decode(latent, w);
             std::printf("vae_decode_ms %.3f\n", now_ms() - t0);
             dump(out, "image", img);
+            return 0;
+        }
+        if (mode == "time-forward" && argc == 5) {
+            // one CFG step's forward as the reference runs it in its loop: the
+            // caption projection (once per loop, src/transformer.cpp:701-708) and
+            // the forward of run_full_denoising_step_with_cfg (:627-681)
+            const size_t sh = std::stoul(argv[2]), ch = std::stoul(argv[3]), side = std::stoul(argv[4]);
+            double t0 = now_ms();
+            SanaDenoiserWeights w = make_denoiser(g, d, d.layers, sh, ch);
+            Tensor latent = randn_torch_cpu({1, d.latent, side, side}, 42);
+            Tensor caption = randn_torch_cpu({2, 300, d.caption}, 43);
+            std::printf("setup_ms %.3f\n", now_ms() - t0);
+            std::fflush(stdout);
+            t0 = now_ms();
+            Tensor ctx = project_caption_context(caption, w.caption.linear_1_weight, &w.caption.linear_1_bias,
+                                                 w.caption.linear_2_weight, &w.caption.linear_2_bias,
+                                                 w.caption_norm_weight);
+            const double cap_ms = now_ms() - t0;
+            std::printf("caption_projection_ms %.3f\n", cap_ms);
+            std::fflush(stdout);
+            t0 = now_ms();
+            Tensor np = forward_noise_pred(latent, ctx, 999.0f, w, nullptr);
+            const double fwd_ms = now_ms() - t0;
+            std::printf("forward_ms %.3f\nstep_ms %.3f\n", fwd_ms, fwd_ms + cap_ms);
+            return np.numel() ? 0 : 1;
+        }
+        if (mode == "time-micro" && argc == 4) {
+            // linear_attention_4d on [2, 16, N, 72] and glumb_conv on [2, 1152, SIDE, SIDE]
+            // (Mix-FFN 1152 -> 5760 -> 2880 -> 1152), inputs N(0, 1), weights N(0, 0.02)
+            const size_t side = std::stoul(argv[2]), reps = std::stoul(argv[3]), N = side * side;
+            Tensor q = randn_torch_cpu({2, 16, N, 72}, 61), k = randn_torch_cpu({2, 16, N, 72}, 62),
+                   v = randn_torch_cpu({2, 16, N, 72}, 63);
+            Tensor x = randn_torch_cpu({2, d.hidden, side, side}, 64);
+            Tensor wi = randn_torch_cpu({d.ffn, d.hidden, 1, 1}, 65), bi = randn_torch_cpu({d.ffn}, 66);
+            Tensor wd = randn_torch_cpu({d.ffn, 1, 3, 3}, 67), bd = randn_torch_cpu({d.ffn}, 68);
+            Tensor wp = randn_torch_cpu({d.hidden, d.ffn / 2, 1, 1}, 69);
+            for (Tensor * t : {&wi, &bi, &wd, &bd, &wp}) t->mul_inplace_scalar(0.02f);
+            std::vector<double> la, ff;
+            for (size_t r = 0; r < reps; ++r) {
+                double t0 = now_ms();
+                Tensor o = linear_attention_4d(q, k, v);
+                la.push_back(now_ms() - t0);
+                t0 = now_ms();
+                Tensor y = glumb_conv(x, wi, &bi, wd, &bd, wp);
+                ff.push_back(now_ms() - t0);
+                if (!o.numel() || !y.numel()) return 1;
+                std::printf("rep %zu linear_attention_ms %.3f mixffn_ms %.3f\n", r, la.back(), ff.back());
+                std::fflush(stdout);
+            }
+            std::sort(la.begin(), la.end());
+            std::sort(ff.begin(), ff.end());
+            std::printf("median_linear_attention_ms %.3f\nmedian_mixffn_ms %.3f\n", la[la.size() / 2],
+                        ff[ff.size() / 2]);
             return 0;
         }
         if (mode == "time-block" && argc == 7) {

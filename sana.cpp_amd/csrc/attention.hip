@@ -1,6 +1,7 @@
 // K3 ReLU linear attention and K4 softmax cross-attention.
 #include <algorithm>
 #include <cmath>
+#include <string>
 
 #include "hip_common.h"
 #include "kernels.h"
@@ -855,6 +856,9 @@ hipError_t launch_xattn_lds1(const f16 * q, int64_t ldq, const f16 * k, int64_t 
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, X::LDS_BYTES) ==
                              hipSuccess;
     (void)attr;
+    static const std::string name = "xattn_lds_kernel<" + std::to_string(LT) + ", " + std::to_string(KS) + ", " +
+                                    (ONES ? "true" : "false") + ">";
+    note_kernel(name.c_str());
     hipLaunchKernelGGL((xattn_lds_kernel<LT, KS, ONES>), dim3(H, (N + kXaQ - 1) / kXaQ, B), dim3(512), X::LDS_BYTES,
                        s, q, ldq, k, ldk, vt, ldvt, bias, out, ldo, N, L, D, scale);
     return hipGetLastError();
@@ -887,6 +891,8 @@ template <int LT>
 hipError_t launch_xattn(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
                         const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D, float scale,
                         int vec, hipStream_t s) {
+    static const std::string name = "xattn_kernel<" + std::to_string(LT) + ">";
+    note_kernel(name.c_str());
     hipLaunchKernelGGL((xattn_kernel<LT>), dim3((N + 63) / 64, H, B), dim3(256), 0, s, q, ldq, k, ldk, vt, ldvt, bias,
                        out, ldo, N, L, H, D, scale, vec);
     return hipGetLastError();
@@ -914,6 +920,7 @@ hipError_t linear_attention_fused(const half_t * q, int64_t ldq, const half_t * 
         return hipErrorInvalidValue;
     // enough workgroups for the 256 CUs: (b, h) pairs times token splits
     const int splits = (int)std::max<int64_t>(1, std::min<int64_t>(8, 256 / ((int64_t)B * H * std::max(co, 1))));
+    note_kernel("la_fused_kernel");
     hipLaunchKernelGGL(la_fused_kernel, dim3((unsigned)(B * H * splits)), dim3(64 * kLfWaves), 0, s,
                        reinterpret_cast<const f16 *>(q), ldq, reinterpret_cast<const f16 *>(kt),
                        reinterpret_cast<const f16 *>(vt), reinterpret_cast<f16 *>(out), ldo, N, H, splits);
@@ -951,6 +958,7 @@ hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v
     const int vec_kv = (D % 8 == 0 && ld % 8 == 0 && al16(k) && al16(v)) ? 1 : 0;
     const int vec_q = (D % 8 == 0 && ld % 8 == 0 && al16(q)) ? 1 : 0;
     const dim3 g1(nch, H, B);
+    note_kernel("la_state_kernel + la_reduce_kernel + la_apply_kernel");
     const int td = (D + 31) / 32;
     if (td == 1) hipLaunchKernelGGL((la_state_kernel<1>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
     else if (td == 2) hipLaunchKernelGGL((la_state_kernel<2>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);

@@ -79,6 +79,11 @@ struct GraphEntry {
 
 namespace sana {
 void set_last_error(const std::string & m) { g_last_error = m; }
+namespace {
+thread_local const char * g_last_kernel = "";
+}
+void note_kernel(const char * name) { g_last_kernel = name; }
+const char * last_kernel() { return g_last_kernel; }
 }  // namespace sana
 
 struct sana_dit {
@@ -1088,65 +1093,133 @@ int sana_dit_time_embed(sana_dit * c, const float * t, int64_t B, float * embedd
     });
 }
 
-int sana_dit_time_gemm(sana_dit * c, int which, int iters, float * avg_ms, double * flops) {
+int sana_dit_time_kernel(sana_dit * c, int which, int iters, float * avg_ms, double * flops, double * bytes,
+                         char * name, size_t name_cap) {
     if (!c || !avg_ms || iters <= 0) return set_err(SANA_ERR_INVALID_ARGUMENT, "bad argument");
     if (c->last_M <= 0) return set_err(SANA_ERR_STATE, "run a forward first");
-    if (which < 0 || which > 5) return set_err(SANA_ERR_INVALID_ARGUMENT, "which must be 0..5");
+    if (which < 0 || which > 9) return set_err(SANA_ERR_INVALID_ARGUMENT, "which must be 0..9");
+    if (!c->ctx_ready) return set_err(SANA_ERR_STATE, "no context set");
     return guarded([&] {
-        const int64_t M = c->last_M, C = c->C, N = c->last_N;
-        // Scratch outputs: the dedicated buffers of each GEMM in the forward.
-        // Launch i uses block i's weights, cycling as the forward does, so the
-        // weights stream from HBM instead of staying in cache.
+        // The shape and launch of the last forward: one batch row per launch
+        // (co = 2) when the CFG pair ran as two branches, else the whole batch.
+        const int64_t N = c->last_N, C = c->C, E = c->E, F = c->F, Lc = c->ctx_L, Btot = c->last_B;
+        const bool branches = Btot == 2 && c->cfg_branches;
+        const int64_t B = branches ? 1 : Btot, M = B * N, side = (int64_t)std::llround(std::sqrt((double)N));
+        const int co = branches ? 2 : 1;
+        hipStream_t s = c->stream;
+        const float * xbias = c->ctx_bias ? c->bias.as<float>() : nullptr;
+        // Launch i runs block i mod layers, as the forward cycles through the
+        // blocks, so the weights come from HBM; outputs go to the forward's own
+        // buffers (they are overwritten).
         auto run = [&](int i) {
-            BlockDev & w = *c->blocks[i % c->L_];
+            const int64_t blk = i % c->L_;
+            BlockDev & w = *c->blocks[blk];
+            const float * mod = c->mod_all.as<float>() + (size_t)blk * Btot * 6 * C;
+            half_t * kt16 = c->la_kt.as<half_t>();
+            half_t * vt16 = c->la_vt.as<half_t>();
             switch (which) {
                 case 0:
                     if (fused_linear_attention(c, N))
-                        gemm_qkv_split(c, w, M / N, N, c->xa16.as<half_t>(), c->qkv16.as<half_t>(),
-                                       c->la_kt.as<half_t>(), c->la_vt.as<half_t>(), 1, c->stream);
+                        gemm_qkv_split(c, w, B, N, c->xa16.as<half_t>(), c->qkv16.as<half_t>(), kt16, vt16, co, s);
                     else
                         gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
-                                   nullptr, sana::kActNone, c->qkv16.as<half_t>(), 3 * C, nullptr, 0, c->stream);
+                                   nullptr, sana::kActNone, c->qkv16.as<half_t>(), 3 * C, nullptr, 0, s, co);
                     break;
                 case 1:
                     gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_out.as<half_t>(), c->Cp, M, C, c->Cp,
-                               w.b_out.as<float>(), c->mod_all.as<float>() + 2 * C, nullptr, 6 * C, N,
-                               c->x32.as<float>(), C, c->r16.as<half_t>(), c->Cp, c->stream);
+                               w.b_out.as<float>(), mod + 2 * C, nullptr, 6 * C, N, c->x32.as<float>(), C,
+                               c->r16.as<half_t>(), c->Cp, s, co);
                     break;
                 case 2:
                     gemm_store(c, c->r16.as<half_t>(), c->Cp, w.w_cq.as<half_t>(), c->Cp, M, C, c->Cp,
-                               w.b_cq.as<float>(), sana::kActNone, c->q16.as<half_t>(), C, nullptr, 0, c->stream);
+                               w.b_cq.as<float>(), sana::kActNone, c->q16.as<half_t>(), C, nullptr, 0, s, co);
                     break;
                 case 3:
-                    gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_co.as<half_t>(), c->Cp, M, C, c->Cp, w.b_co.as<float>(),
-                               nullptr, nullptr, 0, N, c->x32.as<float>(), C, nullptr, 0, c->stream);
+                    gemm_resid(c->o16.as<half_t>(), c->Cp, w.w_co.as<half_t>(), c->Cp, M, C, c->Cp,
+                               w.b_co.as<float>(), nullptr, nullptr, 0, N, c->x32.as<float>(), C, nullptr, 0, s, co);
                     break;
                 case 4:
-                    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_inv.as<half_t>(), c->Cp, M, c->E, c->Cp,
-                               w.b_inv.as<float>(), sana::kActSilu, c->hid16.as<half_t>(), c->E, nullptr, 0, c->stream);
+                    gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_inv.as<half_t>(), c->Cp, M, E, c->Cp,
+                               w.b_inv.as<float>(), sana::kActSilu, c->hid16.as<half_t>(), E, nullptr, 0, s, co);
                     break;
-                default:
+                case 5:
                     gemm_resid(c->glu16.as<half_t>(), c->Fp, w.w_pt.as<half_t>(), c->Fp, M, C, c->Fp, nullptr,
-                               c->mod_all.as<float>() + 5 * C, nullptr, 6 * C, N, c->x32.as<float>(), C,
-                               nullptr, 0, c->stream);
+                               mod + 5 * C, nullptr, 6 * C, N, c->x32.as<float>(), C, nullptr, 0, s, co);
+                    break;
+                case 6:
+                    launch_check(sana::ln_modulate(c->x32.as<float>(), C, c->xa16.as<half_t>(), c->Cp, (int)M, (int)C,
+                                                   (int)N, 1e-6f, w.has_ln1 ? w.ln1_g.as<float>() : nullptr,
+                                                   w.has_ln1 ? w.ln1_b.as<float>() : nullptr, mod, nullptr, 6 * C, 0,
+                                                   C, s),
+                                 "ln_modulate");
+                    break;
+                case 7:
+                    if (fused_linear_attention(c, N))
+                        launch_check(sana::linear_attention_fused(c->qkv16.as<half_t>(), 3 * C, kt16, vt16,
+                                                                  c->o16.as<half_t>(), c->Cp, (int)B, (int)N,
+                                                                  (int)c->Hs, (int)c->Ds, s, co),
+                                     "linear_attention_fused");
+                    else
+                        launch_check(sana::linear_attention(c->qkv16.as<half_t>(), c->qkv16.as<half_t>() + C,
+                                                            c->qkv16.as<half_t>() + 2 * C, 3 * C, c->o16.as<half_t>(),
+                                                            c->Cp, (int)B, (int)N, (int)c->Hs, (int)c->Ds,
+                                                            c->la_ws.as<float>(), s),
+                                     "linear_attention");
+                    break;
+                case 8: {
+                    const half_t * kc = c->kc.as<half_t>() + blk * C;
+                    const half_t * vt = c->vt.as<half_t>() + (size_t)blk * Btot * C * c->ctx_Lp;
+                    launch_check(sana::cross_attention(c->q16.as<half_t>(), C, kc, c->L_ * C, vt, c->ctx_Lp, xbias,
+                                                       c->o16.as<half_t>(), c->Cp, (int)B, (int)N, (int)Lc, (int)c->Hc,
+                                                       (int)c->Dc, s),
+                                 "cross_attention");
+                    break;
+                }
+                default:
+                    launch_check(sana::dwconv_glu(c->hid16.as<half_t>(), E, w.w_dw.as<float>(), w.b_dw.as<float>(),
+                                                  c->glu16.as<half_t>(), c->Fp, (int)B, (int)side, (int)side, (int)F,
+                                                  s),
+                                 "dwconv_glu");
             }
         };
-        const double f[6] = {2.0 * M * 3 * C * C, 2.0 * M * C * C, 2.0 * M * C * C, 2.0 * M * C * C,
-                             2.0 * M * c->E * C, 2.0 * M * C * c->F};
+        // algorithmic work per launch: flops of the contractions; bytes of the
+        // interface tensors at their stored precision (weights included for the
+        // GEMMs, no re-reads)
+        const double m = (double)M, h2 = 2.0, f4 = 4.0;
+        double fl = 0.0, by = 0.0;
+        switch (which) {
+            case 0: fl = 2 * m * 3 * C * C; by = h2 * (m * C + 3.0 * C * C + m * 3 * C); break;
+            case 1: fl = 2 * m * C * C; by = h2 * (m * C + (double)C * C + m * C) + f4 * 2 * m * C; break;
+            case 2: fl = 2 * m * C * C; by = h2 * (m * C + (double)C * C + m * C); break;
+            case 3: fl = 2 * m * C * C; by = h2 * (m * C + (double)C * C) + f4 * 2 * m * C; break;
+            case 4: fl = 2 * m * E * C; by = h2 * (m * C + (double)E * C + m * E); break;
+            case 5: fl = 2 * m * C * F; by = h2 * (m * F + (double)C * F) + f4 * 2 * m * C; break;
+            case 6: fl = 0.0; by = f4 * m * C + h2 * m * C; break;
+            case 7: fl = 2.0 * 2 * B * N * c->Hs * (c->Ds + 1) * c->Ds; by = h2 * 4 * m * C; break;
+            case 8: fl = 2.0 * 2 * B * N * Lc * C; by = h2 * (2 * m * C + 2.0 * B * Lc * C); break;
+            default: fl = 2.0 * m * E * 9; by = h2 * (m * E + m * F); break;
+        }
         run(c->L_ - 1);  // warm
         hipEvent_t e0, e1;
         hip_check(hipEventCreate(&e0), "event");
         hip_check(hipEventCreate(&e1), "event");
-        hip_check(hipEventRecord(e0, c->stream), "record");
+        hip_check(hipEventRecord(e0, s), "record");
         for (int i = 0; i < iters; ++i) run(i);
-        hip_check(hipEventRecord(e1, c->stream), "record");
+        hip_check(hipEventRecord(e1, s), "record");
         hip_check(hipEventSynchronize(e1), "sync");
         float ms = 0.0f;
         hip_check(hipEventElapsedTime(&ms, e0, e1), "elapsed");
         (void)hipEventDestroy(e0);
         (void)hipEventDestroy(e1);
         *avg_ms = ms / iters;
-        if (flops) *flops = f[which];
+        if (flops) *flops = fl;
+        if (bytes) *bytes = by;
+        if (name && name_cap) {
+            const std::string nm = sana::last_kernel();
+            const size_t n = std::min(nm.size(), name_cap - 1);
+            std::memcpy(name, nm.data(), n);
+            name[n] = '\0';
+        }
     });
 }
 
@@ -1216,12 +1289,27 @@ int sana_hip_dwconv_glu(const void * x, int64_t ldx, const float * wt, const flo
     });
 }
 
-int sana_hip_mfma_peak(int64_t workgroups, int64_t iters, float * sink, void * stream, double * flops) {
+int sana_hip_hbm_peak(const void * src, void * dst, int64_t bytes, float * sink, int64_t * sink_floats,
+                      void * stream) {
+    return guarded([&] {
+        if (sink_floats) *sink_floats = (int64_t)sana::hbm_peak_workgroups() * 256;
+        if (!src && !dst && !sink && bytes == 0) return;
+        if (!src || bytes < 16 || bytes % 16 || (!dst && !sink))
+            throw SanaError{SANA_ERR_INVALID_ARGUMENT, "hbm_peak: src, bytes (a positive multiple of 16) and dst or "
+                                                       "sink required"};
+        launch_check(sana::hbm_peak(src, dst, bytes, sink, static_cast<hipStream_t>(stream)), "hbm_peak");
+    });
+}
+
+int sana_hip_mfma_peak(int64_t workgroups, int64_t iters, int zero_operands, float * sink, void * stream,
+                       double * flops) {
     return guarded([&] {
         if (workgroups <= 0 || workgroups > 65536 || iters <= 0 || iters > (1 << 24) || !sink || !flops)
             throw SanaError{SANA_ERR_INVALID_ARGUMENT, "mfma_peak: workgroups in [1, 65536], iters in [1, 2^24], "
                                                        "sink and flops required"};
-        launch_check(sana::mfma_peak((int)workgroups, (int)iters, sink, static_cast<hipStream_t>(stream)), "mfma_peak");
+        launch_check(sana::mfma_peak((int)workgroups, (int)iters, zero_operands != 0, sink,
+                                     static_cast<hipStream_t>(stream)),
+                     "mfma_peak");
         *flops = sana::mfma_peak_flops((int)workgroups, (int)iters);
     });
 }

@@ -150,10 +150,12 @@ hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const flo
         constexpr int XS = 4;
         const int nseg = (Ww + XS - 1) / XS;
         if ((int64_t)Hh * nseg > 2147483647 || B > 65535) return hipErrorInvalidValue;
+        note_kernel("dwglu_row_kernel<4>");
         hipLaunchKernelGGL((dwglu_row_kernel<XS>), dim3((F / 8 + 63) / 64, Hh * nseg, B), dim3(64), 0, s, xx, ldx, wt,
                            bias, oo, ldo, Hh, Ww, F);
     } else {
         const int64_t total = (int64_t)B * Hh * Ww * F;
+        note_kernel("dwglu_scalar_kernel");
         hipLaunchKernelGGL(dwglu_scalar_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, xx, ldx, wt,
                            bias, oo, ldo, B, Hh, Ww, F);
     }

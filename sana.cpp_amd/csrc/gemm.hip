@@ -35,6 +35,8 @@
 //   residual: x += gate * (acc + bias), optional fp16 copy of the new x
 //             (mul_inplace_broadcast_lastdim + add_inplace, src/tensor.cpp:101-160)
 //   V^T     : transposed per-batch store of the cross-attention values.
+#include <string>
+
 #include "hip_common.h"
 #include "kernels.h"
 
@@ -570,6 +572,11 @@ hipError_t launch_mode(const GemmParams & p, int tiles, hipStream_t s) {
     static const bool attr = set_lds_limit(
         reinterpret_cast<const void *>(&gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT, CONV>), G::LDS_BYTES);
     (void)attr;
+    static const std::string name = "gemm_kernel<" + std::to_string(BM) + ", " + std::to_string(BN) + ", " +
+                                    std::to_string(WM) + ", " + std::to_string(WN) + ", " + std::to_string(STAGES) +
+                                    ", " + std::to_string(MODE) + ", " + std::to_string(SCHED) + ", " +
+                                    std::to_string(ACT) + ", " + std::to_string(CONV) + ">";
+    note_kernel(name.c_str());
     hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT, CONV>), dim3(tiles), dim3(G::NT),
                        G::LDS_BYTES, s, p);
     return hipGetLastError();

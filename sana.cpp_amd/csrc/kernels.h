@@ -76,6 +76,12 @@ struct GemmParams {
 
 hipError_t gemm(const GemmParams & p, hipStream_t s);
 
+// Name of the last kernel (instantiation) a launcher on this thread launched,
+// as rocprofv3 prints it, for the measurement hooks; launchers record it with
+// note_kernel (a pointer to storage that outlives the call).
+void note_kernel(const char * name);
+const char * last_kernel();
+
 // LayerNorm (eps, optional gamma/beta) + adaLN modulate, fp32 in, fp16 out:
 // out[m, c] = f16(ln(x)[m, c] * (1 + scale) + shift), with
 // shift = mod_a[b * mod_stride + shift_off + c] + mod_t[shift_off + c] (same for scale; mod_t may be null).
@@ -135,8 +141,13 @@ hipError_t cross_attention(const half_t * q, int64_t ldq, const half_t * k, int6
 // out[b, t, c] = f16(d(c) * silu(d(F + c))), out fp16 [B*H*W, ldo].
 // Measured MFMA ceiling: `workgroups` x 256 threads of independent fp16
 // 32x32x16 MFMA chains, `iters` steps; sink holds workgroups * 256 floats.
-hipError_t mfma_peak(int workgroups, int iters, float * sink, hipStream_t s);
+hipError_t mfma_peak(int workgroups, int iters, bool zero_operands, float * sink, hipStream_t s);
 double mfma_peak_flops(int workgroups, int iters);
+// Measured HBM ceiling: streams `bytes` (a multiple of 16) from src, into dst
+// (copy) or, with dst null, into per-thread sums in sink (read only; sink holds
+// hbm_peak_workgroups() * 256 floats).
+int hbm_peak_workgroups();
+hipError_t hbm_peak(const void * src, void * dst, int64_t bytes, float * sink, hipStream_t s);
 
 hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const float * bias, half_t * out, int64_t ldo,
                       int B, int Hh, int Ww, int F, hipStream_t s);

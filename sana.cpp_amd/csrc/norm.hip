@@ -410,19 +410,24 @@ hipError_t ln_modulate(const float * x, int64_t ldx, half_t * out, int64_t ldo, 
                        reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) & 15) == 0;
     if (vec) {
 #define SANA_LN_VEC(n4)                                                                                           \
-    hipLaunchKernelGGL((ln_modulate_vec_kernel<n4>), dim3((M + 3) / 4), dim3(256), 0, s, x, ldx,                   \
-                       reinterpret_cast<f16 *>(out), ldo, M, C, rpb, eps, gamma, beta, mod_a, mod_t, mod_stride,  \
-                       shift_off, scale_off)
+    do {                                                                                                          \
+        note_kernel("ln_modulate_vec_kernel<" #n4 ">");                                                            \
+        hipLaunchKernelGGL((ln_modulate_vec_kernel<n4>), dim3((M + 3) / 4), dim3(256), 0, s, x, ldx,               \
+                           reinterpret_cast<f16 *>(out), ldo, M, C, rpb, eps, gamma, beta, mod_a, mod_t,          \
+                           mod_stride, shift_off, scale_off);                                                     \
+    } while (0)
         const int per = (C / 4 + 63) / 64;  // float4 chunks per lane
         if (per <= 2) SANA_LN_VEC(2);
         else if (per <= 3) SANA_LN_VEC(3);
         else if (per <= 5) SANA_LN_VEC(5);
         else SANA_LN_VEC(kMaxPerLane / 4);
 #undef SANA_LN_VEC
-    } else
+    } else {
+        note_kernel("ln_modulate_kernel");
         hipLaunchKernelGGL(ln_modulate_kernel, dim3((M + 3) / 4), dim3(256), 0, s, x, ldx,
                            reinterpret_cast<f16 *>(out), ldo, M, C, rpb, eps, gamma, beta, mod_a, mod_t, mod_stride,
                            shift_off, scale_off);
+    }
     return hipGetLastError();
 }
 

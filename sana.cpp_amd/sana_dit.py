@@ -71,7 +71,9 @@ PROTOTYPES = {
                                                     _vp]),
     "sana_dit_loop_model_outputs": (ctypes.c_int, [_vp, _vp, _vp]),
     "sana_dit_time_embed": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
-    "sana_dit_time_gemm": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _fp, ctypes.POINTER(ctypes.c_double)]),
+    "sana_hip_hbm_peak": (ctypes.c_int, [_vp, _vp, _i64, _vp, ctypes.POINTER(_i64), _vp]),
+    "sana_dit_time_kernel": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _fp, ctypes.POINTER(ctypes.c_double),
+                                            ctypes.POINTER(ctypes.c_double), ctypes.c_char_p, ctypes.c_size_t]),
     "sana_gguf_num_tensors": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_i64)]),
     "sana_gguf_tensor_info": (ctypes.c_int, [ctypes.c_char_p, _i64, ctypes.c_char_p, ctypes.c_size_t,
                                              ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_int),
@@ -87,7 +89,7 @@ PROTOTYPES = {
     "sana_hip_cross_attention": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
                                                 _i64, _i64, _vp]),
     "sana_hip_dwconv_glu": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
-    "sana_hip_mfma_peak": (ctypes.c_int, [_i64, _i64, _vp, _vp, ctypes.POINTER(ctypes.c_double)]),
+    "sana_hip_mfma_peak": (ctypes.c_int, [_i64, _i64, ctypes.c_int, _vp, _vp, ctypes.POINTER(ctypes.c_double)]),
     "sana_vae_create": (ctypes.c_int, [ctypes.POINTER(VaeConfig), ctypes.POINTER(_vp)]),
     "sana_vae_destroy": (ctypes.c_int, [_vp]),
     "sana_vae_set_weight": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, ctypes.POINTER(_i64), ctypes.c_int]),
@@ -263,11 +265,19 @@ class Dit:
         check(lib().sana_dit_time_embed(self.h, ptr(t), t.size, ptr(emb), ptr(tmod)))
         return emb, tmod
 
-    def time_gemm(self, which, iters):
+    # kernel classes of sana_dit_time_kernel, in its `which` order
+    KERNELS = ("qkv", "attn_out", "cross_q", "cross_out", "ffn_inverted", "ffn_point", "ln_modulate",
+               "linear_attention", "cross_attention", "dwconv_glu")
+
+    def time_kernel(self, which, iters):
+        """(avg ms, flops, bytes, kernel name) of one block kernel launched as the
+        last forward launched it."""
         ms = ctypes.c_float()
-        fl = ctypes.c_double()
-        check(lib().sana_dit_time_gemm(self.h, which, iters, ctypes.byref(ms), ctypes.byref(fl)))
-        return ms.value, fl.value
+        fl, by = ctypes.c_double(), ctypes.c_double()
+        name = ctypes.create_string_buffer(256)
+        check(lib().sana_dit_time_kernel(self.h, which, iters, ctypes.byref(ms), ctypes.byref(fl), ctypes.byref(by),
+                                         name, 256))
+        return ms.value, fl.value, by.value, name.value.decode()
 
 
 def gguf_index(path):

@@ -263,3 +263,36 @@ def test_dwconv_glu(L, B, S, F):
                                         stream()))
     got = host(out).reshape(B, S, S, F)
     assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
+
+
+def test_peak_kernels_do_their_work(L):
+    """The roofline ceilings' kernels: the HBM copy moves every byte, the
+    read-only pass sums every element, and the MFMA loop gives finite sums
+    (zero with zero operands)."""
+    import ctypes
+    lib = L.lib()
+    n = (3 << 20) + 4                       # not a multiple of the grid's thread count
+    src = torch.arange(n, device="cuda", dtype=torch.float32).remainder_(7.0)
+    dst = torch.zeros_like(src)
+    nsink = ctypes.c_int64()
+    L.check(lib.sana_hip_hbm_peak(None, None, 0, None, ctypes.byref(nsink), None))
+    sink = torch.zeros(nsink.value, device="cuda", dtype=torch.float32)
+    L.check(lib.sana_hip_hbm_peak(src.data_ptr(), dst.data_ptr(), n * 4, sink.data_ptr(), None, stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src)
+    L.check(lib.sana_hip_hbm_peak(src.data_ptr(), None, n * 4, sink.data_ptr(), None, stream()))
+    torch.cuda.synchronize()
+    assert float(sink.double().sum()) == float(src.double().sum())
+    assert lib.sana_hip_hbm_peak(src.data_ptr(), None, n * 4 - 4, sink.data_ptr(), None, stream()) != 0
+    wg = 8
+    msink = torch.full((wg * 256,), float("nan"), device="cuda", dtype=torch.float32)
+    fl = ctypes.c_double()
+    for zero in (0, 1):
+        L.check(lib.sana_hip_mfma_peak(wg, 3, zero, msink.data_ptr(), stream(), ctypes.byref(fl)))
+        torch.cuda.synchronize()
+        assert fl.value == wg * 4 * 4 * 8 * 3 * 32768
+        assert torch.isfinite(msink).all()
+        if zero:
+            assert (msink == 0).all()
+        else:
+            assert (msink != 0).any()
