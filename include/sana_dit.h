@@ -275,6 +275,17 @@ int sana_hip_ln_modulate(const float * x, int64_t ldx, void * out16, int64_t ldo
 int sana_hip_linear_attention(const void * q, const void * k, const void * v, int64_t ld, void * out, int64_t ldo,
                               int64_t B, int64_t N, int64_t H, int64_t D, float * workspace, void * stream);
 size_t sana_hip_linear_attention_workspace(int64_t B, int64_t N, int64_t H, int64_t D);
+/* sana_hip_linear_attention without allocation or workspace argument.  No
+ * counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The workspace is a static 16 MiB device array, one per GPU, kept
+ * until the process ends; calls whose sana_hip_linear_attention_workspace size
+ * exceeds it fail with SANA_ERR_INVALID_ARGUMENT (B=2, H=16, D=72 needs 11.7 MB
+ * at any N).  Every call on a GPU shares that GPU's array: calls that overlap
+ * on one GPU (two streams, two threads) race.  Runs on the current device; the
+ * stream must belong to it.  Results equal sana_hip_linear_attention's. */
+int sana_hip_linear_attention_noalloc(const void * q, const void * k, const void * v, int64_t ld, void * out,
+                                      int64_t ldo, int64_t B, int64_t N, int64_t H, int64_t D, void * stream);
 int sana_hip_cross_attention(const void * q, int64_t ldq, const void * k, int64_t ldk, const void * vt,
                              int64_t ldvt, const float * bias, void * out, int64_t ldo, int64_t B, int64_t N,
                              int64_t L, int64_t H, int64_t D, void * stream);

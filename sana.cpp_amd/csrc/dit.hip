@@ -23,6 +23,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -560,6 +561,34 @@ struct BlockSuffix {
     int kind;
 };
 
+}  // namespace
+
+// Scratch of sana_hip_linear_attention_noalloc: the chunk partial states, the
+// fp16 hi/lo state pair and the partial maxima of the three-kernel linear
+// attention (what the allocating entry point takes as its workspace).  Each GPU
+// the library runs on holds its own copy of the array until the process ends.
+// The kernels overwrite every element they later read, so nothing is cleared.
+constexpr size_t kLaScratchFloats = (size_t)4 << 20;  // 16 MiB
+static __device__ __align__(256) float scratch[kLaScratchFloats];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex scratch_mu;
+float * scratch_addr[kScratchDevices] = {};
+
+// Device address of `scratch` on the current device `dev`, looked up on the
+// first call for that device (the array's name is only a host-side stand-in).
+float * device_scratch(int dev) {
+    if (dev < 0 || dev >= kScratchDevices) throw_err(SANA_ERR_INVALID_ARGUMENT, "scratch: device index out of range");
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_addr[dev]) {
+        void * p = nullptr;
+        hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (!p) throw_err(SANA_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+        scratch_addr[dev] = static_cast<float *>(p);
+    }
+    return scratch_addr[dev];
+}
 }  // namespace
 
 extern "C" {
@@ -1266,6 +1295,28 @@ int sana_hip_linear_attention(const void * q, const void * k, const void * v, in
                                             static_cast<const half_t *>(v), ld, static_cast<half_t *>(out), ldo,
                                             (int)B, (int)N, (int)H, (int)D, ws, static_cast<hipStream_t>(stream)),
                      "linear_attention");
+    });
+}
+
+int sana_hip_linear_attention_noalloc(const void * q, const void * k, const void * v, int64_t ld, void * out,
+                                      int64_t ldo, int64_t B, int64_t N, int64_t H, int64_t D, void * stream) {
+    return guarded([&] {
+        if (B <= 0 || N <= 0 || H <= 0 || D <= 0 || D > 112 || B > 65535 || H > 65535 || N > (1 << 30))
+            throw_err(SANA_ERR_INVALID_ARGUMENT, "linear_attention_noalloc: B, H in [1, 65535], N in [1, 2^30], "
+                                                 "D in [1, 112]");
+        const size_t need = sana::linattn_workspace_floats((int)B, (int)N, (int)H, (int)D);
+        if (need > kLaScratchFloats)
+            throw_err(SANA_ERR_INVALID_ARGUMENT,
+                      "linear_attention_noalloc: needs " + std::to_string(need * sizeof(float)) +
+                          " bytes of scratch, above the static " + std::to_string(kLaScratchFloats * sizeof(float)) +
+                          " (use sana_hip_linear_attention with a workspace)");
+        int dev = 0;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        float * ws = device_scratch(dev);
+        launch_check(sana::linear_attention(static_cast<const half_t *>(q), static_cast<const half_t *>(k),
+                                            static_cast<const half_t *>(v), ld, static_cast<half_t *>(out), ldo,
+                                            (int)B, (int)N, (int)H, (int)D, ws, static_cast<hipStream_t>(stream)),
+                     "linear_attention_noalloc");
     });
 }
 

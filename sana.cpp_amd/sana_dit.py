@@ -85,6 +85,7 @@ PROTOTYPES = {
     "sana_hip_ln_modulate": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _vp,
                                             _vp, _i64, _i64, _i64, _vp]),
     "sana_hip_linear_attention": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "sana_hip_linear_attention_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
     "sana_hip_linear_attention_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
     "sana_hip_cross_attention": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
                                                 _i64, _i64, _vp]),
