@@ -118,6 +118,8 @@ struct sana_dit {
     std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, const void *, const void *, const void *, const void *>,
              GraphEntry>
         graphs;
+    // whole denoise loops, keyed by shape, buffers and schedule (a few kept)
+    std::map<std::string, GraphEntry> loop_graphs;
     int64_t last_M = 0, last_B = 0, last_N = 0;
     int64_t loop_steps = 0, loop_n = 0;  // shape of the last denoise loop (its converted outputs stay in loop_x0)
     // Execution switches, read from the environment once by sana_dit_create:
@@ -127,6 +129,8 @@ struct sana_dit {
 
     ~sana_dit() {
         for (auto & kv : graphs)
+            if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+        for (auto & kv : loop_graphs)
             if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
         if (ev_fork) (void)hipEventDestroy(ev_fork);
         if (ev_join) (void)hipEventDestroy(ev_join);
@@ -138,10 +142,17 @@ struct sana_dit {
 
 namespace {
 
+void drop_loop_graphs(sana_dit * c) {
+    for (auto & kv : c->loop_graphs)
+        if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+    c->loop_graphs.clear();
+}
+
 void drop_graphs(sana_dit * c) {
     for (auto & kv : c->graphs)
         if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
     c->graphs.clear();
+    drop_loop_graphs(c);
 }
 
 // Host fp32 -> device fp16 [rows, ld] with zero padding; src is [rows, cols]
@@ -524,6 +535,31 @@ void set_t(sana_dit * c, int64_t B, float t, hipStream_t s) {
 }
 
 
+// Capture `body` on the context stream into an executable graph.
+template <class Body>
+hipGraphExec_t capture_graph(sana_dit * c, Body body) {
+    hipGraph_t g = nullptr;
+    hip_check(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    try {
+        body(c->stream);
+    } catch (...) {
+        (void)hipStreamEndCapture(c->stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    hip_check(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    hipError_t r = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    hip_check(r, "hipGraphInstantiate");
+    return exec;
+}
+
+template <class T>
+void key_append(std::string & k, const T & v) {
+    k.append(reinterpret_cast<const char *>(&v), sizeof(T));
+}
+
 // Run `body` on stream s through a cached HIP graph (captured on the context
 // stream on first use for this key).
 template <class Body>
@@ -537,20 +573,8 @@ void run_graph(sana_dit * c,
     }
     auto it = c->graphs.find(key);
     if (it == c->graphs.end()) {
-        hipGraph_t g = nullptr;
-        hip_check(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-        try {
-            body(c->stream);
-        } catch (...) {
-            (void)hipStreamEndCapture(c->stream, &g);
-            if (g) (void)hipGraphDestroy(g);
-            throw;
-        }
-        hip_check(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
         GraphEntry e;
-        hipError_t r = hipGraphInstantiate(&e.exec, g, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(g);
-        hip_check(r, "hipGraphInstantiate");
+        e.exec = capture_graph(c, body);
         it = c->graphs.emplace(key, e).first;
     }
     hip_check(hipGraphLaunch(it->second.exec, s), "hipGraphLaunch");
@@ -1003,37 +1027,69 @@ float flow_lambda(float sigma) {  // log(alpha) - log(sigma) with alpha = 1 - si
 
 // The whole loop on `s`: step i runs the forward at timesteps[i] on latent
 // buffer i % 2 and writes buffer (i + 1) % 2; the converted outputs of the two
-// latest steps alternate in loop_x0.  Returns the buffer holding the result.
+// latest steps alternate in loop_x0.  With graphs on, the whole loop (latent
+// copy, and per step the timestep fill, the forward and the CFG + solver
+// update) is one graph, captured once per shape, buffers and schedule.
+// Returns the buffer holding the result.
 float * enqueue_loop(sana_dit * c, const float * d_latent, int64_t Bl, int64_t Hh, int64_t Ww, const float * ts,
                      const float * sg, int64_t steps, float guidance, hipStream_t s) {
     const int64_t n = Bl * c->Cl * Hh * Ww;
+    const int64_t B = 2 * Bl, N = Hh * Ww;
     for (int k = 0; k < 2; ++k) {
         c->loop_lat[k].ensure((size_t)n * 4, false);
         c->loop_x0[k].ensure((size_t)n * 4, false);
     }
-    hip_check(hipMemcpyAsync(c->loop_lat[0].p, d_latent, (size_t)n * 4, hipMemcpyDeviceToDevice, s), "latent");
-    for (int64_t i = 0; i < steps; ++i) {
-        float * cur = c->loop_lat[i & 1].as<float>();
-        float * nxt = c->loop_lat[(i + 1) & 1].as<float>();
-        int r = sana_dit_forward_device(c, cur, Bl, Hh, Ww, ts[i], c->np_out.as<float>(), s);
-        if (r != SANA_OK) throw_err(r, g_last_error);
-        // step_sana_scheduler (src/scheduler.cpp:272-318) with solver_order 2, midpoint,
-        // lower_order_final: first order at the first and at the last step.
-        const bool first = i == 0 || i == steps - 1;
-        const float st_v = sg[i + 1], s0_v = sg[i];
-        const float alpha_t = 1.0f - st_v;
-        const float h = flow_lambda(st_v) - flow_lambda(s0_v);
-        const float ca = st_v / s0_v, cb = -alpha_t * (std::exp(-h) - 1.0f);
-        float cc = 0.0f, inv_r0 = 0.0f;
-        if (!first) {
-            const float h0 = flow_lambda(s0_v) - flow_lambda(sg[i - 1]);
-            inv_r0 = 1.0f / (h0 / h);
-            cc = -0.5f * alpha_t * (std::exp(-h) - 1.0f);
+    c->last_M = B * N;
+    c->last_B = B;
+    c->last_N = N;
+    const float * xbias = c->ctx_bias ? c->bias.as<float>() : nullptr;
+    auto body = [&](hipStream_t gs) {
+        hip_check(hipMemcpyAsync(c->loop_lat[0].p, d_latent, (size_t)n * 4, hipMemcpyDeviceToDevice, gs), "latent");
+        for (int64_t i = 0; i < steps; ++i) {
+            float * cur = c->loop_lat[i & 1].as<float>();
+            float * nxt = c->loop_lat[(i + 1) & 1].as<float>();
+            set_t(c, B, ts[i], gs);
+            enqueue_forward(c, cur, Bl, Hh, Ww, xbias, c->np_out.as<float>(), gs);
+            // step_sana_scheduler (src/scheduler.cpp:272-318) with solver_order 2, midpoint,
+            // lower_order_final: first order at the first and at the last step.
+            const bool first = i == 0 || i == steps - 1;
+            const float st_v = sg[i + 1], s0_v = sg[i];
+            const float alpha_t = 1.0f - st_v;
+            const float h = flow_lambda(st_v) - flow_lambda(s0_v);
+            const float ca = st_v / s0_v, cb = -alpha_t * (std::exp(-h) - 1.0f);
+            float cc = 0.0f, inv_r0 = 0.0f;
+            if (!first) {
+                const float h0 = flow_lambda(s0_v) - flow_lambda(sg[i - 1]);
+                inv_r0 = 1.0f / (h0 / h);
+                cc = -0.5f * alpha_t * (std::exp(-h) - 1.0f);
+            }
+            hipLaunchKernelGGL(cfg_dpm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, gs,
+                               c->np_out.as<float>(), cur, c->loop_x0[(i + 1) & 1].as<float>(), nxt,
+                               c->loop_x0[i & 1].as<float>(), (int)n, guidance, s0_v, ca, cb, cc, inv_r0,
+                               first ? 0 : 1);
+            hip_check(hipGetLastError(), "cfg_dpm");
         }
-        hipLaunchKernelGGL(cfg_dpm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, c->np_out.as<float>(),
-                           cur, c->loop_x0[(i + 1) & 1].as<float>(), nxt, c->loop_x0[i & 1].as<float>(), (int)n,
-                           guidance, s0_v, ca, cb, cc, inv_r0, first ? 0 : 1);
-        hip_check(hipGetLastError(), "cfg_dpm");
+    };
+    if (!c->use_graphs) {
+        body(s);
+    } else {
+        std::string key;
+        for (int64_t v : {Bl, Hh, Ww, c->ctx_L, (int64_t)c->ctx_bias, steps}) key_append(key, v);
+        for (const void * p : {(const void *)d_latent, (const void *)c->loop_lat[0].p, (const void *)c->loop_lat[1].p,
+                               (const void *)c->loop_x0[0].p, (const void *)c->loop_x0[1].p,
+                               (const void *)c->np_out.p})
+            key_append(key, p);
+        key_append(key, guidance);
+        for (int64_t i = 0; i < steps; ++i) key_append(key, ts[i]);
+        for (int64_t i = 0; i <= steps; ++i) key_append(key, sg[i]);
+        auto it = c->loop_graphs.find(key);
+        if (it == c->loop_graphs.end()) {
+            if (c->loop_graphs.size() >= 4) drop_loop_graphs(c);
+            GraphEntry e;
+            e.exec = capture_graph(c, body);
+            it = c->loop_graphs.emplace(key, e).first;
+        }
+        hip_check(hipGraphLaunch(it->second.exec, s), "hipGraphLaunch");
     }
     hip_check(hipEventRecord(c->ev_loop, s), "hipEventRecord");
     c->loop_steps = steps;

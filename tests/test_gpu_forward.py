@@ -223,3 +223,35 @@ def test_small_forward_one_chain_no_graph_vs_oracle(monkeypatch):
         assert np.array_equal(got, again)
     finally:
         d.close()
+
+
+def test_small_loop_graph_replays_match_direct_launches(small_model, monkeypatch):
+    """The denoise loop as one cached graph: replayed with a forward and a loop
+    of another schedule between the replays, every result equals the loop
+    launched kernel by kernel (SANA_DIT_NO_GRAPH=1, read at context creation)."""
+    import sana_dit
+    m, d = small_model
+    latent = O.randn((1, 8, 8, 8), 21)
+    caption = O.randn((2, 16, 96), 22)
+    ts6, sg6 = O.scheduler_timesteps(6)
+    ts4, sg4 = O.scheduler_timesteps(4)
+    d.set_context(caption, projected=False)
+    first = d.denoise_loop(latent, ts6, sg6, 4.5)
+    d.forward(O.randn((1, 8, 8, 8), 23), 500.0)
+    other = d.denoise_loop(latent, ts4, sg4, 4.5)
+    replays = [d.denoise_loop(latent, ts6, sg6, 4.5) for _ in range(2)]
+    monkeypatch.setenv("SANA_DIT_NO_GRAPH", "1")
+    e = sana_dit.Dit(layers=2, hidden=128, ffn=256, caption_dim=96, latent_channels=8, self_heads=4, cross_heads=2)
+    try:
+        for name, shape in sana_dit.manifest(2, 128, 256, 96, 8).items():
+            e.set_weight(name, m.get(name, shape))
+        e.set_context(caption, projected=False)
+        direct6 = e.denoise_loop(latent, ts6, sg6, 4.5)
+        direct4 = e.denoise_loop(latent, ts4, sg4, 4.5)
+    finally:
+        e.close()
+    assert np.isfinite(direct6).all() and np.isfinite(direct4).all()
+    assert np.array_equal(first, direct6)
+    assert np.array_equal(other, direct4)
+    for r in replays:
+        assert np.array_equal(r, direct6)
