@@ -615,9 +615,14 @@ __global__ __launch_bounds__(256) void xattn_kernel(const f16 * __restrict__ q, 
 // produces the softmax denominator sum_k p_k.  The two key halves' (max, O^T) are merged
 // through LDS: O = O_0 2^(m_0 - m) + O_1 2^(m_1 - m), m = max(m_0, m_1).
 //
-// Staging issues every 16-byte load before the first use, with a
-// power-of-two thread -> (row, chunk) map; chunks outside the head are
-// written as zeros instead of loaded, so no load waits behind a branch.
+// Staging issues every 16-byte load (Q, K, V^T) up front, unconditionally and
+// in bounds (clamped rows and chunks, masked afterwards with dword ANDs), with
+// a power-of-two thread -> (row, chunk) map.  Measured slower: writing V^T to
+// LDS only after the softmax (+0.5 us), and a dense map that loads only the
+// head's own chunks with every lane busy (+0.5 us, though 40 % fewer bytes).
+// Without a key bias and with the ones row, the softmax takes the max
+// of the raw scores and needs no bias add: keys past L repeat key L - 1 and
+// meet zeroed V^T columns and ones-row entries.
 constexpr int kXaQ = 128;  // queries per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -664,48 +669,59 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         const int d0 = ks * 16 + 8 * hh;
-        const f16x8 v = *reinterpret_cast<const f16x8 *>(qr + (d0 < D ? d0 : 0));
+        const f16x8 v = *reinterpret_cast<const f16x8 *>(qr + min(d0, D - 8));
+        uint32_t w[4];
+        __builtin_memcpy(w, &v, 16);
+        const uint32_t m = d0 < D ? 0xffffffffu : 0u;  // dims past D are zero
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qf[ks][e] = d0 < D ? v[e] : (f16)0.0f;
+        for (int e = 0; e < 4; ++e) w[e] &= m;
+        __builtin_memcpy(&qf[ks], w, 16);
     }
 
-    // K staging: thread -> chunk kc = tid & 15 (8 dims), rows kr0 + 32 j.  Chunks
-    // past D and rows past L are written as zeros; lanes load only what exists.
+    // K staging: thread -> chunk kc = tid & 15 (8 dims), rows kr0 + 32 j.  Every
+    // load is in bounds and unconditional: rows past L repeat row L - 1 and
+    // chunks past D repeat the head's last chunk, so every staged value is real
+    // (finite) data.  A repeated key scores like key L - 1 (the max is
+    // unchanged) and its V^T column and ones-row entries are staged as zeros,
+    // so it adds nothing to O or to the denominator; dims past D meet zero
+    // query dims.
     const int kc = tid & 15, kr0 = tid >> 4;
     const bool kc_live = kc < KS * 2;  // chunks 0 .. 2 KS - 1 are staged
-    const bool kc_data = kc * 8 < D;
-    const f16 * kp = k + ((int64_t)b * L + kr0) * ldk + (int64_t)h * D + kc * 8;
+    const f16 * kp = k + (int64_t)b * L * ldk + (int64_t)h * D + min(kc, (D - 1) >> 3) * 8;
     f16x8 kreg[LT];
-    if (kc_data) {
 #pragma unroll
-        for (int j = 0; j < LT; ++j)
-            if (kr0 + 32 * j < L) kreg[j] = *reinterpret_cast<const f16x8 *>(kp + (int64_t)(32 * j) * ldk);
-    }
+    for (int j = 0; j < LT; ++j)
+        kreg[j] = *reinterpret_cast<const f16x8 *>(kp + (int64_t)min(kr0 + 32 * j, L - 1) * ldk);
     // V^T staging: thread -> 8-key chunk vc = tid & 63, dims vd0 + 8 j (vd0 = the
-    // wave index, so the dim of a step is uniform over the wave)
+    // wave index).  Chunks past L repeat the last chunk and dims past D repeat
+    // dim D - 1 (output dims past D are never stored); keys past L are then
+    // zeroed with per-dword masks.
     constexpr int VJ = DP / 8;
-    const int vc = tid & 63, vd0 = tid >> 6;
+    const int vc = tid & 63;
+    const int vd0 = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool vc_live = vc < LP / 8;
-    const int vkeys = min(max(L - vc * 8, 0), 8);  // keys of this chunk below L
-    const f16 * vp = vt + ((int64_t)b * H * D + (int64_t)h * D + vd0) * ldvt + vc * 8;
+    const f16 * vp = vt + ((int64_t)b * H * D + (int64_t)h * D) * ldvt + min(vc, (L - 1) >> 3) * 8;
     f16x8 vreg[VJ];
-    if (vkeys > 0) {
 #pragma unroll
-        for (int j = 0; j < VJ; ++j)
-            if (vd0 + 8 * j < D) vreg[j] = *reinterpret_cast<const f16x8 *>(vp + (int64_t)(8 * j) * ldvt);
+    for (int j = 0; j < VJ; ++j)
+        vreg[j] = *reinterpret_cast<const f16x8 *>(vp + (int64_t)min(vd0 + 8 * j, D - 1) * ldvt);
+    uint32_t km[4];  // keys 8 vc + 2 e and 8 vc + 2 e + 1 below L
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int k0 = vc * 8 + 2 * e;
+        km[e] = k0 + 1 < L ? 0xffffffffu : (k0 < L ? 0x0000ffffu : 0u);
     }
-    for (int key = tid; key < LP; key += 512)
-        bs[key] = key < L ? (bias ? bias[(int64_t)b * L + key] * kLog2e : 0.0f) : -INFINITY;
-    const f16x8 zero8 = {(f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f};
+    // log2-scaled key bias; keys past L repeat key L - 1's, or are -inf where no
+    // ones row masks the denominator (D a multiple of 32)
+    for (int key = tid; key < LP; key += 512) {
+        const int kb = min(key, L - 1);
+        const float bv = bias ? bias[(int64_t)b * L + kb] * kLog2e : 0.0f;
+        bs[key] = (ONES || key < L) ? bv : -INFINITY;
+    }
     if (kc_live) {
 #pragma unroll
-        for (int j = 0; j < LT; ++j) {
-            f16 * dst = Ks + (kr0 + 32 * j) * KROW + kc * 8;
-            if (kc_data && kr0 + 32 * j < L)
-                *reinterpret_cast<f16x8 *>(dst) = kreg[j];
-            else
-                *reinterpret_cast<f16x8 *>(dst) = zero8;
-        }
+        for (int j = 0; j < LT; ++j)
+            *reinterpret_cast<f16x8 *>(Ks + (kr0 + 32 * j) * KROW + kc * 8) = kreg[j];
     }
     if (vc_live) {
         // keys 8 vc .. 8 vc + 7: the first four go to positions 16 (vc >> 1) + 4 (vc & 1),
@@ -714,26 +730,16 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
 #pragma unroll
         for (int j = 0; j < VJ; ++j) {
             const int d = vd0 + 8 * j;
-            f16x8 v = zero8;
-            if (d < D) {
-                if (vkeys == 8) {
-                    v = vreg[j];
-                } else if (vkeys > 0) {
+            uint32_t w[4];
+            __builtin_memcpy(w, &vreg[j], 16);
+            if (ONES && j == VJ - 1 && vd0 == 7) {  // d == DP - 1: the ones row
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = e < vkeys ? vreg[j][e] : (f16)0.0f;
-                }
-            } else if (d == DP - 1 && ones_row) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = e < vkeys ? (f16)1.0f : (f16)0.0f;
+                for (int e = 0; e < 4; ++e) w[e] = 0x3c003c00u;
             }
-            f16x4 lo, hi;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                lo[e] = v[e];
-                hi[e] = v[4 + e];
-            }
-            *reinterpret_cast<f16x4 *>(Vs + d * VROW + pos) = lo;
-            *reinterpret_cast<f16x4 *>(Vs + d * VROW + pos + 8) = hi;
+            for (int e = 0; e < 4; ++e) w[e] &= km[e];
+            *reinterpret_cast<uint2 *>(Vs + d * VROW + pos) = make_uint2(w[0], w[1]);
+            *reinterpret_cast<uint2 *>(Vs + d * VROW + pos + 8) = make_uint2(w[2], w[3]);
         }
     }
     __syncthreads();
@@ -756,31 +762,44 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
     }
     const float scale2 = scale * kLog2e;
     float mx = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < LTH; ++t)
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-            const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bs + (tb + t) * 32 + 8 * i4 + 4 * hh);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float sv = st[t][4 * i4 + u] * scale2 + b4[u];
-                st[t][4 * i4 + u] = sv;
-                mx = fmaxf(mx, sv);
-            }
-        }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    // a half whose keys are all past L has mx = -inf: its probabilities are exp2(-inf) = 0
-    const float mref = mx == -INFINITY ? 0.0f : mx;
     f16x8 pf[LTH][2];
     float sum = 0.0f;
+    if (ONES && !bias) {
+        // no bias to add: the max of the raw scores, then 2^(s scale2 - max scale2)
 #pragma unroll
-    for (int t = 0; t < LTH; ++t)
+        for (int t = 0; t < LTH; ++t)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float e = __builtin_amdgcn_exp2f(st[t][i] - mref);
-            if constexpr (!ones_row) sum += e;
-            pf[t][i >> 3][i & 7] = (f16)e;
-        }
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[t][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale2;
+#pragma unroll
+        for (int t = 0; t < LTH; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) pf[t][i >> 3][i & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(st[t][i], scale2, -mx));
+    } else {
+#pragma unroll
+        for (int t = 0; t < LTH; ++t)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bs + (tb + t) * 32 + 8 * i4 + 4 * hh);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float sv = st[t][4 * i4 + u] * scale2 + b4[u];
+                    st[t][4 * i4 + u] = sv;
+                    mx = fmaxf(mx, sv);
+                }
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        // a half whose keys are all -inf has mx = -inf: its probabilities are exp2(-inf) = 0
+        const float mref = mx == -INFINITY ? 0.0f : mx;
+#pragma unroll
+        for (int t = 0; t < LTH; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float e = __builtin_amdgcn_exp2f(st[t][i] - mref);
+                if constexpr (!ones_row) sum += e;
+                pf[t][i >> 3][i & 7] = (f16)e;
+            }
+    }
 
     f32x16 o[DT];
 #pragma unroll

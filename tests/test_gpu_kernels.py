@@ -201,12 +201,12 @@ def test_linear_attention_negative_query_gives_zero(L):
     assert np.all(got[5, :D] == 0.0)
 
 
-def _xattn(L, q, k, v, H, bias):
+def _xattn(L, q, k, v, H, bias, pad=0.0):
     B, N, C = q.shape
     Lk = k.shape[1]
     D = C // H
     Lp = (Lk + 31) // 32 * 32
-    vt = np.zeros((B, C, Lp), np.float32)
+    vt = np.full((B, C, Lp), pad, np.float32)
     vt[:, :, :Lk] = np.transpose(v, (0, 2, 1))
     dq, dk, dvt = dev(q, torch.float16), dev(k, torch.float16), dev(vt, torch.float16)
     db = None if bias is None else dev(bias, torch.float32)
@@ -296,3 +296,23 @@ def test_peak_kernels_do_their_work(L):
             assert (msink == 0).all()
         else:
             assert (msink != 0).any()
+
+
+@pytest.mark.parametrize("Lk,masked", [(300, False), (300, True), (77, False)])
+def test_cross_attention_ignores_vt_padding(L, Lk, masked):
+    """V^T columns past the key count hold NaN: the kernel must not read them
+    into the result (keys past L get zero weight and zero values)."""
+    rng = np.random.default_rng(Lk + masked)
+    B, N, H, D = 2, 160, 16, 72
+    q = f16(rng.standard_normal((B, N, H * D)))
+    k = f16(rng.standard_normal((B, Lk, H * D)))
+    v = f16(rng.standard_normal((B, Lk, H * D)))
+    bias = None
+    if masked:
+        bias = np.full((B, Lk), -10000.0, np.float32)
+        bias[0, :7] = 0
+        bias[1, :Lk // 2] = 0
+    ref = O.attention(q, k, v, H, bias)
+    got = _xattn(L, q, k, v, H, bias, pad=np.nan)
+    assert np.isfinite(got).all()
+    assert rel_l2(got, ref) < 2e-3, rel_l2(got, ref)
