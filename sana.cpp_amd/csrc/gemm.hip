@@ -230,6 +230,56 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
             for (int j = 0; j < G::TN; ++j) acc[i][j] = mfma_32x32x16(af[buf][i], bf[buf][j], acc[i][j]);
     };
 
+    // Residual epilogue inputs (x rows and the gate), loaded before the main loop
+    // so their latency hides behind it: single-pass epilogues with at most two
+    // rows per thread (the 64 x 64 and 128 x 64 tiles), plain A.  The thread ->
+    // (8-column chunk, rows) map is the epilogue's.
+    constexpr int ECPR = BN / 8, ERSTEP = G::NT / ECPR, ERPT = (G::EPI_ROWS + ERSTEP - 1) / ERSTEP;
+    constexpr bool kPrefetch = MODE == kGemmResidual && CONV == 0 && G::EPI_ROWS == BM && ERPT <= 2;
+    float xpre[kPrefetch ? ERPT : 1][8], gpre[kPrefetch ? ERPT : 1][8];
+    if constexpr (kPrefetch) {
+        const int col = n0 + (tid % ECPR) * 8;
+        const int nc = min(8, p.N - col);
+        const bool act = nc > 0 && tid < ERSTEP * ECPR;
+#pragma unroll
+        for (int k = 0; k < ERPT; ++k) {
+            const int row = m0 + tid / ECPR + k * ERSTEP;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                xpre[k][e] = 0.0f;
+                gpre[k][e] = 1.0f;
+            }
+            if (!act || row >= p.M) continue;
+            const float * xr = p.out32 + (int64_t)row * p.ldo32 + col;
+            const float * ga = p.gate_a ? p.gate_a + (int64_t)(row / p.rows_per_batch) * p.gate_stride + col : nullptr;
+            if (p.vec && nc == 8) {
+                const float4 x0 = *reinterpret_cast<const float4 *>(xr);
+                const float4 x1 = *reinterpret_cast<const float4 *>(xr + 4);
+                xpre[k][0] = x0.x; xpre[k][1] = x0.y; xpre[k][2] = x0.z; xpre[k][3] = x0.w;
+                xpre[k][4] = x1.x; xpre[k][5] = x1.y; xpre[k][6] = x1.z; xpre[k][7] = x1.w;
+                if (ga) {
+                    const float4 g0 = *reinterpret_cast<const float4 *>(ga);
+                    const float4 g1 = *reinterpret_cast<const float4 *>(ga + 4);
+                    gpre[k][0] = g0.x; gpre[k][1] = g0.y; gpre[k][2] = g0.z; gpre[k][3] = g0.w;
+                    gpre[k][4] = g1.x; gpre[k][5] = g1.y; gpre[k][6] = g1.z; gpre[k][7] = g1.w;
+                    if (p.gate_t) {
+                        const float4 t0 = *reinterpret_cast<const float4 *>(p.gate_t + col);
+                        const float4 t1 = *reinterpret_cast<const float4 *>(p.gate_t + col + 4);
+                        gpre[k][0] += t0.x; gpre[k][1] += t0.y; gpre[k][2] += t0.z; gpre[k][3] += t0.w;
+                        gpre[k][4] += t1.x; gpre[k][5] += t1.y; gpre[k][6] += t1.z; gpre[k][7] += t1.w;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    if (e >= nc) continue;
+                    xpre[k][e] = xr[e];
+                    if (ga) gpre[k][e] = ga[e] + (p.gate_t ? p.gate_t[col + e] : 0.0f);
+                }
+            }
+        }
+    }
+
     const int KT = p.K / kBK;
 #pragma unroll
     for (int s = 0; s < STAGES; ++s)
@@ -468,6 +518,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                         const int row = m0 + pass * ER + rr;
 #pragma unroll
                         for (int e = 0; e < 8; ++e) xin[k][e] = 0.0f;
+                        if constexpr (kPrefetch) {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) xin[k][e] = xpre[k][e];
+                            continue;
+                        }
                         if (rr >= ER || row >= p.M) continue;
                         bool gathered = false;
                         if constexpr (CONV == 2) {
@@ -512,7 +567,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
                                       v1.x + bv[4], v1.y + bv[5], v1.z + bv[6], v1.w + bv[7]};
                         const int b = row / p.rows_per_batch;
                         float g[8];
-                        if (p.gate_a && vec8) {
+                        if constexpr (kPrefetch) {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) g[e] = gpre[k][e];
+                        } else if (p.gate_a && vec8) {
                             const float * ga = p.gate_a + (int64_t)b * p.gate_stride + col;
                             const float4 g0 = *reinterpret_cast<const float4 *>(ga);
                             const float4 g1 = *reinterpret_cast<const float4 *>(ga + 4);
