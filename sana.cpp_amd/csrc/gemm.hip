@@ -363,25 +363,35 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
     // ------------------------------------------------------------ epilogue
     if constexpr (MODE == kGemmVT) {
         // Lane owns column (lane & 31) of each 32x32 block and rows
-        // 8*(r/4) + 4*(lane/32) + r%4.
+        // 8*(r/4) + 4*(lane/32) + r%4.  The (batch, key) split of the column and
+        // the (block, channel) split of the block's first row are divided once;
+        // the 16 rows then step through the channel groups without dividing.
+        f16 * o16 = reinterpret_cast<f16 *>(p.out16);
 #pragma unroll
-        for (int i = 0; i < G::TM; ++i)
+        for (int j = 0; j < G::TN; ++j) {
+            const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
+            if (col >= p.N) continue;
+            const int b = col / p.vt_cols, jj = col - b * p.vt_cols;
 #pragma unroll
-            for (int j = 0; j < G::TN; ++j) {
-                const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
+            for (int i = 0; i < G::TM; ++i) {
+                const int rb = m0 + wm * G::WTM + i * 32 + 4 * (lane >> 5);
+                const int blk0 = rb / p.vt_rows, rr0 = rb - blk0 * p.vt_rows;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int row = m0 + wm * G::WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < p.M && col < p.N) {
-                        float v = acc[i][j][r];
-                        if (p.bias) v += p.bias[row];
-                        const int blk = row / p.vt_rows, rr = row - blk * p.vt_rows;
-                        const int b = col / p.vt_cols, jj = col - b * p.vt_cols;
-                        reinterpret_cast<f16 *>(p.out16)[((int64_t)(blk * p.vt_batch + b) * p.vt_rows + rr) * p.vt_ld +
-                                                         jj] = (f16)v;
+                    const int off = 8 * (r >> 2) + (r & 3);
+                    const int row = rb + off;
+                    if (row >= p.M) continue;
+                    int blk = blk0, rr = rr0 + off;
+                    while (rr >= p.vt_rows) {
+                        rr -= p.vt_rows;
+                        ++blk;
                     }
+                    float v = acc[i][j][r];
+                    if (p.bias) v += p.bias[row];
+                    o16[((int64_t)(blk * p.vt_batch + b) * p.vt_rows + rr) * p.vt_ld + jj] = (f16)v;
                 }
             }
+        }
         return;
     } else {
         float * ct = reinterpret_cast<float *>(smem);
