@@ -98,8 +98,17 @@ SANA_DEV void wait_stages(int keep) {
 // CONV: 0 plain A rows; 1 implicit 3x3 conv over a zero-bordered NHWC input;
 // 2 the same over the nearest-2x upsample of the input (GemmParams::conv).
 template <int BM, int BN, int WM, int WN, int STAGES, int MODE, int SCHED, int ACT, int CONV = 0>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
+__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
     using G = Cfg<BM, BN, WM, WN, STAGES>;
+    // product blockIdx.y of a batched launch (plain stores only)
+    GemmParams p = p_in;
+    if constexpr (MODE == kGemmStore && CONV == 0) {
+        const int z = blockIdx.y;
+        p.A += z * p.batch_a;
+        p.W += (z / p.batch_w_div) * p.batch_w;
+        if (p.out16) p.out16 += z * p.batch_o16;
+        if (p.out32) p.out32 += z * p.batch_o32;
+    }
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     // Workgroup -> tile: XCD x (= id % 8) takes a contiguous range of tiles in
@@ -645,7 +654,7 @@ hipError_t launch_mode(const GemmParams & p, int tiles, hipStream_t s) {
                                     ", " + std::to_string(MODE) + ", " + std::to_string(SCHED) + ", " +
                                     std::to_string(ACT) + ", " + std::to_string(CONV) + ">";
     note_kernel(name.c_str());
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT, CONV>), dim3(tiles), dim3(G::NT),
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, STAGES, MODE, SCHED, ACT, CONV>), dim3(tiles, p.batch), dim3(G::NT),
                        G::LDS_BYTES, s, p);
     return hipGetLastError();
 }
@@ -710,6 +719,10 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
          ((reinterpret_cast<uintptr_t>(p.kt16) | reinterpret_cast<uintptr_t>(p.vt16)) & 15)))
         return hipErrorInvalidValue;
     if (p.gate_a && p.rows_per_batch <= 0) return hipErrorInvalidValue;
+    if (p.batch < 1 || p.batch > 65535 || p.batch_w_div < 1 ||
+        (p.batch > 1 && (p.mode != kGemmStore || p.conv ||
+                         ((p.batch_a | p.batch_w | p.batch_o16 | p.batch_o32) & 7) != 0)))
+        return hipErrorInvalidValue;
     // 16-byte epilogue accesses need 8-element aligned rows and 16-byte aligned bases.
     bool vec = true;
     if (p.out16) vec = vec && p.ldo16 % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out16) & 15) == 0;
@@ -724,7 +737,7 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     }
     // Tile choice from sweeps on MI355X with cold weights (each GEMM's weights
     // come from HBM, as in the 28-block forward).  Every CU pulls at most
-    // ~55 GB/s from L2, so larger tiles (fewer operand bytes per flop) win as
+    // ~110 GB/s from L2, so larger tiles (fewer operand bytes per flop) win as
     // long as the grid still covers the 256 CUs:
     //  * grids of <= 160 128x128 tiles: shared with a concurrent launch (the
     //    two CFG branches), 64x64 tiles with three stages and early release;
@@ -733,8 +746,9 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     //  * plain stores whose N splits into 192-wide tiles with >= 256 tiles:
     //    128x192 with early stage release (two workgroups per CU);
     //  * otherwise 128x128 tiles with two stages, two workgroups per CU.
-    // (tile counts are scaled by the launches that share the CUs, p.co)
-    const int64_t co = std::max(p.co, 1);
+    // (tile counts are scaled by the launches that share the CUs, p.co, and
+    // by the products of a batched launch)
+    const int64_t co = std::max(p.co, 1) * (int64_t)p.batch;
     const int64_t tm128 = (p.M + 127) / 128;
     const int64_t t128 = tm128 * ((p.N + 127) / 128) * co;
     if (t128 <= 160) {

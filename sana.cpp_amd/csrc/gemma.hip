@@ -7,13 +7,14 @@
 //   a16  = rmsnorm(x) * attn_norm                        gemma_norm_kernel
 //   qkv  = a16 [Wq; Wk; Wv]^T                            one MFMA GEMM, fp32 out
 //   q16, k16 = rope(q) * query_scale, rope(k); V^T       gemma_qkv_kernel
-//   S_h  = q16_h k16_kv(h)^T                             one GEMM per head
+//   S_h  = q16_h k16_kv(h)^T                             all heads in one batched GEMM
 //   P_h  = softmax(causal / window mask, soft-cap)       gemma_softmax_kernel
-//   o16_h = P_h V_kv(h)                                  one GEMM per head (B = V^T)
-//   x   += rmsnorm(o16 Wo^T) * post_attention_norm       GEMM + gemma_norm_kernel
+//   o16_h = P_h V_kv(h)                                  all heads in one batched GEMM (B = V^T)
+//   x   += rmsnorm(o16 Wo^T) * post_attention_norm       split-K GEMM + gemma_norm_kernel
 //   a16  = rmsnorm(x) * ffn_norm
 //   gu   = a16 [Wgate; Wup]^T; g16 = gelu_tanh(gate) up  GEMM + gemma_geglu_kernel
-//   x   += rmsnorm(g16 Wdown^T) * post_ffw_norm
+//   x   += rmsnorm(g16 Wdown^T) * post_ffw_norm          split-K GEMM + gemma_norm_kernel
+// The layers of one encode run as one cached graph per token count.
 // out = rmsnorm(x) * output_norm.  Activations are token-major; GEMM operands
 // fp16 with fp32 accumulation; the residual stream, norms, softmax and RoPE
 // in fp32.  RMSNorm weights are taken as stored in the GGUF (1 + w).
@@ -48,29 +49,42 @@ __global__ void gemma_embed_kernel(const int32_t * __restrict__ tok, const f16 *
     x[i] = (float)emb[(int64_t)tok[t] * H + c] * scale;
 }
 
-// One wave per row of C (<= 256 * NC4) channels: v = y / sqrt(mean(y^2) + eps) * w.
-// mode 0: out16 = fp16(v); 1: x += v (post-norm residual, out32 = x); 2: out32 = v.
+// One workgroup of 256 threads per row of C (<= 1024 * NC4) channels:
+// v = y / sqrt(mean(y^2) + eps) * w, y the fixed-order sum of `parts` split-K
+// partials part_stride floats apart; the sum of squares is reduced over the
+// four waves through LDS.  mode 0: out16 = fp16(v); 1: x += v (post-norm
+// residual, out32 = x); 2: out32 = v.
 template <int NC4>
-__global__ __launch_bounds__(256) void gemma_norm_kernel(const float * __restrict__ y, int C, int M,
+__global__ __launch_bounds__(256) void gemma_norm_kernel(const float * __restrict__ y, int parts,
+                                                         int64_t part_stride, int C, int M,
                                                          const float * __restrict__ w, float eps, int mode,
                                                          f16 * __restrict__ out16, float * __restrict__ out32) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= M) return;
+    __shared__ float wsum[4];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int n4 = C >> 2;
     const float4 * yr = reinterpret_cast<const float4 *>(y + (int64_t)row * C);
     float4 v[NC4];
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NC4; ++i) {
-        const int c4 = lane + 64 * i;
+        const int c4 = tid + 256 * i;
         v[i] = c4 < n4 ? yr[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int z = 1; z < parts; ++z) {
+            if (c4 >= n4) break;
+            const float4 u = reinterpret_cast<const float4 *>(y + z * part_stride + (int64_t)row * C)[c4];
+            v[i] = make_float4(v[i].x + u.x, v[i].y + u.y, v[i].z + u.z, v[i].w + u.w);
+        }
         ss += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
     }
-    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)C + eps);
+    ss = wave_sum(ss);
+    if (lane == 0) wsum[tid >> 6] = ss;
+    __syncthreads();
+    const float tot = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    const float inv = 1.0f / sqrtf(tot / (float)C + eps);
 #pragma unroll
     for (int i = 0; i < NC4; ++i) {
-        const int c4 = lane + 64 * i;
+        const int c4 = tid + 256 * i;
         if (c4 >= n4) continue;
         const float4 g = reinterpret_cast<const float4 *>(w)[c4];
         float o[4] = {v[i].x * inv * g.x, v[i].y * inv * g.y, v[i].z * inv * g.z, v[i].w * inv * g.w};
@@ -178,12 +192,21 @@ struct sana_gemma {
     // workspace
     int64_t ws_T = 0;
     DevMem tok, x32, y32, a16, qkv32, q16, k16, vt16, s32, p16, o16, gu32, g16, out32;
+    // the encoder's kernels as one graph per token count (workspace and weight
+    // pointers are baked in: dropped when either is reallocated)
+    std::map<int64_t, hipGraphExec_t> graphs;
     ~sana_gemma() {
+        for (auto & kv : graphs) (void)hipGraphExecDestroy(kv.second);
         if (stream) (void)hipStreamDestroy(stream);
     }
 };
 
 namespace {
+
+void drop_graphs(sana_gemma * g) {
+    for (auto & kv : g->graphs) (void)hipGraphExecDestroy(kv.second);
+    g->graphs.clear();
+}
 
 void upload_bytes(DevMem & d, const void * src, size_t bytes) {
     d.ensure(bytes, false);
@@ -218,6 +241,7 @@ std::vector<std::string> required_names(const sana_gemma * g) {
 }
 
 void set_weight(sana_gemma * g, const std::string & n, const float * d, const int64_t * sh, int nd) {
+    drop_graphs(g);
     const sana_gemma_config & c = g->cfg;
     const int64_t H = c.hidden, F = c.ffn, Dq = g->Dq, Dkv = g->Dkv;
     if (n == "token_embd.weight") {
@@ -278,11 +302,12 @@ void check_ready(const sana_gemma * g) {
 
 void ensure_workspace(sana_gemma * g, int64_t T) {
     if (T <= g->ws_T) return;
+    drop_graphs(g);
     const sana_gemma_config & c = g->cfg;
     const int64_t H = c.hidden, Tp = round_up(T, 64);
     g->tok.ensure((size_t)T * 4, false);
     g->x32.ensure((size_t)T * H * 4, false);
-    g->y32.ensure((size_t)T * H * 4, false);
+    g->y32.ensure((size_t)T * H * 4 * 2, false);  // two split-K partials
     g->a16.ensure((size_t)T * H * 2, false);
     g->qkv32.ensure((size_t)T * (g->Dq + 2 * g->Dkv) * 4, false);
     g->q16.ensure((size_t)T * g->Dq * 2, false);
@@ -314,20 +339,55 @@ void gemm(const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t 
     launch_check(sana::gemm(p, s), "gemma gemm");
 }
 
+// `batch` products in one launch: product z reads A + z * sa and W + (z / wdiv) * sw,
+// writes o16 + z * so16 / o32 + z * so32.
+void gemm_batched(const half_t * A, int64_t lda, int64_t sa, const half_t * W, int64_t ldw, int64_t sw, int wdiv,
+                  int64_t M, int64_t N, int64_t K, half_t * o16, int64_t ldo16, int64_t so16, float * o32,
+                  int64_t ldo32, int64_t so32, int batch, hipStream_t s) {
+    sana::GemmParams p;
+    p.A = A;
+    p.lda = lda;
+    p.W = W;
+    p.ldw = ldw;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.out16 = o16;
+    p.ldo16 = ldo16;
+    p.out32 = o32;
+    p.ldo32 = ldo32;
+    p.batch = batch;
+    p.batch_w_div = wdiv;
+    p.batch_a = sa;
+    p.batch_w = sw;
+    p.batch_o16 = so16;
+    p.batch_o32 = so32;
+    launch_check(sana::gemm(p, s), "gemma batched gemm");
+}
+
 void norm(const sana_gemma * g, const float * y, int64_t M, const DevMem & w, int mode, half_t * o16, float * o32,
-          hipStream_t s) {
+          hipStream_t s, int parts = 1) {
     const int64_t C = g->cfg.hidden;
-    const dim3 grid((unsigned)((M + 3) / 4)), blk(256);
+    const dim3 grid((unsigned)M), blk(256);
     f16 * h = reinterpret_cast<f16 *>(o16);
     const float eps = g->cfg.rms_eps;
-#define SANA_GEMMA_NORM(n4) \
-    hipLaunchKernelGGL((gemma_norm_kernel<n4>), grid, blk, 0, s, y, (int)C, (int)M, w.as<float>(), eps, mode, h, o32)
-    if (C <= 1024) SANA_GEMMA_NORM(4);
-    else if (C <= 2048) SANA_GEMMA_NORM(8);
-    else SANA_GEMMA_NORM(16);
+    const int64_t pstride = M * C;
+#define SANA_GEMMA_NORM(n4)                                                                                      \
+    hipLaunchKernelGGL((gemma_norm_kernel<n4>), grid, blk, 0, s, y, parts, pstride, (int)C, (int)M, w.as<float>(), \
+                       eps, mode, h, o32)
+    if (C <= 1024) SANA_GEMMA_NORM(1);
+    else if (C <= 2048) SANA_GEMMA_NORM(2);
+    else SANA_GEMMA_NORM(4);
 #undef SANA_GEMMA_NORM
     launch_check(hipGetLastError(), "gemma norm");
 }
+
+// Split-K factor of a T x H output with contraction K: the down and output
+// projections have long K and only T/64 x H/64 tiles, so their K is cut in
+// two halves (each a multiple of 64 and at least 512 deep) whose fp32
+// partials the following norm kernel sums in fixed order (measured on the
+// 2B shapes with 438 + 300 tokens: 14.3 ms unsplit, 10.7 ms in two, 10.9 ms in four).
+int split_k(int64_t K) { return K % 128 == 0 && K / 2 >= 512 ? 2 : 1; }
 
 // decode_embeddings (src/gemma_encoder.cpp:95-152) on device token ids.
 void encode(sana_gemma * g, int64_t T, hipStream_t s) {
@@ -349,25 +409,28 @@ void encode(sana_gemma * g, int64_t T, hipStream_t s) {
                                g->k16.as<f16>(), g->vt16.as<f16>());
             launch_check(hipGetLastError(), "gemma qkv");
         }
-        for (int64_t h = 0; h < nh; ++h)
-            gemm(g->q16.as<half_t>() + h * d, Dq, g->k16.as<half_t>() + (h / grp) * d, Dkv, T, T, d, nullptr, 0,
-                 g->s32.as<float>() + h * T * Tp, Tp, s);
+        // scores of all heads in one launch: head h uses K head h / grp
+        gemm_batched(g->q16.as<half_t>(), Dq, d, g->k16.as<half_t>(), Dkv, d, (int)grp, T, T, d, nullptr, 0, 0,
+                     g->s32.as<float>(), Tp, T * Tp, (int)nh, s);
         const int window = (c.sliding_window > 0 && l % 2 == 0) ? (int)c.sliding_window : 0;
         hipLaunchKernelGGL(gemma_softmax_kernel, dim3((unsigned)((nh * T + 3) / 4)), dim3(256), 0, s,
                            g->s32.as<float>(), g->p16.as<f16>(), (int)nh, (int)T, (int)Tp, c.attn_softcap, window);
         launch_check(hipGetLastError(), "gemma softmax");
-        for (int64_t h = 0; h < nh; ++h)
-            gemm(g->p16.as<half_t>() + h * T * Tp, Tp, g->vt16.as<half_t>() + (h / grp) * d * Tp, Tp, T, d, Tp,
-                 g->o16.as<half_t>() + h * d, Dq, nullptr, 0, s);
-        gemm(g->o16.as<half_t>(), Dq, L.wo.as<half_t>(), Dq, T, H, Dq, nullptr, 0, g->y32.as<float>(), H, s);
-        norm(g, g->y32.as<float>(), T, L.n_post_attn, 1, nullptr, g->x32.as<float>(), s);
+        gemm_batched(g->p16.as<half_t>(), Tp, T * Tp, g->vt16.as<half_t>(), Tp, d * Tp, (int)grp, T, d, Tp,
+                     g->o16.as<half_t>(), Dq, d, nullptr, 0, 0, (int)nh, s);
+        const int so = split_k(Dq);
+        gemm_batched(g->o16.as<half_t>(), Dq, Dq / so, L.wo.as<half_t>(), Dq, Dq / so, 1, T, H, Dq / so, nullptr, 0,
+                     0, g->y32.as<float>(), H, T * H, so, s);
+        norm(g, g->y32.as<float>(), T, L.n_post_attn, 1, nullptr, g->x32.as<float>(), s, so);
         norm(g, g->x32.as<float>(), T, L.n_ffn, 0, a16, nullptr, s);
         gemm(a16, H, L.wgu.as<half_t>(), H, T, 2 * F, H, nullptr, 0, g->gu32.as<float>(), 2 * F, s);
         hipLaunchKernelGGL(gemma_geglu_kernel, dim3(blocks_for(T * F)), dim3(256), 0, s, g->gu32.as<float>(), (int)T,
                            (int)F, g->g16.as<f16>());
         launch_check(hipGetLastError(), "gemma geglu");
-        gemm(g->g16.as<half_t>(), F, L.wdown.as<half_t>(), F, T, H, F, nullptr, 0, g->y32.as<float>(), H, s);
-        norm(g, g->y32.as<float>(), T, L.n_post_ffw, 1, nullptr, g->x32.as<float>(), s);
+        const int sd = split_k(F);
+        gemm_batched(g->g16.as<half_t>(), F, F / sd, L.wdown.as<half_t>(), F, F / sd, 1, T, H, F / sd, nullptr, 0, 0,
+                     g->y32.as<float>(), H, T * H, sd, s);
+        norm(g, g->y32.as<float>(), T, L.n_post_ffw, 1, nullptr, g->x32.as<float>(), s, sd);
     }
     norm(g, g->x32.as<float>(), T, g->out_norm, 2, nullptr, g->out32.as<float>(), s);
 }
@@ -486,7 +549,26 @@ int sana_gemma_encode(sana_gemma * g, const int32_t * tokens, int64_t n, float *
                 throw_err(SANA_ERR_INVALID_ARGUMENT, "gemma token id out of range at position " + std::to_string(i));
         ensure_workspace(g, n);
         hip_check(hipMemcpyAsync(g->tok.p, tokens, (size_t)n * 4, hipMemcpyHostToDevice, g->stream), "upload tokens");
-        encode(g, n, g->stream);
+        auto it = g->graphs.find(n);
+        if (it == g->graphs.end()) {
+            if (g->graphs.size() >= 8) drop_graphs(g);
+            hipGraph_t graph = nullptr;
+            hip_check(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+            try {
+                encode(g, n, g->stream);
+            } catch (...) {
+                (void)hipStreamEndCapture(g->stream, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                throw;
+            }
+            hip_check(hipStreamEndCapture(g->stream, &graph), "hipStreamEndCapture");
+            hipGraphExec_t exec = nullptr;
+            const hipError_t r = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            hip_check(r, "hipGraphInstantiate");
+            it = g->graphs.emplace(n, exec).first;
+        }
+        hip_check(hipGraphLaunch(it->second, g->stream), "hipGraphLaunch");
         hip_check(hipMemcpyAsync(hidden, g->out32.p, (size_t)n * g->cfg.hidden * 4, hipMemcpyDeviceToHost, g->stream),
                   "download hidden");
         hip_check(hipStreamSynchronize(g->stream), "gemma encode");

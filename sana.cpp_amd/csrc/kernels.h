@@ -67,6 +67,12 @@ struct GemmParams {
     // (y, x), channel n takes up_src[(y/2, x/2)][(4n + 2(y%2) + x%2) / up_rep].
     const float * up_src = nullptr;
     int up_c = 0, up_rep = 1;
+    // Batched plain stores (mode kGemmStore, conv 0): `batch` independent
+    // products in one launch; product z reads A + z * batch_a, W + (z / batch_w_div)
+    // * batch_w (grouped heads share a W) and writes out16 + z * batch_o16 and
+    // out32 + z * batch_o32 (element offsets).
+    int batch = 1, batch_w_div = 1;
+    int64_t batch_a = 0, batch_w = 0, batch_o16 = 0, batch_o32 = 0;
     // Launches of this shape that run concurrently with this one (on other
     // streams or graph branches); the tile choice sizes its grid for the CUs
     // it shares with them.

@@ -61,6 +61,26 @@ def test_encode_vs_oracle(name, T):
         dev.close()
 
 
+def test_graph_replays_and_weight_reload():
+    """The encoder runs as one cached graph per token count: interleaved
+    lengths replay their own graphs with new tokens, and a weight set after a
+    capture (which drops the graphs) is used by the next encode."""
+    cfg = CONFIGS["gqa_window"]
+    w, dev = build(cfg)
+    try:
+        rng = np.random.default_rng(11)
+        for T in (23, 40, 23, 40, 23):
+            tokens = rng.integers(0, cfg["vocab"], size=T)
+            assert rel_l2(dev.encode(tokens), G.forward(w, cfg, tokens)) < TOL
+        name = "blk.1.ffn_down.weight"
+        w[name] = (w[name] * -1.5).astype(np.float32)
+        dev.set_weight(name, w[name])
+        tokens = rng.integers(0, cfg["vocab"], size=23)
+        assert rel_l2(dev.encode(tokens), G.forward(w, cfg, tokens)) < TOL
+    finally:
+        dev.close()
+
+
 def test_prefix_positions_are_causal():
     """Causal attention: the hidden states of a prefix do not depend on the
     tokens after it (the reference pads prompts at the end for this reason)."""
