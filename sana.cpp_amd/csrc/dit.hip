@@ -218,8 +218,14 @@ void gemm_qkv_split(sana_dit * c, BlockDev & w, int64_t B, int64_t N, const half
 }
 
 // Whether the self attention runs as kGemmQKV + one fused linear-attention kernel.
+// The fused linear attention rebuilds each head's state in every workgroup
+// that shares the head, which stops paying off on long sequences: at 16384
+// tokens per image the three-kernel path (chunk states, reduction, apply) made
+// the 4096 px forward 2 ms faster (57.9 against 59.9 ms), at 4096 tokens they tie.
+constexpr int64_t kLaFusedMaxTokens = 8192;
+
 bool fused_linear_attention(const sana_dit * c, int64_t N) {
-    return sana::linear_attention_fused_ok((int)N, (int)c->Ds) && c->C % 8 == 0;
+    return sana::linear_attention_fused_ok((int)N, (int)c->Ds) && c->C % 8 == 0 && N <= kLaFusedMaxTokens;
 }
 
 void gemm_store(sana_dit * c, const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N,
