@@ -615,6 +615,11 @@ __global__ __launch_bounds__(256) void xattn_kernel(const f16 * __restrict__ q, 
 // produces the softmax denominator sum_k p_k.  The two key halves' (max, O^T) are merged
 // through LDS: O = O_0 2^(m_0 - m) + O_1 2^(m_1 - m), m = max(m_0, m_1).
 //
+// With FLASH (long sequences) each wave instead takes 32 queries of each of
+// `qblocks` 256-query blocks in turn and both key halves itself, with a
+// running max (online softmax), so one staging of the head serves many queries
+// and no merge is needed.
+//
 // Staging issues every 16-byte load (Q, K, V^T) up front, unconditionally and
 // in bounds (clamped rows and chunks, masked afterwards with dword ANDs), with
 // a power-of-two thread -> (row, chunk) map.  Measured slower: writing V^T to
@@ -640,12 +645,12 @@ struct XaCfg {
     static constexpr int LDS_BYTES = STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES;
 };
 
-template <int LT, int KS, bool ONES>
+template <int LT, int KS, bool ONES, bool FLASH>
 __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__ q, int64_t ldq,
                                                         const f16 * __restrict__ k, int64_t ldk,
                                                         const f16 * __restrict__ vt, int64_t ldvt,
                                                         const float * __restrict__ bias, f16 * __restrict__ out,
-                                                        int64_t ldo, int N, int L, int D, float scale) {
+                                                        int64_t ldo, int N, int L, int D, float scale, int qblocks) {
     using X = XaCfg<LT, KS>;
     static_assert(LT % 2 == 0, "key tiles split in two halves");
     static_assert(X::DP <= 128 && X::LP / 8 <= 64, "staging map");
@@ -659,24 +664,27 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = w & 3, kh = w >> 2;
     const int hh = lane >> 5;
-    const int q0 = blockIdx.y * kXaQ + g * 32;
     constexpr bool ones_row = ONES;  // D < DP: the last V^T row carries the denominator
 
     // query fragments (B operand of the score MFMA): query (lane & 31), dims 16 ks + 8 hh ..
-    const int qcol = min(q0 + (lane & 31), N - 1);
-    const f16 * qr = q + ((int64_t)b * N + qcol) * ldq + (int64_t)h * D;
     f16x8 qf[KS];
+    auto load_q = [&](int q0) {
+        const int qcol = min(q0 + (lane & 31), N - 1);
+        const f16 * qr = q + ((int64_t)b * N + qcol) * ldq + (int64_t)h * D;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const int d0 = ks * 16 + 8 * hh;
-        const f16x8 v = *reinterpret_cast<const f16x8 *>(qr + min(d0, D - 8));
-        uint32_t w[4];
-        __builtin_memcpy(w, &v, 16);
-        const uint32_t m = d0 < D ? 0xffffffffu : 0u;  // dims past D are zero
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d0 = ks * 16 + 8 * hh;
+            const f16x8 v = *reinterpret_cast<const f16x8 *>(qr + min(d0, D - 8));
+            uint32_t w[4];
+            __builtin_memcpy(w, &v, 16);
+            const uint32_t m = d0 < D ? 0xffffffffu : 0u;  // dims past D are zero
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] &= m;
-        __builtin_memcpy(&qf[ks], w, 16);
-    }
+            for (int e = 0; e < 4; ++e) w[e] &= m;
+            __builtin_memcpy(&qf[ks], w, 16);
+        }
+    };
+    const int q0 = blockIdx.y * kXaQ + g * 32;  // key-split path: this wave's query group
+    if constexpr (!FLASH) load_q(q0);
 
     // K staging: thread -> chunk kc = tid & 15 (8 dims), rows kr0 + 32 j.  Every
     // load is in bounds and unconditional: rows past L repeat row L - 1 and
@@ -743,6 +751,125 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
         }
     }
     __syncthreads();
+
+    if constexpr (FLASH) {
+        // Long sequences: the staged head serves `qblocks` blocks of 256 queries.
+        // Each wave takes 32 queries per block and both key halves in turn with
+        // a running max (online softmax), so no cross-wave merge is needed and
+        // the waves never synchronise after the staging.
+        const float scale2 = scale * kLog2e;
+        for (int qb = 0; qb < qblocks; ++qb) {
+            const int qw = ((blockIdx.y * qblocks + qb) * 8 + w) * 32;
+            if (qw >= N) break;
+            load_q(qw);
+            f32x16 o[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
+            float m = -INFINITY, sum = 0.0f;
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int tb = half * LTH;
+                f32x16 st[LTH];
+#pragma unroll
+                for (int t = 0; t < LTH; ++t)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) st[t][i] = 0.0f;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int d0 = ks * 16 + 8 * hh;
+#pragma unroll
+                    for (int t = 0; t < LTH; ++t) {
+                        const f16x8 kf =
+                            *reinterpret_cast<const f16x8 *>(Ks + ((tb + t) * 32 + (lane & 31)) * KROW + d0);
+                        st[t] = mfma_32x32x16(kf, qf[ks], st[t]);
+                    }
+                }
+                float mh = -INFINITY;
+                const bool raw = ONES && !bias;
+                if (raw) {
+#pragma unroll
+                    for (int t = 0; t < LTH; ++t)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) mh = fmaxf(mh, st[t][i]);
+                    mh = fmaxf(mh, __shfl_xor(mh, 32, 64)) * scale2;
+                } else {
+#pragma unroll
+                    for (int t = 0; t < LTH; ++t)
+#pragma unroll
+                        for (int i4 = 0; i4 < 4; ++i4) {
+                            const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bs + (tb + t) * 32 + 8 * i4 + 4 * hh);
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+                                const float sv = st[t][4 * i4 + u] * scale2 + b4[u];
+                                st[t][4 * i4 + u] = sv;
+                                mh = fmaxf(mh, sv);
+                            }
+                        }
+                    mh = fmaxf(mh, __shfl_xor(mh, 32, 64));
+                }
+                const float mn = fmaxf(m, mh);
+                // all keys so far at -inf: keep their probabilities at exp2(-inf) = 0
+                const float mref = mn == -INFINITY ? 0.0f : mn;
+                if (half == 1) {
+                    const float a = __builtin_amdgcn_exp2f(m - mref);
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) o[dt][i] *= a;
+                    sum *= a;
+                }
+                f16x8 pf[LTH][2];
+#pragma unroll
+                for (int t = 0; t < LTH; ++t)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const float e = raw ? __builtin_amdgcn_exp2f(fmaf(st[t][i], scale2, -mref))
+                                            : __builtin_amdgcn_exp2f(st[t][i] - mref);
+                        if constexpr (!ones_row) sum += e;
+                        pf[t][i >> 3][i & 7] = (f16)e;
+                    }
+#pragma unroll
+                for (int t = 0; t < LTH; ++t)
+#pragma unroll
+                    for (int s2 = 0; s2 < 2; ++s2) {
+                        const int kpos = (tb + t) * 32 + 16 * s2 + 8 * hh;
+#pragma unroll
+                        for (int dt = 0; dt < DT; ++dt) {
+                            const f16x8 af =
+                                *reinterpret_cast<const f16x8 *>(Vs + (dt * 32 + (lane & 31)) * VROW + kpos);
+                            o[dt] = mfma_32x32x16(af, pf[t][s2], o[dt]);
+                        }
+                    }
+                m = mn;
+            }
+            float den;
+            if constexpr (ones_row) {
+                den = __shfl(o[DT - 1][15], (lane & 31) + 32, 64);
+            } else {
+                den = sum + __shfl_xor(sum, 32, 64);
+            }
+            const float rs = 1.0f / den;
+            const int qq = qw + (lane & 31);
+            if (qq < N) {
+                f16 * orow = out + ((int64_t)b * N + qq) * ldo + (int64_t)h * D;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4) {
+                        const int dim = dt * 32 + 8 * i4 + 4 * hh;
+                        if (dim < D) {
+                            f16x4 v4;
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) v4[u] = (f16)(o[dt][4 * i4 + u] * rs);
+                            *reinterpret_cast<f16x4 *>(orow + dim) = v4;
+                        }
+                    }
+            }
+        }
+        return;
+    }
 
     // scores of this wave's key half: tile t is global key tile kh * LTH + t
     const int tb = kh * LTH;
@@ -866,21 +993,48 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
     }
 }
 
+// Queries per image from which one staging of a head serves several 256-query
+// blocks (the online-softmax path of xattn_lds_kernel, for 320 staged keys).
+// Measured per 300-key, 16 x 72-head launch: 14.3 against 18.6 us at 4096
+// queries, 40.5 against 68.8 us at 16384; at 1024 the key-split path's
+// 128-query workgroups win (9.4 against 12.0 us).
+constexpr int kXaFlashTokens = 4096;
+
+template <int LT, int KS, bool ONES, bool FLASH>
+hipError_t launch_xattn_lds2(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
+                             const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D,
+                             float scale, hipStream_t s) {
+    using X = XaCfg<LT, KS>;
+    static const bool attr =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&xattn_lds_kernel<LT, KS, ONES, FLASH>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, X::LDS_BYTES) == hipSuccess;
+    (void)attr;
+    static const std::string name = "xattn_lds_kernel<" + std::to_string(LT) + ", " + std::to_string(KS) + ", " +
+                                    (ONES ? "true" : "false") + (FLASH ? ", true>" : ", false>");
+    note_kernel(name.c_str());
+    dim3 grid(H, (N + kXaQ - 1) / kXaQ, B);
+    int qblocks = 1;
+    if (FLASH) {
+        // blocks of 256 queries per workgroup: about 256 workgroups in all
+        const int64_t nqb = (N + 255) / 256;
+        qblocks = (int)std::max<int64_t>(1, nqb * H * B / 256);
+        grid.y = (unsigned)((nqb + qblocks - 1) / qblocks);
+    }
+    hipLaunchKernelGGL((xattn_lds_kernel<LT, KS, ONES, FLASH>), grid, dim3(512), X::LDS_BYTES, s, q, ldq, k, ldk, vt,
+                       ldvt, bias, out, ldo, N, L, D, scale, qblocks);
+    return hipGetLastError();
+}
+
 template <int LT, int KS, bool ONES>
 hipError_t launch_xattn_lds1(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
                              const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D,
                              float scale, hipStream_t s) {
-    using X = XaCfg<LT, KS>;
-    static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&xattn_lds_kernel<LT, KS, ONES>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, X::LDS_BYTES) ==
-                             hipSuccess;
-    (void)attr;
-    static const std::string name = "xattn_lds_kernel<" + std::to_string(LT) + ", " + std::to_string(KS) + ", " +
-                                    (ONES ? "true" : "false") + ">";
-    note_kernel(name.c_str());
-    hipLaunchKernelGGL((xattn_lds_kernel<LT, KS, ONES>), dim3(H, (N + kXaQ - 1) / kXaQ, B), dim3(512), X::LDS_BYTES,
-                       s, q, ldq, k, ldk, vt, ldvt, bias, out, ldo, N, L, D, scale);
-    return hipGetLastError();
+    if constexpr (LT == 10) {
+        if (N >= kXaFlashTokens)
+            return launch_xattn_lds2<LT, KS, ONES, true>(q, ldq, k, ldk, vt, ldvt, bias, out, ldo, B, N, L, H, D,
+                                                         scale, s);
+    }
+    return launch_xattn_lds2<LT, KS, ONES, false>(q, ldq, k, ldk, vt, ldvt, bias, out, ldo, B, N, L, H, D, scale, s);
 }
 
 template <int LT, int KS>

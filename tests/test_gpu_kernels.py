@@ -298,6 +298,29 @@ def test_peak_kernels_do_their_work(L):
             assert (msink != 0).any()
 
 
+@pytest.mark.parametrize("B,N,Lk,H,D,masked", [(2, 4096, 300, 16, 72, False), (1, 4500, 300, 16, 72, True),
+                                               (1, 4099, 290, 4, 64, True), (1, 8192, 300, 2, 72, False)])
+def test_cross_attention_long_sequences(L, B, N, Lk, H, D, masked):
+    """From 4096 queries the staged head serves several 256-query blocks with
+    an online softmax over the two key halves (ragged last blocks, masks, and
+    D = 64 with the in-register denominator)."""
+    rng = np.random.default_rng(N + Lk + D)
+    C = H * D
+    q = f16(rng.standard_normal((B, N, C)))
+    k = f16(rng.standard_normal((B, Lk, C)))
+    v = f16(rng.standard_normal((B, Lk, C)))
+    bias = None
+    if masked:
+        bias = np.full((B, Lk), -10000.0, np.float32)
+        bias[0, :Lk // 3] = 0
+        if B > 1:
+            bias[1, :7] = 0
+    ref = O.attention(q, k, v, H, bias)
+    got = _xattn(L, q, k, v, H, bias, pad=np.nan)
+    assert np.isfinite(got).all()
+    assert rel_l2(got, ref) < 2e-3, rel_l2(got, ref)
+
+
 @pytest.mark.parametrize("Lk,masked", [(300, False), (300, True), (77, False)])
 def test_cross_attention_ignores_vt_padding(L, Lk, masked):
     """V^T columns past the key count hold NaN: the kernel must not read them
