@@ -145,6 +145,9 @@ hipError_t cross_attention(const half_t * q, int64_t ldq, const half_t * k, int6
 // Depthwise 3x3 (zero pad, bias) + GLU gate on a token-major grid:
 // x fp16 [B, H*W, ldx] (E = 2F channels), wt fp32 tap-major [9][E], bias [E],
 // out[b, t, c] = f16(d(c) * silu(d(F + c))), out fp16 [B*H*W, ldo].
+hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const float * bias, half_t * out, int64_t ldo,
+                      int B, int Hh, int Ww, int F, hipStream_t s);
+
 // Measured MFMA ceiling: `workgroups` x 256 threads of independent fp16
 // 32x32x16 MFMA chains, `iters` steps; sink holds workgroups * 256 floats.
 hipError_t mfma_peak(int workgroups, int iters, bool zero_operands, float * sink, hipStream_t s);
@@ -154,8 +157,5 @@ double mfma_peak_flops(int workgroups, int iters);
 // hbm_peak_workgroups() * 256 floats).
 int hbm_peak_workgroups();
 hipError_t hbm_peak(const void * src, void * dst, int64_t bytes, float * sink, hipStream_t s);
-
-hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const float * bias, half_t * out, int64_t ldo,
-                      int B, int Hh, int Ww, int F, hipStream_t s);
 
 }  // namespace sana
