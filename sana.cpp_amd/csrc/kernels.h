@@ -91,9 +91,21 @@ const char * last_kernel();
 // LayerNorm (eps, optional gamma/beta) + adaLN modulate, fp32 in, fp16 out:
 // out[m, c] = f16(ln(x)[m, c] * (1 + scale) + shift), with
 // shift = mod_a[b * mod_stride + shift_off + c] + mod_t[shift_off + c] (same for scale; mod_t may be null).
+// Device ranges a launch reads on the side to pull them into the 256 MB
+// last-level cache before a later kernel needs them (the next GEMMs' weights):
+// `workgroups` extra workgroups stream the n ranges (16-byte multiples,
+// 16-byte aligned) and discard the data.
+struct CacheWarm {
+    static constexpr int kMax = 4;
+    const void * p[kMax] = {nullptr, nullptr, nullptr, nullptr};
+    int64_t bytes[kMax] = {0, 0, 0, 0};
+    int n = 0, workgroups = 0;
+};
+// warm: optional cache warm-up carried by the same launch (vectorised rows only).
 hipError_t ln_modulate(const float * x, int64_t ldx, half_t * out, int64_t ldo, int M, int C, int rows_per_batch,
                        float eps, const float * gamma, const float * beta, const float * mod_a, const float * mod_t,
-                       int64_t mod_stride, int64_t shift_off, int64_t scale_off, hipStream_t s);
+                       int64_t mod_stride, int64_t shift_off, int64_t scale_off, hipStream_t s,
+                       const CacheWarm * warm = nullptr);
 
 // comb[l][b][i] = tmod[b][i] + tables[l][i] (l < L, b < B, i < W).
 hipError_t mod_combine(const float * tmod, const float * tables, int L, int B, int W, float * comb, hipStream_t s);
