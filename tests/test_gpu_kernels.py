@@ -49,7 +49,9 @@ GEMM_SHAPES = [
     (2048, 5760, 1152),   # Mix-FFN inverted
     (2048, 1152, 2880),   # Mix-FFN point
     (2048, 1152, 1152),   # attention out / cross q / cross out
-    (2000, 5760, 1152),   # 128x192 tiles, last row tile partial
+    (2000, 5760, 1152),   # 128x192 tiles in one round, last row tile partial
+    (1000, 5760, 1152),   # 128x128 tiles, last row tile partial
+    (16300, 1152, 1152),  # 128x192 tiles over many rounds, last row tile partial
     (2000, 1152, 2880),   # 128x64 tiles, last row tile partial
     (600, 4608, 1152),    # cross K of 4 blocks
     (100, 70, 64),        # ragged M and N
@@ -91,7 +93,8 @@ def test_gemm_activation(L, act):
     assert rel_l2(host(o32), ref) < 1e-5
 
 
-@pytest.mark.parametrize("B,Ntok,C,K", [(2, 96, 160, 128), (2, 1000, 1152, 2880)])
+@pytest.mark.parametrize("B,Ntok,C,K", [(2, 96, 160, 128), (2, 1000, 1152, 2880),
+                                         (2, 8192, 1152, 1152)])   # 128x192 residual tiles
 def test_gemm_residual_gate(L, B, Ntok, C, K):
     M = B * Ntok
     rng = np.random.default_rng(5)
