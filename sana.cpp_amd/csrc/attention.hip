@@ -466,6 +466,85 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
     }
 }
 
+// la_chunk_kernel: the chunk partial states of the three-kernel path for
+// head_dim 32, from the kGemmQKV layouts (relu(K)^T and V^T token-contiguous
+// per channel).  One workgroup of 8 waves per (token chunk, b, h): each wave
+// sums its share of the chunk as la_fused_kernel's step 1 does (MFMA operands
+// straight from global memory), the 8 partials are added in LDS in wave order
+// and the chunk's (D+1) x D partial is written in la_state_kernel's layout
+// (part[r * D + d] = S[r][d], ksum in row D) with its max |entry|, so
+// la_reduce_kernel and la_apply_kernel follow unchanged.
+__global__ __launch_bounds__(64 * kLfWaves) void la_chunk_kernel(const f16 * __restrict__ kt,
+                                                                 const f16 * __restrict__ vt, int N, int T, int nch,
+                                                                 float * __restrict__ part,
+                                                                 float * __restrict__ pmax) {
+    __shared__ float sp[kLfWaves][33][33];  // per-wave S^T (rows d) + ksum row, padded rows
+    __shared__ float wmax[kLfWaves];
+    const int c = blockIdx.x, bh = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5;
+    const f16 * K = kt + (int64_t)bh * 32 * N;
+    const f16 * V = vt + (int64_t)bh * 32 * N;
+    const int cb = c * T, ce = min(N, cb + T);
+    const int span = ((ce - cb + kLfWaves - 1) / kLfWaves + 15) / 16 * 16;
+    const int tb = min(ce, cb + w * span), te = min(ce, tb + span);
+    f32x16 sacc, ks;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sacc[i] = ks[i] = 0.0f;
+    f16x8 ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (f16)1.0f;
+    const f16 * krow = K + (int64_t)(lane & 31) * N + 8 * hh;
+    const f16 * vrow = V + (int64_t)(lane & 31) * N + 8 * hh;
+    constexpr int kG = 8;
+    for (int g0 = tb; g0 < te; g0 += 16 * kG) {
+        f16x8 ka[kG], va[kG];
+#pragma unroll
+        for (int u = 0; u < kG; ++u) {
+            const int t = g0 + 16 * u;
+            if (t < te) {
+                ka[u] = *reinterpret_cast<const f16x8 *>(krow + t);
+                va[u] = *reinterpret_cast<const f16x8 *>(vrow + t);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kG; ++u) {
+            if (g0 + 16 * u < te) {
+                sacc = mfma_32x32x16(ka[u], va[u], sacc);
+                ks = mfma_32x32x16(ka[u], ones, ks);
+            }
+        }
+    }
+    // lane holds column r = lane & 31 and rows d = 8*(i/4) + 4*hh + i%4
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int d = 8 * (i >> 2) + 4 * hh + (i & 3);
+        sp[w][d][lane & 31] = sacc[i];
+        if ((lane & 31) == 0) sp[w][32][d] = ks[i];
+    }
+    __syncthreads();
+    float * out = part + ((int64_t)bh * nch + c) * (33 * 32);
+    float m = 0.0f;
+    for (int e = tid; e < 33 * 32; e += 64 * kLfWaves) {
+        const int r = e >> 5, d = e & 31;
+        float a = 0.0f;
+        if (r < 32) {
+            for (int ww = 0; ww < kLfWaves; ++ww) a += sp[ww][d][r];
+        } else {
+            for (int ww = 0; ww < kLfWaves; ++ww) a += sp[ww][32][d];
+        }
+        out[e] = a;
+        m = fmaxf(m, fabsf(a));
+    }
+    m = wave_max(m);
+    if (lane == 0) wmax[w] = m;
+    __syncthreads();
+    if (tid == 0) {
+        float mm = 0.0f;
+        for (int ww = 0; ww < kLfWaves; ++ww) mm = fmaxf(mm, wmax[ww]);
+        pmax[(int64_t)bh * nch + c] = mm;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // K4: softmax cross-attention (attention_4d, src/transformer_ops.cpp:348-392:
 // scores * 1/sqrt(D), + bias, softmax over keys, . V) fused per
@@ -1097,6 +1176,30 @@ hipError_t linear_attention_fused(const half_t * q, int64_t ldq, const half_t * 
     hipLaunchKernelGGL(la_fused_kernel, dim3((unsigned)(B * H * splits)), dim3(64 * kLfWaves), 0, s,
                        reinterpret_cast<const f16 *>(q), ldq, reinterpret_cast<const f16 *>(kt),
                        reinterpret_cast<const f16 *>(vt), reinterpret_cast<f16 *>(out), ldo, N, H, splits);
+    return hipGetLastError();
+}
+
+hipError_t linear_attention_chunked(const half_t * q, int64_t ldq, const half_t * kt, const half_t * vt,
+                                    half_t * out, int64_t ldo, int B, int N, int H, int D, float * ws, hipStream_t s) {
+    if (!linear_attention_fused_ok(N, D) || B <= 0 || H <= 0 || ldq < (int64_t)H * D || ldo < (int64_t)H * D ||
+        ldq % 8 || (int64_t)B * H > 65535 || !ws ||
+        ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kt) | reinterpret_cast<uintptr_t>(vt)) & 15))
+        return hipErrorInvalidValue;
+    const int T = la_chunk_tokens(N);
+    const int nch = (N + T - 1) / T;
+    constexpr int E = 33 * 32, NP = 64, KP = 32;  // NT = 2 column tiles of [S | ksum], KS = 2 steps over d
+    float * part = ws;
+    f16 * shi = reinterpret_cast<f16 *>(ws + ((size_t)B * H * E * nch + 3) / 4 * 4);
+    f16 * slo = shi + (size_t)B * H * NP * KP;
+    float * pmax = reinterpret_cast<float *>(slo + (size_t)B * H * NP * KP);
+    note_kernel("la_chunk_kernel + la_reduce_kernel + la_apply_kernel");
+    hipLaunchKernelGGL(la_chunk_kernel, dim3((unsigned)nch, (unsigned)(B * H)), dim3(64 * kLfWaves), 0, s,
+                       reinterpret_cast<const f16 *>(kt), reinterpret_cast<const f16 *>(vt), N, T, nch, part, pmax);
+    hipLaunchKernelGGL(la_reduce_kernel, dim3((NP * KP + 255) / 256, B * H), dim3(256), 0, s, part, pmax, nch, D, NP,
+                       KP, shi, slo);
+    hipLaunchKernelGGL((la_apply_kernel<2, 2>), dim3((N + 127) / 128, H, B), dim3(256), 0, s,
+                       reinterpret_cast<const f16 *>(q), ldq, shi, slo, pmax, nch, reinterpret_cast<f16 *>(out), ldo,
+                       N, H, D, 1);
     return hipGetLastError();
 }
 

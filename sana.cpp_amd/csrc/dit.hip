@@ -229,6 +229,14 @@ bool fused_linear_attention(const sana_dit * c, int64_t N) {
     return sana::linear_attention_fused_ok((int)N, (int)c->Ds) && c->C % 8 == 0 && N <= kLaFusedMaxTokens;
 }
 
+// Whether the q | k | v projection writes the kGemmQKV layouts: head_dim 32,
+// for the fused kernel up to kLaFusedMaxTokens and the chunked three-kernel
+// path from relu(K)^T / V^T beyond (at 16384 tokens per branch 55 us against
+// 80 us for the token-major three-kernel path).
+bool qkv_split_layout(const sana_dit * c, int64_t N) {
+    return sana::linear_attention_fused_ok((int)N, (int)c->Ds) && c->C % 8 == 0;
+}
+
 void gemm_store(sana_dit * c, const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N,
                 int64_t K, const float * bias, int act, half_t * o16, int64_t ldo16, float * o32, int64_t ldo32,
                 hipStream_t s, int co = 1) {
@@ -445,19 +453,24 @@ void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * 
                                    w.has_ln1 ? w.ln1_g.as<float>() : nullptr, w.has_ln1 ? w.ln1_b.as<float>() : nullptr,
                                    mod, nullptr, 6 * C, 0, C, s, &warm1),
                  "ln_modulate");
-    if (fused_linear_attention(c, N)) {
+    float * la_ws = (b0 > 0 && B == 1) ? c->la_ws2.as<float>() : c->la_ws.as<float>();
+    if (qkv_split_layout(c, N)) {
         half_t * kt16 = c->la_kt.as<half_t>() + b0 * C * N;
         half_t * vt16 = c->la_vt.as<half_t>() + b0 * C * N;
         gemm_qkv_split(c, w, B, N, xa16, qkv16, kt16, vt16, co, s);
-        launch_check(sana::linear_attention_fused(qkv16, 3 * C, kt16, vt16, o16, c->Cp, (int)B, (int)N, (int)c->Hs,
-                                                  (int)c->Ds, s, co),
-                     "linear_attention_fused");
+        if (fused_linear_attention(c, N))
+            launch_check(sana::linear_attention_fused(qkv16, 3 * C, kt16, vt16, o16, c->Cp, (int)B, (int)N,
+                                                      (int)c->Hs, (int)c->Ds, s, co),
+                         "linear_attention_fused");
+        else
+            launch_check(sana::linear_attention_chunked(qkv16, 3 * C, kt16, vt16, o16, c->Cp, (int)B, (int)N,
+                                                        (int)c->Hs, (int)c->Ds, la_ws, s),
+                         "linear_attention_chunked");
     } else {
         gemm_store(c, xa16, c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
                    w.has_qkv_bias ? w.b_qkv.as<float>() : nullptr, sana::kActNone, qkv16, 3 * C, nullptr, 0, s, co);
-        float * ws = (b0 > 0 && B == 1) ? c->la_ws2.as<float>() : c->la_ws.as<float>();
         launch_check(sana::linear_attention(qkv16, qkv16 + C, qkv16 + 2 * C, 3 * C, o16, c->Cp, (int)B, (int)N,
-                                            (int)c->Hs, (int)c->Ds, ws, s),
+                                            (int)c->Hs, (int)c->Ds, la_ws, s),
                      "linear_attention");
     }
     // x += gate_msa * (o Wo^T + bo); r16 = fp16(x) for the cross-attention query
@@ -1241,7 +1254,7 @@ int sana_dit_time_kernel(sana_dit * c, int which, int iters, float * avg_ms, dou
             half_t * vt16 = c->la_vt.as<half_t>();
             switch (which) {
                 case 0:
-                    if (fused_linear_attention(c, N))
+                    if (qkv_split_layout(c, N))
                         gemm_qkv_split(c, w, B, N, c->xa16.as<half_t>(), c->qkv16.as<half_t>(), kt16, vt16, co, s);
                     else
                         gemm_store(c, c->xa16.as<half_t>(), c->Cp, w.w_qkv.as<half_t>(), c->Cp, M, 3 * C, c->Cp,
@@ -1281,6 +1294,11 @@ int sana_dit_time_kernel(sana_dit * c, int which, int iters, float * avg_ms, dou
                                                                   c->o16.as<half_t>(), c->Cp, (int)B, (int)N,
                                                                   (int)c->Hs, (int)c->Ds, s, co),
                                      "linear_attention_fused");
+                    else if (qkv_split_layout(c, N))
+                        launch_check(sana::linear_attention_chunked(c->qkv16.as<half_t>(), 3 * C, kt16, vt16,
+                                                                    c->o16.as<half_t>(), c->Cp, (int)B, (int)N,
+                                                                    (int)c->Hs, (int)c->Ds, c->la_ws.as<float>(), s),
+                                     "linear_attention_chunked");
                     else
                         launch_check(sana::linear_attention(c->qkv16.as<half_t>(), c->qkv16.as<half_t>() + C,
                                                             c->qkv16.as<half_t>() + 2 * C, 3 * C, c->o16.as<half_t>(),

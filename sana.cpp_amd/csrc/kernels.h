@@ -144,6 +144,13 @@ bool linear_attention_fused_ok(int N, int D);
 // co: launches of this shape running concurrently (sizes the token splits).
 hipError_t linear_attention_fused(const half_t * q, int64_t ldq, const half_t * kt, const half_t * vt, half_t * out,
                                   int64_t ldo, int B, int N, int H, int D, hipStream_t s, int co = 1);
+// The same from the kGemmQKV layouts in three kernels (chunk states straight
+// from relu(K)^T and V^T, the fixed-order reduction, the apply), for long
+// sequences where rebuilding the state per token split does not pay; head_dim
+// 32, workspace of linattn_workspace_floats(B, N, H, 32) floats.
+hipError_t linear_attention_chunked(const half_t * q, int64_t ldq, const half_t * kt, const half_t * vt,
+                                    half_t * out, int64_t ldo, int B, int N, int H, int D, float * workspace,
+                                    hipStream_t s);
 hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v, int64_t ld, half_t * out,
                             int64_t ldo, int B, int N, int H, int D, float * workspace, hipStream_t s);
 

@@ -69,6 +69,19 @@ def test_block_4096_tokens_large_state(one_block):
     _check_block(m, d, x, tm, ctx, f"N=4096 heads={heads} amplified")
 
 
+def test_block_16384_tokens_large_state(one_block):
+    # the same amplification through the chunked linear attention (chunk
+    # partial states, fixed-order reduction, scaled fp16 hi/lo apply)
+    heads, m, d, tmod, ctx = one_block
+    if heads != 36:
+        pytest.skip("production head layout only at 16384 tokens")
+    C = 1152
+    tm = tmod.copy()
+    tm[:, C:2 * C] += 31.0
+    x = O.randn((2, 16384, C), 9) * np.float32(0.5)
+    _check_block(m, d, x, tm, ctx, "N=16384 heads=36 amplified")
+
+
 def test_forward_4096px_finite_and_deterministic():
     import sana_dit
     print("generating the seeded 28-block weights on the host ...", flush=True)
