@@ -545,6 +545,91 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_chunk_kernel(const f16 * __r
     }
 }
 
+// la_apply32_kernel: the apply step of the chunked path for head_dim 32 as
+// la_fused_kernel's step 3: O^T[r][t] = [S | ksum] . relu(q)^T with the
+// reduced hi/lo state (la_reduce_kernel's [64][32] layout: rows 0..31 S,
+// row 32 ksum) as the A operand, so each lane holds four consecutive head dims
+// of one token and 32-token blocks leave through LDS as 64-byte token rows.
+// Workgroup: 8 waves over `span` tokens of one (b, h), 64 tokens per step.
+__global__ __launch_bounds__(64 * kLfWaves) void la_apply32_kernel(const f16 * __restrict__ q, int64_t ldq,
+                                                                   const f16 * __restrict__ shi,
+                                                                   const f16 * __restrict__ slo,
+                                                                   const float * __restrict__ pmax, int nch,
+                                                                   f16 * __restrict__ out, int64_t ldo, int N,
+                                                                   int H, int span) {
+    __shared__ __attribute__((aligned(16))) f16 ost[kLfWaves][32][kLfSrow];
+    const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5;
+    const int wspan = span / kLfWaves;  // a multiple of 64
+    const int ta = min(N, blockIdx.x * span + w * wspan), tz = min(N, ta + wspan);
+    const float eps = ldexpf(1e-15f, la_state_exponent(la_bound(pmax + (int64_t)bh * nch, nch)));
+    constexpr int KP = 32;
+    const int64_t sb = (int64_t)bh * 64 * KP + (lane & 31) * KP + 8 * hh;
+    f16x8 sa[2][2][2];  // [tile][hi|lo][k-step]
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            sa[tile][0][kk] = *reinterpret_cast<const f16x8 *>(shi + sb + tile * 32 * KP + kk * 16);
+            sa[tile][1][kk] = *reinterpret_cast<const f16x8 *>(slo + sb + tile * 32 * KP + kk * 16);
+        }
+    const f16 * qbase = q + (int64_t)b * N * ldq + (int64_t)h * 32 + 8 * hh;
+    auto load_q = [&](int t0, f16x8 (&qf)[2]) {
+        const int tq = min(t0 + (lane & 31), N - 1);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            qf[kk] = *reinterpret_cast<const f16x8 *>(qbase + (int64_t)tq * ldq + kk * 16);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[kk][e] = qf[kk][e] > (f16)0.0f ? qf[kk][e] : (f16)0.0f;
+        }
+    };
+    auto apply_store = [&](int t0, const f32x16 & o, const f32x16 & dn) {
+        const float rden = 1.0f / (__shfl(dn[0], lane & 31, 64) + eps);
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            f16x4 v4;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v4[u] = (f16)(o[4 * i4 + u] * rden);
+            *reinterpret_cast<f16x4 *>(&ost[w][lane & 31][8 * i4 + 4 * hh]) = v4;
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int tl = half * 16 + (lane >> 2), c8 = (lane & 3) * 8;
+            const f16x8 v8 = *reinterpret_cast<const f16x8 *>(&ost[w][tl][c8]);
+            const int t = t0 + tl;
+            if (t < tz) *reinterpret_cast<f16x8 *>(out + ((int64_t)b * N + t) * ldo + (int64_t)h * 32 + c8) = v8;
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+    f16x8 qa[2], qb[2];
+    if (ta < tz) {
+        load_q(ta, qa);
+        load_q(ta + 32, qb);
+    }
+    for (int t0 = ta; t0 < tz; t0 += 64) {
+        f32x16 oa, da, ob, db;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oa[i] = da[i] = ob[i] = db[i] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl) {
+                oa = mfma_32x32x16(sa[0][hl][kk], qa[kk], oa);
+                ob = mfma_32x32x16(sa[0][hl][kk], qb[kk], ob);
+                da = mfma_32x32x16(sa[1][hl][kk], qa[kk], da);
+                db = mfma_32x32x16(sa[1][hl][kk], qb[kk], db);
+            }
+        // the next step's queries are requested before this step's stores
+        if (t0 + 64 < tz) {
+            load_q(t0 + 64, qa);
+            load_q(t0 + 96, qb);
+        }
+        apply_store(t0, oa, da);
+        if (t0 + 32 < tz) apply_store(t0 + 32, ob, db);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // K4: softmax cross-attention (attention_4d, src/transformer_ops.cpp:348-392:
 // scores * 1/sqrt(D), + bias, softmax over keys, . V) fused per
@@ -1182,8 +1267,9 @@ hipError_t linear_attention_fused(const half_t * q, int64_t ldq, const half_t * 
 hipError_t linear_attention_chunked(const half_t * q, int64_t ldq, const half_t * kt, const half_t * vt,
                                     half_t * out, int64_t ldo, int B, int N, int H, int D, float * ws, hipStream_t s) {
     if (!linear_attention_fused_ok(N, D) || B <= 0 || H <= 0 || ldq < (int64_t)H * D || ldo < (int64_t)H * D ||
-        ldq % 8 || (int64_t)B * H > 65535 || !ws ||
-        ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kt) | reinterpret_cast<uintptr_t>(vt)) & 15))
+        ldq % 8 || ldo % 8 || (int64_t)B * H > 65535 || !ws ||
+        ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kt) | reinterpret_cast<uintptr_t>(vt) |
+          reinterpret_cast<uintptr_t>(out)) & 15))
         return hipErrorInvalidValue;
     const int T = la_chunk_tokens(N);
     const int nch = (N + T - 1) / T;
@@ -1192,14 +1278,16 @@ hipError_t linear_attention_chunked(const half_t * q, int64_t ldq, const half_t 
     f16 * shi = reinterpret_cast<f16 *>(ws + ((size_t)B * H * E * nch + 3) / 4 * 4);
     f16 * slo = shi + (size_t)B * H * NP * KP;
     float * pmax = reinterpret_cast<float *>(slo + (size_t)B * H * NP * KP);
-    note_kernel("la_chunk_kernel + la_reduce_kernel + la_apply_kernel");
+    note_kernel("la_chunk_kernel + la_reduce_kernel + la_apply32_kernel");
     hipLaunchKernelGGL(la_chunk_kernel, dim3((unsigned)nch, (unsigned)(B * H)), dim3(64 * kLfWaves), 0, s,
                        reinterpret_cast<const f16 *>(kt), reinterpret_cast<const f16 *>(vt), N, T, nch, part, pmax);
     hipLaunchKernelGGL(la_reduce_kernel, dim3((NP * KP + 255) / 256, B * H), dim3(256), 0, s, part, pmax, nch, D, NP,
                        KP, shi, slo);
-    hipLaunchKernelGGL((la_apply_kernel<2, 2>), dim3((N + 127) / 128, H, B), dim3(256), 0, s,
-                       reinterpret_cast<const f16 *>(q), ldq, shi, slo, pmax, nch, reinterpret_cast<f16 *>(out), ldo,
-                       N, H, D, 1);
+    // apply: 8 waves x 128 tokens per workgroup
+    constexpr int kSpan = 64 * 2 * kLfWaves;
+    hipLaunchKernelGGL(la_apply32_kernel, dim3((unsigned)((N + kSpan - 1) / kSpan), (unsigned)(B * H)),
+                       dim3(64 * kLfWaves), 0, s, reinterpret_cast<const f16 *>(q), ldq, shi, slo, pmax, nch,
+                       reinterpret_cast<f16 *>(out), ldo, N, H, kSpan);
     return hipGetLastError();
 }
 
