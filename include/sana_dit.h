@@ -272,6 +272,10 @@ int sana_hip_ln_modulate(const float * x, int64_t ldx, void * out16, int64_t ldo
                          int64_t rows_per_batch, float eps, const float * gamma, const float * beta,
                          const float * mod_a, const float * mod_t, int64_t mod_stride, int64_t shift_off,
                          int64_t scale_off, void * stream);
+/* ReLU linear attention (linear_attention_4d, src/transformer_ops.cpp:496-537)
+ * on fp16 token-major q / k / v [B*N, ld] (head h at columns h*D..), out fp16
+ * [B*N, ldo]; D <= 112, B * H <= 65535; workspace of
+ * sana_hip_linear_attention_workspace(B, N, H, D) bytes. */
 int sana_hip_linear_attention(const void * q, const void * k, const void * v, int64_t ld, void * out, int64_t ldo,
                               int64_t B, int64_t N, int64_t H, int64_t D, float * workspace, void * stream);
 size_t sana_hip_linear_attention_workspace(int64_t B, int64_t N, int64_t H, int64_t D);

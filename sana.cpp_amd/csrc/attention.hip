@@ -1304,7 +1304,7 @@ size_t linattn_workspace_floats(int B, int N, int H, int D) {
 hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v, int64_t ld, half_t * out,
                             int64_t ldo, int B, int N, int H, int D, float * ws, hipStream_t s) {
     if (B <= 0 || N <= 0 || H <= 0 || D <= 0 || D > 112 || ld < (int64_t)H * D || ldo < (int64_t)H * D || !ws ||
-        H > 65535 || B > 65535)
+        (int64_t)B * H > 65535)  // B * H workgroup rows of the reduction and the head_dim-32 apply
         return hipErrorInvalidValue;
     const int T = la_chunk_tokens(N);
     const int nch = (N + T - 1) / T;
@@ -1322,7 +1322,10 @@ hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v
     const int vec_kv = (D % 8 == 0 && ld % 8 == 0 && al16(k) && al16(v)) ? 1 : 0;
     const int vec_q = (D % 8 == 0 && ld % 8 == 0 && al16(q)) ? 1 : 0;
     const dim3 g1(nch, H, B);
-    note_kernel("la_state_kernel + la_reduce_kernel + la_apply_kernel");
+    // head_dim 32: the transposed apply with 64-byte token-row stores
+    const bool apply32 = D == 32 && vec_q && ldo % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    note_kernel(apply32 ? "la_state_kernel + la_reduce_kernel + la_apply32_kernel"
+                        : "la_state_kernel + la_reduce_kernel + la_apply_kernel");
     const int td = (D + 31) / 32;
     if (td == 1) hipLaunchKernelGGL((la_state_kernel<1>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
     else if (td == 2) hipLaunchKernelGGL((la_state_kernel<2>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
@@ -1330,8 +1333,14 @@ hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v
     else hipLaunchKernelGGL((la_state_kernel<4>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
     hipLaunchKernelGGL(la_reduce_kernel, dim3((NP * KP + 255) / 256, B * H), dim3(256), 0, s, part, pmax, nch, D,
                        NP, KP, shi, slo);
-    const dim3 g3((N + 127) / 128, H, B);
     f16 * oo = reinterpret_cast<f16 *>(out);
+    if (apply32) {
+        constexpr int kSpan = 64 * 2 * kLfWaves;
+        hipLaunchKernelGGL(la_apply32_kernel, dim3((unsigned)((N + kSpan - 1) / kSpan), (unsigned)(B * H)),
+                           dim3(64 * kLfWaves), 0, s, qq, ld, shi, slo, pmax, nch, oo, ldo, N, H, kSpan);
+        return hipGetLastError();
+    }
+    const dim3 g3((N + 127) / 128, H, B);
 #define SANA_LA_APPLY(nt, ks)                                                                                     \
     hipLaunchKernelGGL((la_apply_kernel<nt, ks>), g3, dim3(256), 0, s, qq, ld, shi, slo, pmax, nch, oo, ldo, N, H, \
                        D, vec_q)

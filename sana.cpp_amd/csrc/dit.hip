@@ -1412,9 +1412,9 @@ int sana_hip_linear_attention(const void * q, const void * k, const void * v, in
 int sana_hip_linear_attention_noalloc(const void * q, const void * k, const void * v, int64_t ld, void * out,
                                       int64_t ldo, int64_t B, int64_t N, int64_t H, int64_t D, void * stream) {
     return guarded([&] {
-        if (B <= 0 || N <= 0 || H <= 0 || D <= 0 || D > 112 || B > 65535 || H > 65535 || N > (1 << 30))
-            throw_err(SANA_ERR_INVALID_ARGUMENT, "linear_attention_noalloc: B, H in [1, 65535], N in [1, 2^30], "
-                                                 "D in [1, 112]");
+        if (B <= 0 || N <= 0 || H <= 0 || D <= 0 || D > 112 || B * H > 65535 || N > (1 << 30))
+            throw_err(SANA_ERR_INVALID_ARGUMENT, "linear_attention_noalloc: B, H >= 1 with B * H <= 65535, "
+                                                 "N in [1, 2^30], D in [1, 112]");
         const size_t need = sana::linattn_workspace_floats((int)B, (int)N, (int)H, (int)D);
         if (need > kLaScratchFloats)
             throw_err(SANA_ERR_INVALID_ARGUMENT,
