@@ -16,12 +16,14 @@ namespace {
 // denominator column"); then
 //   out[t][r] = sum_d S[r][d] relu(q[t][d]) / (sum_d S[D][d] relu(q[t][d]) + 1e-15).
 //
-// la_state_kernel: one wave per (token chunk, h, b).  Sub-chunks of 64 tokens
-//   of relu(K) and V are staged in LDS transposed (token-contiguous rows), so
-//   S^T = relu(K)^T . V is a chain of v_mfma_f32_32x32x16_f16 over tokens with
-//   16-byte operand reads; fp32 accumulation of exact fp16 products.  ksum is
-//   summed on the VALU from the same LDS rows.  Each chunk writes its partial
-//   (D+1) x D state.
+// la_state_kernel: one workgroup of 4 waves per (token chunk, h, b).  Sub-chunks
+//   of 64 tokens of relu(K) and V are staged in LDS transposed (token-contiguous
+//   rows) by all four waves, so S^T = relu(K)^T . V is a chain of
+//   v_mfma_f32_32x32x16_f16 over tokens with 16-byte operand reads; fp32
+//   accumulation of exact fp16 products.  The waves split the 32x32 tiles of
+//   the state, or for D <= 32 (one tile) the 16-token steps, added in LDS in
+//   wave order.  ksum is summed on the VALU from the same LDS rows.  Each chunk
+//   writes its partial (D+1) x D state.
 // la_reduce_kernel: sums the chunk partials in fixed chunk order (no atomics,
 //   bit-reproducible) into an fp16 hi/lo pair of the state, scaled by 2^k.
 // la_apply_kernel: relu(Q) . [S | ksum]^T on MFMA (hi and lo halves), one wave
@@ -55,29 +57,36 @@ constexpr int kLaSub = 64;                 // tokens per LDS sub-chunk
 constexpr int kLaChunks = 16;              // partial states per (b, h)
 constexpr int kLaRow = kLaSub + 8;         // halves per transposed LDS row (144 B: conflict-free reads)
 
+constexpr int kLsWaves = 4;                // waves per la_state_kernel workgroup
+
 template <int TD>  // ceil(D / 32): 32x32 MFMA tiles per side of the state
-__global__ __launch_bounds__(64) void la_state_kernel(const f16 * __restrict__ k, const f16 * __restrict__ v,
-                                                      int64_t ld, int N, int H, int D, int T, int nch, int vec,
-                                                      float * __restrict__ part, float * __restrict__ pmax) {
+__global__ __launch_bounds__(64 * kLsWaves) void la_state_kernel(const f16 * __restrict__ k,
+                                                                 const f16 * __restrict__ v, int64_t ld, int N,
+                                                                 int H, int D, int T, int nch, int vec,
+                                                                 float * __restrict__ part,
+                                                                 float * __restrict__ pmax) {
     constexpr int DP = TD * 32;
+    constexpr int NTILE = TD * TD;
+    // one tile (D <= 32): the waves split each sub-chunk's four 16-token steps
+    // and their partials are added in LDS; more tiles: the waves split the tiles
+    constexpr bool kSplitSteps = TD == 1;
+    constexpr int MYT = kSplitSteps ? 1 : (NTILE + kLsWaves - 1) / kLsWaves;
     __shared__ __attribute__((aligned(16))) f16 Kt[DP][kLaRow];
     __shared__ __attribute__((aligned(16))) f16 Vt[DP][kLaRow];
+    __shared__ float red[kSplitSteps ? kLsWaves : 1][kSplitSteps ? 32 : 1][33];
+    __shared__ float wmax[kLsWaves];
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x;
-    for (int i = lane; i < DP * kLaRow; i += 64) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    for (int i = tid; i < DP * kLaRow; i += 64 * kLsWaves) {
         (&Kt[0][0])[i] = (f16)0.0f;
         (&Vt[0][0])[i] = (f16)0.0f;
     }
-    f32x16 acc[TD][TD];
+    f32x16 acc[MYT];
 #pragma unroll
-    for (int i = 0; i < TD; ++i)
+    for (int u = 0; u < MYT; ++u)
 #pragma unroll
-        for (int j = 0; j < TD; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    float ks[(DP + 63) / 64];
-#pragma unroll
-    for (int i = 0; i < (DP + 63) / 64; ++i) ks[i] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[u][r] = 0.0f;
+    float ks = 0.0f;  // ksum[tid] for tid < D
 
     const int t_begin = c * T, t_end = min(N, t_begin + T);
     const f16 * kb = k + (int64_t)b * N * ld + (int64_t)h * D;
@@ -86,7 +95,7 @@ __global__ __launch_bounds__(64) void la_state_kernel(const f16 * __restrict__ k
     for (int t0 = t_begin; t0 < t_end; t0 += kLaSub) {
         __syncthreads();
         if (vec) {
-            for (int idx = lane; idx < kLaSub * G; idx += 64) {
+            for (int idx = tid; idx < kLaSub * G; idx += 64 * kLsWaves) {
                 const int t = idx / G, g = idx - t * G;
                 const int gt = t0 + t;
                 f16x8 kv, vv;
@@ -104,7 +113,7 @@ __global__ __launch_bounds__(64) void la_state_kernel(const f16 * __restrict__ k
                 }
             }
         } else {
-            for (int idx = lane; idx < kLaSub * D; idx += 64) {
+            for (int idx = tid; idx < kLaSub * D; idx += 64 * kLsWaves) {
                 const int t = idx / D, d = idx - t * D;
                 const int gt = t0 + t;
                 f16 kv = (f16)0.0f, vv = (f16)0.0f;
@@ -117,64 +126,86 @@ __global__ __launch_bounds__(64) void la_state_kernel(const f16 * __restrict__ k
             }
         }
         __syncthreads();
+        if (tid < D) {
+            float sum = 0.0f;
+            for (int t = 0; t < kLaSub; t += 8) {
+                const f16x8 x = *reinterpret_cast<const f16x8 *>(&Kt[tid][t]);
 #pragma unroll
-        for (int i = 0; i < (DP + 63) / 64; ++i) {
-            const int d = lane + 64 * i;
-            if (d < D) {
-                float s = 0.0f;
-                for (int t = 0; t < kLaSub; t += 8) {
-                    const f16x8 x = *reinterpret_cast<const f16x8 *>(&Kt[d][t]);
+                for (int e = 0; e < 8; ++e) sum += (float)x[e];
+            }
+            ks += sum;
+        }
+        if constexpr (kSplitSteps) {
+            const int col = 16 * w + 8 * (lane >> 5);
+            const f16x8 af = *reinterpret_cast<const f16x8 *>(&Kt[lane & 31][col]);
+            const f16x8 bf = *reinterpret_cast<const f16x8 *>(&Vt[lane & 31][col]);
+            acc[0] = mfma_32x32x16(af, bf, acc[0]);
+        } else {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) s += (float)x[e];
+            for (int kk = 0; kk < kLaSub; kk += 16) {
+                const int col = kk + 8 * (lane >> 5);
+#pragma unroll
+                for (int u = 0; u < MYT; ++u) {
+                    const int tile = w + u * kLsWaves;
+                    if (tile < NTILE) {
+                        const int i = tile / TD, j = tile - (tile / TD) * TD;
+                        const f16x8 af = *reinterpret_cast<const f16x8 *>(&Kt[i * 32 + (lane & 31)][col]);
+                        const f16x8 bf = *reinterpret_cast<const f16x8 *>(&Vt[j * 32 + (lane & 31)][col]);
+                        acc[u] = mfma_32x32x16(af, bf, acc[u]);
+                    }
                 }
-                ks[i] += s;
             }
         }
-#pragma unroll
-        for (int kk = 0; kk < kLaSub; kk += 16) {
-            const int col = kk + 8 * (lane >> 5);
-            f16x8 af[TD], bf[TD];
-#pragma unroll
-            for (int i = 0; i < TD; ++i) af[i] = *reinterpret_cast<const f16x8 *>(&Kt[i * 32 + (lane & 31)][col]);
-#pragma unroll
-            for (int j = 0; j < TD; ++j) bf[j] = *reinterpret_cast<const f16x8 *>(&Vt[j * 32 + (lane & 31)][col]);
-#pragma unroll
-            for (int i = 0; i < TD; ++i)
-#pragma unroll
-                for (int j = 0; j < TD; ++j) acc[i][j] = mfma_32x32x16(af[i], bf[j], acc[i][j]);
-        }
     }
-    // acc[i][j]: lane holds r = j*32 + (lane & 31) and d = i*32 + 8*(q/4) + 4*(lane/32) + q%4.
+    // acc tile (i, j): lane holds r = j*32 + (lane & 31) and d = i*32 + 8*(q/4) + 4*(lane/32) + q%4.
     const int E = (D + 1) * D;
     float * out = part + (((int64_t)b * H + h) * nch + c) * E;
+    float m = 0.0f;
+    if constexpr (kSplitSteps) {
 #pragma unroll
-    for (int i = 0; i < TD; ++i)
+        for (int q = 0; q < 16; ++q) red[w][8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)][lane & 31] = acc[0][q];
+        __syncthreads();
+        for (int e = tid; e < 32 * 32; e += 64 * kLsWaves) {
+            const int r = e >> 5, d = e & 31;
+            float a = 0.0f;
 #pragma unroll
-        for (int j = 0; j < TD; ++j) {
+            for (int ww = 0; ww < kLsWaves; ++ww) a += red[ww][d][r];
+            if (r < D && d < D) {
+                out[r * D + d] = a;
+                m = fmaxf(m, fabsf(a));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < MYT; ++u) {
+            const int tile = w + u * kLsWaves;
+            if (tile >= NTILE) continue;
+            const int i = tile / TD, j = tile - (tile / TD) * TD;
             const int r = j * 32 + (lane & 31);
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int d = i * 32 + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-                if (r < D && d < D) out[r * D + d] = acc[i][j][q];
+                if (r < D && d < D) {
+                    out[r * D + d] = acc[u][q];
+                    m = fmaxf(m, fabsf(acc[u][q]));
+                }
             }
         }
-#pragma unroll
-    for (int i = 0; i < (DP + 63) / 64; ++i) {
-        const int d = lane + 64 * i;
-        if (d < D) out[D * D + d] = ks[i];
     }
-    // max |entry| of this partial (padding entries are zero)
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < TD; ++i)
-#pragma unroll
-        for (int j = 0; j < TD; ++j)
-#pragma unroll
-            for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(acc[i][j][q]));
-#pragma unroll
-    for (int i = 0; i < (DP + 63) / 64; ++i) m = fmaxf(m, ks[i]);
+    if (tid < D) {
+        out[D * D + tid] = ks;
+        m = fmaxf(m, ks);
+    }
+    // max |entry| of this partial
     m = wave_max(m);
-    if (lane == 0) pmax[((int64_t)b * H + h) * nch + c] = m;
+    if (lane == 0) wmax[w] = m;
+    __syncthreads();
+    if (tid == 0) {
+        float mm = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < kLsWaves; ++ww) mm = fmaxf(mm, wmax[ww]);
+        pmax[((int64_t)b * H + h) * nch + c] = mm;
+    }
 }
 
 // Sums the chunk partials in fixed order and writes the state 2^k S, transposed
@@ -1327,10 +1358,11 @@ hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v
     note_kernel(apply32 ? "la_state_kernel + la_reduce_kernel + la_apply32_kernel"
                         : "la_state_kernel + la_reduce_kernel + la_apply_kernel");
     const int td = (D + 31) / 32;
-    if (td == 1) hipLaunchKernelGGL((la_state_kernel<1>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
-    else if (td == 2) hipLaunchKernelGGL((la_state_kernel<2>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
-    else if (td == 3) hipLaunchKernelGGL((la_state_kernel<3>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
-    else hipLaunchKernelGGL((la_state_kernel<4>), g1, dim3(64), 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
+    const dim3 t1(64 * kLsWaves);
+    if (td == 1) hipLaunchKernelGGL((la_state_kernel<1>), g1, t1, 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
+    else if (td == 2) hipLaunchKernelGGL((la_state_kernel<2>), g1, t1, 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
+    else if (td == 3) hipLaunchKernelGGL((la_state_kernel<3>), g1, t1, 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
+    else hipLaunchKernelGGL((la_state_kernel<4>), g1, t1, 0, s, kq, vq, ld, N, H, D, T, nch, vec_kv, part, pmax);
     hipLaunchKernelGGL(la_reduce_kernel, dim3((NP * KP + 255) / 256, B * H), dim3(256), 0, s, part, pmax, nch, D,
                        NP, KP, shi, slo);
     f16 * oo = reinterpret_cast<f16 *>(out);

@@ -147,7 +147,7 @@ def test_ln_modulate(L, C):
 
 
 @pytest.mark.parametrize("B,N,H,D", [(2, 1024, 36, 32), (2, 4096, 16, 72), (1, 256, 16, 72), (1, 5, 1, 2),
-                                     (2, 300, 3, 7)])
+                                     (2, 300, 3, 7), (1, 200, 4, 48), (1, 130, 2, 112), (1, 70, 3, 24)])
 def test_linear_attention(L, B, N, H, D):
     rng = np.random.default_rng(N + D)
     C = H * D
