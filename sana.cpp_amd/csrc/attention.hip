@@ -49,7 +49,16 @@ SANA_DEV int la_state_exponent(float m) {
 // their maxima, in chunk order (every kernel computes the same k from it).
 SANA_DEV float la_bound(const float * __restrict__ pmax, int nch) {
     float m = 0.0f;
-    for (int c = 0; c < nch; ++c) m += pmax[c];
+    int c = 0;
+    // eight loads in flight, summed in chunk order
+    for (; c + 8 <= nch; c += 8) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = pmax[c + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) m += x[u];
+    }
+    for (; c < nch; ++c) m += pmax[c];
     return m;
 }
 
@@ -92,24 +101,40 @@ __global__ __launch_bounds__(64 * kLsWaves) void la_state_kernel(const f16 * __r
     const f16 * kb = k + (int64_t)b * N * ld + (int64_t)h * D;
     const f16 * vb = v + (int64_t)b * N * ld + (int64_t)h * D;
     const int G = D / 8;
+    // vec: one item per thread = 8 head dims (group g) of 4 consecutive tokens,
+    // loaded for the next sub-chunk while the MFMAs of this one run, written to
+    // LDS as 8-byte runs of 4 tokens (D <= 112: at most 64 x 14 / 4 = 224 items)
+    const int item_t = tid / max(G, 1), item_g = tid - item_t * max(G, 1);
+    const bool has_item = vec && tid < (kLaSub / 4) * G;
+    f16x8 kreg[4], vreg[4];
+    auto load_item = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int gt = t0 + 4 * item_t + u;
+            if (gt < t_end) {
+                kreg[u] = *reinterpret_cast<const f16x8 *>(kb + (int64_t)gt * ld + item_g * 8);
+                vreg[u] = *reinterpret_cast<const f16x8 *>(vb + (int64_t)gt * ld + item_g * 8);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) kreg[u][e] = vreg[u][e] = (f16)0.0f;
+            }
+        }
+    };
+    if (has_item && t_begin < t_end) load_item(t_begin);
     for (int t0 = t_begin; t0 < t_end; t0 += kLaSub) {
         __syncthreads();
         if (vec) {
-            for (int idx = tid; idx < kLaSub * G; idx += 64 * kLsWaves) {
-                const int t = idx / G, g = idx - t * G;
-                const int gt = t0 + t;
-                f16x8 kv, vv;
-                if (gt < t_end) {
-                    kv = *reinterpret_cast<const f16x8 *>(kb + (int64_t)gt * ld + g * 8);
-                    vv = *reinterpret_cast<const f16x8 *>(vb + (int64_t)gt * ld + g * 8);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) kv[e] = vv[e] = (f16)0.0f;
-                }
+            if (has_item) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    Kt[g * 8 + e][t] = kv[e] > (f16)0.0f ? kv[e] : (f16)0.0f;
-                    Vt[g * 8 + e][t] = vv[e];
+                    f16x4 k4, v4;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        k4[u] = kreg[u][e] > (f16)0.0f ? kreg[u][e] : (f16)0.0f;
+                        v4[u] = vreg[u][e];
+                    }
+                    *reinterpret_cast<f16x4 *>(&Kt[item_g * 8 + e][4 * item_t]) = k4;
+                    *reinterpret_cast<f16x4 *>(&Vt[item_g * 8 + e][4 * item_t]) = v4;
                 }
             }
         } else {
@@ -126,6 +151,7 @@ __global__ __launch_bounds__(64 * kLsWaves) void la_state_kernel(const f16 * __r
             }
         }
         __syncthreads();
+        if (has_item && t0 + kLaSub < t_end) load_item(t0 + kLaSub);
         if (tid < D) {
             float sum = 0.0f;
             for (int t = 0; t < kLaSub; t += 8) {
@@ -226,7 +252,16 @@ __global__ __launch_bounds__(256) void la_reduce_kernel(const float * __restrict
     if (r <= D && d < D) {
         const int E = (D + 1) * D;
         const float * p = part + (int64_t)bh * nch * E + r * D + d;
-        for (int c = 0; c < nch; ++c) s += p[(int64_t)c * E];
+        int c = 0;
+        // eight loads in flight, summed in chunk order
+        for (; c + 8 <= nch; c += 8) {
+            float x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) x[u] = p[(int64_t)(c + u) * E];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += x[u];
+        }
+        for (; c < nch; ++c) s += p[(int64_t)c * E];
     }
     s *= scale;
     const f16 h = (f16)s;
@@ -658,6 +693,98 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_apply32_kernel(const f16 * _
         }
         apply_store(t0, oa, da);
         if (t0 + 32 < tz) apply_store(t0 + 32, ob, db);
+    }
+}
+
+// la_applyT_kernel: the transposed apply of la_apply32_kernel for other head
+// dims (D % 8 == 0, D + 1 <= 96): O^T[r][t] = [S | ksum] . relu(q)^T with NT
+// 32-row tiles of the reduced hi/lo state as the A operand (rows 0..D-1 S,
+// row D ksum) and KS 16-deep steps over d; 32 tokens per step, staged in LDS
+// and stored as 16-byte pieces of the token rows.
+template <int NT, int KS>
+__global__ __launch_bounds__(64 * kLfWaves) void la_applyT_kernel(const f16 * __restrict__ q, int64_t ldq,
+                                                                  const f16 * __restrict__ shi,
+                                                                  const f16 * __restrict__ slo,
+                                                                  const float * __restrict__ pmax, int nch,
+                                                                  f16 * __restrict__ out, int64_t ldo, int N, int H,
+                                                                  int D, int span) {
+    constexpr int KP = KS * 16, NP = NT * 32, SROW = NP + 8;  // SROW: halves per staged token row
+    __shared__ __attribute__((aligned(16))) f16 ost[kLfWaves][32][SROW];
+    const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5;
+    const int wspan = span / kLfWaves;  // a multiple of 32
+    const int ta = min(N, blockIdx.x * span + w * wspan), tz = min(N, ta + wspan);
+    const float eps = ldexpf(1e-15f, la_state_exponent(la_bound(pmax + (int64_t)bh * nch, nch)));
+    const int64_t sb = (int64_t)bh * NP * KP + (lane & 31) * KP + 8 * hh;
+    f16x8 sa[NT][2][KS];  // [tile][hi|lo][k-step]
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            sa[j][0][kk] = *reinterpret_cast<const f16x8 *>(shi + sb + j * 32 * KP + kk * 16);
+            sa[j][1][kk] = *reinterpret_cast<const f16x8 *>(slo + sb + j * 32 * KP + kk * 16);
+        }
+    // the denominator row D: tile D / 32, element (D % 32) of the lane layout
+    const int jd = D >> 5, rd = D & 31;
+    const int id = 4 * (rd >> 3) + (rd & 3), hd = (rd >> 2) & 1;
+    const f16 * qbase = q + (int64_t)b * N * ldq + (int64_t)h * D + 8 * hh;
+    const int G = D / 8;  // 16-byte pieces per token row
+    f16x8 qf[KS];
+    auto load_q = [&](int t0) {
+        const int tq = min(t0 + (lane & 31), N - 1);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            if (kk * 16 + 8 * hh < D) {
+                qf[kk] = *reinterpret_cast<const f16x8 *>(qbase + (int64_t)tq * ldq + kk * 16);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qf[kk][e] = qf[kk][e] > (f16)0.0f ? qf[kk][e] : (f16)0.0f;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qf[kk][e] = (f16)0.0f;
+            }
+        }
+    };
+    if (ta < tz) load_q(ta);
+    for (int t0 = ta; t0 < tz; t0 += 32) {
+        f32x16 o[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[j][i] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+                for (int j = 0; j < NT; ++j) o[j] = mfma_32x32x16(sa[j][hl][kk], qf[kk], o[j]);
+        // the next step's queries are requested before this step's stores
+        if (t0 + 32 < tz) load_q(t0 + 32);
+        float dv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (j == jd && i == id) dv = o[j][i];
+        const float rden = 1.0f / (__shfl(dv, (lane & 31) | (hd << 5), 64) + eps);
+        // lane: token lane & 31, rows 32 j + 8 i4 + 4 hh + {0..3}
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                f16x4 v4;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v4[u] = (f16)(o[j][4 * i4 + u] * rden);
+                *reinterpret_cast<f16x4 *>(&ost[w][lane & 31][32 * j + 8 * i4 + 4 * hh]) = v4;
+            }
+        __builtin_amdgcn_wave_barrier();
+        for (int it = lane; it < 32 * G; it += 64) {
+            const int tl = it / G, g = it - (it / G) * G;
+            const int t = t0 + tl;
+            if (t < tz)
+                *reinterpret_cast<f16x8 *>(out + ((int64_t)b * N + t) * ldo + (int64_t)h * D + 8 * g) =
+                    *reinterpret_cast<const f16x8 *>(&ost[w][tl][8 * g]);
+        }
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -1314,8 +1441,8 @@ hipError_t linear_attention_chunked(const half_t * q, int64_t ldq, const half_t 
                        reinterpret_cast<const f16 *>(kt), reinterpret_cast<const f16 *>(vt), N, T, nch, part, pmax);
     hipLaunchKernelGGL(la_reduce_kernel, dim3((NP * KP + 255) / 256, B * H), dim3(256), 0, s, part, pmax, nch, D, NP,
                        KP, shi, slo);
-    // apply: 8 waves x 128 tokens per workgroup
-    constexpr int kSpan = 64 * 2 * kLfWaves;
+    // apply: 8 waves x 64 tokens per workgroup
+    constexpr int kSpan = 64 * kLfWaves;
     hipLaunchKernelGGL(la_apply32_kernel, dim3((unsigned)((N + kSpan - 1) / kSpan), (unsigned)(B * H)),
                        dim3(64 * kLfWaves), 0, s, reinterpret_cast<const f16 *>(q), ldq, shi, slo, pmax, nch,
                        reinterpret_cast<f16 *>(out), ldo, N, H, kSpan);
@@ -1367,10 +1494,26 @@ hipError_t linear_attention(const half_t * q, const half_t * k, const half_t * v
                        NP, KP, shi, slo);
     f16 * oo = reinterpret_cast<f16 *>(out);
     if (apply32) {
-        constexpr int kSpan = 64 * 2 * kLfWaves;
+        constexpr int kSpan = 64 * kLfWaves;
         hipLaunchKernelGGL(la_apply32_kernel, dim3((unsigned)((N + kSpan - 1) / kSpan), (unsigned)(B * H)),
                            dim3(64 * kLfWaves), 0, s, qq, ld, shi, slo, pmax, nch, oo, ldo, N, H, kSpan);
         return hipGetLastError();
+    }
+    if (D % 8 == 0 && D + 1 <= 96 && vec_q && ldo % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+        // transposed apply with 16-byte stores of the token rows: 8 waves x 64 tokens
+        constexpr int kSpan = 64 * kLfWaves;
+        const dim3 gt((unsigned)((N + kSpan - 1) / kSpan), (unsigned)(B * H));
+        const dim3 tt(64 * kLfWaves);
+#define SANA_LA_APPLYT(nt, ks)                                                                                    \
+    if (NT == nt && KS == ks) {                                                                                   \
+        hipLaunchKernelGGL((la_applyT_kernel<nt, ks>), gt, tt, 0, s, qq, ld, shi, slo, pmax, nch, oo, ldo, N, H, D, \
+                           kSpan);                                                                                \
+        return hipGetLastError();                                                                                 \
+    }
+        // (NT, KS) of D = 8..88 in steps of 8
+        SANA_LA_APPLYT(1, 1) SANA_LA_APPLYT(1, 2) SANA_LA_APPLYT(2, 2) SANA_LA_APPLYT(2, 3) SANA_LA_APPLYT(2, 4)
+        SANA_LA_APPLYT(3, 4) SANA_LA_APPLYT(3, 5) SANA_LA_APPLYT(3, 6)
+#undef SANA_LA_APPLYT
     }
     const dim3 g3((N + 127) / 128, H, B);
 #define SANA_LA_APPLY(nt, ks)                                                                                     \
