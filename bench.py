@@ -364,7 +364,8 @@ def gemma_prompt_pair(sana_dit, rng, pos_tokens=438, neg_tokens=300):
     sequences encode_prompt_pair runs: the instruction-prefixed positive
     prompt (instruction + 300 - 2 tokens) and the negative prompt (300).
     Seeded N(0, 0.02) weights, one draw per tensor shape shared by the 26
-    layers; mean of 3 pairs after one warm-up."""
+    layers; both sequences in one pass (sana_gemma_encode_pair, as the host
+    encode_prompt_pair runs them); mean of 3 pairs after one warm-up."""
     import numpy as np
     c = sana_dit.GEMMA2_2B
     g = sana_dit.Gemma(c)
@@ -377,12 +378,10 @@ def gemma_prompt_pair(sana_dit, rng, pos_tokens=438, neg_tokens=300):
     g.check_weights()
     pos = rng.integers(0, c["vocab"], size=pos_tokens)
     neg = rng.integers(0, c["vocab"], size=neg_tokens)
-    g.encode(pos)
-    g.encode(neg)
+    g.encode_pair(pos, neg)
     t0 = time.perf_counter()
     for _ in range(3):
-        h = g.encode(pos)
-        g.encode(neg)
+        h, _ = g.encode_pair(pos, neg)
     ms = (time.perf_counter() - t0) * 1e3 / 3
     if not np.isfinite(h).all():
         raise RuntimeError("non-finite Gemma hidden states")

@@ -229,6 +229,13 @@ int sana_gemma_check_weights(sana_gemma * g);
 int sana_gemma_load_gguf(sana_gemma * g, const char * path);
 /* tokens [n] -> hidden [n, hidden] fp32 (host pointers). */
 int sana_gemma_encode(sana_gemma * g, const int32_t * tokens, int64_t n, float * hidden);
+/* Two independent sequences in one pass, as encode_prompt_pair
+ * (src/gemma_encoder.cpp) needs for the prompt and the negative prompt: their
+ * rows share the per-token kernels, attention stays within each sequence.
+ * hidden_a / hidden_b equal what two sana_gemma_encode calls return, bit for
+ * bit.  Each sequence up to 8192 tokens, na + nb <= 16384. */
+int sana_gemma_encode_pair(sana_gemma * g, const int32_t * tokens_a, int64_t na, const int32_t * tokens_b,
+                           int64_t nb, float * hidden_a, float * hidden_b);
 
 /* Measured MFMA ceiling for roofline reports (no counterpart in the reference):
  * `workgroups` x 256 threads (4 waves) run `iters` steps of 8 independent fp16

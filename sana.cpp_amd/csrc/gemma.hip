@@ -20,6 +20,7 @@
 // in fp32.  RMSNorm weights are taken as stored in the GGUF (1 + w).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -189,12 +190,13 @@ struct sana_gemma {
     std::map<std::string, bool> loaded;
     std::vector<std::string> required;
     hipStream_t stream = nullptr;
-    // workspace
-    int64_t ws_T = 0;
+    // workspace: rows of all sequences of one encode, and the per-sequence
+    // attention buffers (V^T, scores, probabilities) back to back
+    int64_t ws_M = 0, ws_vt = 0, ws_att = 0;
     DevMem tok, x32, y32, a16, qkv32, q16, k16, vt16, s32, p16, o16, gu32, g16, out32;
-    // the encoder's kernels as one graph per token count (workspace and weight
-    // pointers are baked in: dropped when either is reallocated)
-    std::map<int64_t, hipGraphExec_t> graphs;
+    // the encoder's kernels as one graph per sequence-length list (workspace
+    // and weight pointers are baked in: dropped when either is reallocated)
+    std::map<std::vector<int64_t>, hipGraphExec_t> graphs;
     ~sana_gemma() {
         for (auto & kv : graphs) (void)hipGraphExecDestroy(kv.second);
         if (stream) (void)hipStreamDestroy(stream);
@@ -300,26 +302,50 @@ void check_ready(const sana_gemma * g) {
         if (!g->loaded.count(n)) throw_err(SANA_ERR_STATE, "gemma weight not set: " + n);
 }
 
-void ensure_workspace(sana_gemma * g, int64_t T) {
-    if (T <= g->ws_T) return;
+// One sequence of an encode: its rows [row0, row0 + T) of the token-major
+// buffers and its offsets into the per-sequence attention buffers.
+struct Seq {
+    int64_t row0, T, Tp, vt_off, att_off;
+};
+
+std::vector<Seq> layout(const sana_gemma * g, const std::vector<int64_t> & lens) {
+    std::vector<Seq> q;
+    int64_t row = 0, vt = 0, att = 0;
+    for (int64_t T : lens) {
+        const int64_t Tp = round_up(T, 64);
+        q.push_back({row, T, Tp, vt, att});
+        row += T;
+        vt += g->Dkv * Tp;
+        att += g->cfg.heads * T * Tp;
+    }
+    return q;
+}
+
+void ensure_workspace(sana_gemma * g, const std::vector<Seq> & q) {
+    const Seq & e = q.back();
+    const int64_t M = e.row0 + e.T, vt = e.vt_off + g->Dkv * e.Tp, att = e.att_off + g->cfg.heads * e.T * e.Tp;
+    if (M <= g->ws_M && vt <= g->ws_vt && att <= g->ws_att) return;
     drop_graphs(g);
     const sana_gemma_config & c = g->cfg;
-    const int64_t H = c.hidden, Tp = round_up(T, 64);
-    g->tok.ensure((size_t)T * 4, false);
-    g->x32.ensure((size_t)T * H * 4, false);
-    g->y32.ensure((size_t)T * H * 4 * 2, false);  // two split-K partials
-    g->a16.ensure((size_t)T * H * 2, false);
-    g->qkv32.ensure((size_t)T * (g->Dq + 2 * g->Dkv) * 4, false);
-    g->q16.ensure((size_t)T * g->Dq * 2, false);
-    g->k16.ensure((size_t)T * g->Dkv * 2, false);
-    g->vt16.ensure((size_t)g->Dkv * Tp * 2, false);
-    g->s32.ensure((size_t)c.heads * T * Tp * 4, false);
-    g->p16.ensure((size_t)c.heads * T * Tp * 2, false);
-    g->o16.ensure((size_t)T * g->Dq * 2, false);
-    g->gu32.ensure((size_t)T * 2 * c.ffn * 4, false);
-    g->g16.ensure((size_t)T * c.ffn * 2, false);
-    g->out32.ensure((size_t)T * H * 4, false);
-    g->ws_T = T;
+    const int64_t H = c.hidden;
+    g->ws_M = std::max(g->ws_M, M);
+    g->ws_vt = std::max(g->ws_vt, vt);
+    g->ws_att = std::max(g->ws_att, att);
+    const size_t R = (size_t)g->ws_M;
+    g->tok.ensure(R * 4, false);
+    g->x32.ensure(R * H * 4, false);
+    g->y32.ensure(R * H * 4 * 2, false);  // two split-K partials
+    g->a16.ensure(R * H * 2, false);
+    g->qkv32.ensure(R * (g->Dq + 2 * g->Dkv) * 4, false);
+    g->q16.ensure(R * g->Dq * 2, false);
+    g->k16.ensure(R * g->Dkv * 2, false);
+    g->vt16.ensure((size_t)g->ws_vt * 2, false);
+    g->s32.ensure((size_t)g->ws_att * 4, false);
+    g->p16.ensure((size_t)g->ws_att * 2, false);
+    g->o16.ensure(R * g->Dq * 2, false);
+    g->gu32.ensure(R * 2 * c.ffn * 4, false);
+    g->g16.ensure(R * c.ffn * 2, false);
+    g->out32.ensure(R * H * 4, false);
 }
 
 void gemm(const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
@@ -389,50 +415,113 @@ void norm(const sana_gemma * g, const float * y, int64_t M, const DevMem & w, in
 // 2B shapes with 438 + 300 tokens: 14.3 ms unsplit, 10.7 ms in two, 10.9 ms in four).
 int split_k(int64_t K) { return K % 128 == 0 && K / 2 >= 512 ? 2 : 1; }
 
-// decode_embeddings (src/gemma_encoder.cpp:95-152) on device token ids.
-void encode(sana_gemma * g, int64_t T, hipStream_t s) {
+// decode_embeddings (src/gemma_encoder.cpp:95-152) on device token ids, for
+// one or more independent sequences at once: their rows share every
+// per-token kernel (norms, the projections, GeGLU) and only the attention
+// (RoPE positions, scores, softmax, P.V) runs per sequence.  Each row's
+// result is bit-identical to encoding its sequence alone: the per-row
+// arithmetic and its order do not depend on the other rows.
+void encode(sana_gemma * g, const std::vector<Seq> & seqs, hipStream_t s) {
     const sana_gemma_config & c = g->cfg;
-    const int64_t H = c.hidden, F = c.ffn, d = c.head_dim, nh = c.heads, nkv = c.kv_heads, Tp = round_up(T, 64);
+    const int64_t H = c.hidden, F = c.ffn, d = c.head_dim, nh = c.heads, nkv = c.kv_heads;
     const int64_t Dq = g->Dq, Dkv = g->Dkv, Dqkv = Dq + 2 * Dkv, grp = nh / nkv;
-    hipLaunchKernelGGL(gemma_embed_kernel, dim3(blocks_for(T * H)), dim3(256), 0, s, g->tok.as<int32_t>(),
-                       g->emb16.as<f16>(), g->x32.as<float>(), (int)T, (int)H, std::sqrt((float)H));
+    const int64_t M = seqs.back().row0 + seqs.back().T;
+    hipLaunchKernelGGL(gemma_embed_kernel, dim3(blocks_for(M * H)), dim3(256), 0, s, g->tok.as<int32_t>(),
+                       g->emb16.as<f16>(), g->x32.as<float>(), (int)M, (int)H, std::sqrt((float)H));
     launch_check(hipGetLastError(), "gemma embed");
     half_t * a16 = g->a16.as<half_t>();
     for (int64_t l = 0; l < c.layers; ++l) {
         LayerDev & L = *g->layers[l];
-        norm(g, g->x32.as<float>(), T, L.n_attn, 0, a16, nullptr, s);
-        gemm(a16, H, L.wqkv.as<half_t>(), H, T, Dqkv, H, nullptr, 0, g->qkv32.as<float>(), Dqkv, s);
-        {
-            const int64_t n = T * (nh + nkv) * (d / 2) + nkv * d * Tp;
-            hipLaunchKernelGGL(gemma_qkv_kernel, dim3(blocks_for(n)), dim3(256), 0, s, g->qkv32.as<float>(), (int)T,
-                               (int)Tp, (int)nh, (int)nkv, (int)d, c.rope_theta, c.query_scale, g->q16.as<f16>(),
-                               g->k16.as<f16>(), g->vt16.as<f16>());
-            launch_check(hipGetLastError(), "gemma qkv");
-        }
-        // scores of all heads in one launch: head h uses K head h / grp
-        gemm_batched(g->q16.as<half_t>(), Dq, d, g->k16.as<half_t>(), Dkv, d, (int)grp, T, T, d, nullptr, 0, 0,
-                     g->s32.as<float>(), Tp, T * Tp, (int)nh, s);
+        norm(g, g->x32.as<float>(), M, L.n_attn, 0, a16, nullptr, s);
+        gemm(a16, H, L.wqkv.as<half_t>(), H, M, Dqkv, H, nullptr, 0, g->qkv32.as<float>(), Dqkv, s);
         const int window = (c.sliding_window > 0 && l % 2 == 0) ? (int)c.sliding_window : 0;
-        hipLaunchKernelGGL(gemma_softmax_kernel, dim3((unsigned)((nh * T + 3) / 4)), dim3(256), 0, s,
-                           g->s32.as<float>(), g->p16.as<f16>(), (int)nh, (int)T, (int)Tp, c.attn_softcap, window);
-        launch_check(hipGetLastError(), "gemma softmax");
-        gemm_batched(g->p16.as<half_t>(), Tp, T * Tp, g->vt16.as<half_t>(), Tp, d * Tp, (int)grp, T, d, Tp,
-                     g->o16.as<half_t>(), Dq, d, nullptr, 0, 0, (int)nh, s);
+        for (const Seq & q : seqs) {
+            const int64_t T = q.T, Tp = q.Tp;
+            half_t * q16 = g->q16.as<half_t>() + q.row0 * Dq;
+            half_t * k16 = g->k16.as<half_t>() + q.row0 * Dkv;
+            half_t * vt16 = g->vt16.as<half_t>() + q.vt_off;
+            float * s32 = g->s32.as<float>() + q.att_off;
+            half_t * p16 = g->p16.as<half_t>() + q.att_off;
+            const int64_t n = T * (nh + nkv) * (d / 2) + nkv * d * Tp;
+            hipLaunchKernelGGL(gemma_qkv_kernel, dim3(blocks_for(n)), dim3(256), 0, s,
+                               g->qkv32.as<float>() + q.row0 * Dqkv, (int)T, (int)Tp, (int)nh, (int)nkv, (int)d,
+                               c.rope_theta, c.query_scale, reinterpret_cast<f16 *>(q16),
+                               reinterpret_cast<f16 *>(k16), reinterpret_cast<f16 *>(vt16));
+            launch_check(hipGetLastError(), "gemma qkv");
+            // scores of all heads in one launch: head h uses K head h / grp
+            gemm_batched(q16, Dq, d, k16, Dkv, d, (int)grp, T, T, d, nullptr, 0, 0, s32, Tp, T * Tp, (int)nh, s);
+            hipLaunchKernelGGL(gemma_softmax_kernel, dim3((unsigned)((nh * T + 3) / 4)), dim3(256), 0, s, s32,
+                               reinterpret_cast<f16 *>(p16), (int)nh, (int)T, (int)Tp, c.attn_softcap, window);
+            launch_check(hipGetLastError(), "gemma softmax");
+            gemm_batched(p16, Tp, T * Tp, vt16, Tp, d * Tp, (int)grp, T, d, Tp, g->o16.as<half_t>() + q.row0 * Dq,
+                         Dq, d, nullptr, 0, 0, (int)nh, s);
+        }
         const int so = split_k(Dq);
-        gemm_batched(g->o16.as<half_t>(), Dq, Dq / so, L.wo.as<half_t>(), Dq, Dq / so, 1, T, H, Dq / so, nullptr, 0,
-                     0, g->y32.as<float>(), H, T * H, so, s);
-        norm(g, g->y32.as<float>(), T, L.n_post_attn, 1, nullptr, g->x32.as<float>(), s, so);
-        norm(g, g->x32.as<float>(), T, L.n_ffn, 0, a16, nullptr, s);
-        gemm(a16, H, L.wgu.as<half_t>(), H, T, 2 * F, H, nullptr, 0, g->gu32.as<float>(), 2 * F, s);
-        hipLaunchKernelGGL(gemma_geglu_kernel, dim3(blocks_for(T * F)), dim3(256), 0, s, g->gu32.as<float>(), (int)T,
+        gemm_batched(g->o16.as<half_t>(), Dq, Dq / so, L.wo.as<half_t>(), Dq, Dq / so, 1, M, H, Dq / so, nullptr, 0,
+                     0, g->y32.as<float>(), H, M * H, so, s);
+        norm(g, g->y32.as<float>(), M, L.n_post_attn, 1, nullptr, g->x32.as<float>(), s, so);
+        norm(g, g->x32.as<float>(), M, L.n_ffn, 0, a16, nullptr, s);
+        gemm(a16, H, L.wgu.as<half_t>(), H, M, 2 * F, H, nullptr, 0, g->gu32.as<float>(), 2 * F, s);
+        hipLaunchKernelGGL(gemma_geglu_kernel, dim3(blocks_for(M * F)), dim3(256), 0, s, g->gu32.as<float>(), (int)M,
                            (int)F, g->g16.as<f16>());
         launch_check(hipGetLastError(), "gemma geglu");
         const int sd = split_k(F);
-        gemm_batched(g->g16.as<half_t>(), F, F / sd, L.wdown.as<half_t>(), F, F / sd, 1, T, H, F / sd, nullptr, 0, 0,
-                     g->y32.as<float>(), H, T * H, sd, s);
-        norm(g, g->y32.as<float>(), T, L.n_post_ffw, 1, nullptr, g->x32.as<float>(), s, sd);
+        gemm_batched(g->g16.as<half_t>(), F, F / sd, L.wdown.as<half_t>(), F, F / sd, 1, M, H, F / sd, nullptr, 0, 0,
+                     g->y32.as<float>(), H, M * H, sd, s);
+        norm(g, g->y32.as<float>(), M, L.n_post_ffw, 1, nullptr, g->x32.as<float>(), s, sd);
     }
-    norm(g, g->x32.as<float>(), T, g->out_norm, 2, nullptr, g->out32.as<float>(), s);
+    norm(g, g->x32.as<float>(), M, g->out_norm, 2, nullptr, g->out32.as<float>(), s);
+}
+
+// Encodes the token sequences seqs[i] (host ids, lengths lens[i]) into
+// hidden[i] (host, lens[i] x hidden floats) through the cached graph of
+// this length list.
+void run_encode(sana_gemma * g, const std::vector<const int32_t *> & toks, const std::vector<int64_t> & lens,
+                const std::vector<float *> & hidden) {
+    hip_check(hipSetDevice(g->cfg.device), "hipSetDevice");
+    check_ready(g);
+    int64_t total = 0;
+    for (size_t i = 0; i < lens.size(); ++i) {
+        const int64_t n = lens[i];
+        if (n <= 0 || n > 8192) throw_err(SANA_ERR_INVALID_ARGUMENT, "gemma token count must be in [1, 8192]");
+        for (int64_t j = 0; j < n; ++j)
+            if (toks[i][j] < 0 || toks[i][j] >= g->cfg.vocab)
+                throw_err(SANA_ERR_INVALID_ARGUMENT, "gemma token id out of range at position " + std::to_string(j) +
+                                                         (lens.size() > 1 ? " of sequence " + std::to_string(i) : ""));
+        total += n;
+    }
+    if (total > 16384) throw_err(SANA_ERR_INVALID_ARGUMENT, "gemma token count of one encode must be <= 16384");
+    const std::vector<Seq> seqs = layout(g, lens);
+    ensure_workspace(g, seqs);
+    for (size_t i = 0; i < lens.size(); ++i)
+        hip_check(hipMemcpyAsync(g->tok.as<int32_t>() + seqs[i].row0, toks[i], (size_t)lens[i] * 4,
+                                 hipMemcpyHostToDevice, g->stream),
+                  "upload tokens");
+    auto it = g->graphs.find(lens);
+    if (it == g->graphs.end()) {
+        if (g->graphs.size() >= 8) drop_graphs(g);
+        hipGraph_t graph = nullptr;
+        hip_check(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            encode(g, seqs, g->stream);
+        } catch (...) {
+            (void)hipStreamEndCapture(g->stream, &graph);
+            if (graph) (void)hipGraphDestroy(graph);
+            throw;
+        }
+        hip_check(hipStreamEndCapture(g->stream, &graph), "hipStreamEndCapture");
+        hipGraphExec_t exec = nullptr;
+        const hipError_t r = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        hip_check(r, "hipGraphInstantiate");
+        it = g->graphs.emplace(lens, exec).first;
+    }
+    hip_check(hipGraphLaunch(it->second, g->stream), "hipGraphLaunch");
+    for (size_t i = 0; i < lens.size(); ++i)
+        hip_check(hipMemcpyAsync(hidden[i], g->out32.as<float>() + seqs[i].row0 * g->cfg.hidden,
+                                 (size_t)lens[i] * g->cfg.hidden * 4, hipMemcpyDeviceToHost, g->stream),
+                  "download hidden");
+    hip_check(hipStreamSynchronize(g->stream), "gemma encode");
 }
 
 void validate_config(const sana_gemma_config * c) {
@@ -540,39 +629,14 @@ int sana_gemma_load_gguf(sana_gemma * g, const char * path) {
 
 int sana_gemma_encode(sana_gemma * g, const int32_t * tokens, int64_t n, float * hidden) {
     if (!g || !tokens || !hidden) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
-    return guarded([&] {
-        hip_check(hipSetDevice(g->cfg.device), "hipSetDevice");
-        check_ready(g);
-        if (n <= 0 || n > 8192) throw_err(SANA_ERR_INVALID_ARGUMENT, "gemma token count must be in [1, 8192]");
-        for (int64_t i = 0; i < n; ++i)
-            if (tokens[i] < 0 || tokens[i] >= g->cfg.vocab)
-                throw_err(SANA_ERR_INVALID_ARGUMENT, "gemma token id out of range at position " + std::to_string(i));
-        ensure_workspace(g, n);
-        hip_check(hipMemcpyAsync(g->tok.p, tokens, (size_t)n * 4, hipMemcpyHostToDevice, g->stream), "upload tokens");
-        auto it = g->graphs.find(n);
-        if (it == g->graphs.end()) {
-            if (g->graphs.size() >= 8) drop_graphs(g);
-            hipGraph_t graph = nullptr;
-            hip_check(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-            try {
-                encode(g, n, g->stream);
-            } catch (...) {
-                (void)hipStreamEndCapture(g->stream, &graph);
-                if (graph) (void)hipGraphDestroy(graph);
-                throw;
-            }
-            hip_check(hipStreamEndCapture(g->stream, &graph), "hipStreamEndCapture");
-            hipGraphExec_t exec = nullptr;
-            const hipError_t r = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(graph);
-            hip_check(r, "hipGraphInstantiate");
-            it = g->graphs.emplace(n, exec).first;
-        }
-        hip_check(hipGraphLaunch(it->second, g->stream), "hipGraphLaunch");
-        hip_check(hipMemcpyAsync(hidden, g->out32.p, (size_t)n * g->cfg.hidden * 4, hipMemcpyDeviceToHost, g->stream),
-                  "download hidden");
-        hip_check(hipStreamSynchronize(g->stream), "gemma encode");
-    });
+    return guarded([&] { run_encode(g, {tokens}, {n}, {hidden}); });
+}
+
+int sana_gemma_encode_pair(sana_gemma * g, const int32_t * tokens_a, int64_t na, const int32_t * tokens_b,
+                           int64_t nb, float * hidden_a, float * hidden_b) {
+    if (!g || !tokens_a || !tokens_b || !hidden_a || !hidden_b)
+        return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] { run_encode(g, {tokens_a, tokens_b}, {na, nb}, {hidden_a, hidden_b}); });
 }
 
 }  // extern "C"

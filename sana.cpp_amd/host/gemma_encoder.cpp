@@ -287,6 +287,15 @@ struct GemmaEncoder::Impl {
         ck(sana_gemma_encode(model, tokens.data(), (int64_t)tokens.size(), out.data().data()));
         return out;
     }
+
+    // Both sequences in one device pass; the same values as two
+    // decode_embeddings calls.
+    std::pair<Tensor, Tensor> decode_embeddings_pair(const std::vector<int32_t> & a, const std::vector<int32_t> & b) {
+        Tensor oa({a.size(), static_cast<size_t>(hidden)}), ob({b.size(), static_cast<size_t>(hidden)});
+        ck(sana_gemma_encode_pair(model, a.data(), (int64_t)a.size(), b.data(), (int64_t)b.size(),
+                                  oa.data().data(), ob.data().data()));
+        return {std::move(oa), std::move(ob)};
+    }
 };
 
 GemmaEncoder::GemmaEncoder(const GemmaEncoderConfig & config) : impl(std::make_unique<Impl>(config)) {}
@@ -347,13 +356,15 @@ GemmaPromptPair encode_prompt_pair(GemmaEncoder & encoder, const std::string & p
     const size_t chi = m.tok.encode(kComplexHumanInstruction).size();
     const size_t all = chi + L - 2;
     const Padded pos = tokenize_padded(m.tok, std::string(kComplexHumanInstruction) + prompt, all);
-    const Tensor pos_sel = select_rows_first_and_last(m.decode_embeddings(pos.tokens), L);
     size_t pos_real = pos.real > 0 ? 1 : 0;  // row 0 (BOS)
     for (size_t p = all - (L - 1); p < all; ++p)
         if (p < pos.real) ++pos_real;
     // negative: no instruction, padded to L, no selection
     const Padded neg = tokenize_padded(m.tok, negative_prompt, L);
-    const Tensor neg_emb = m.decode_embeddings(neg.tokens);
+    // both prompts through the encoder in one pass
+    std::pair<Tensor, Tensor> emb = m.decode_embeddings_pair(pos.tokens, neg.tokens);
+    const Tensor pos_sel = select_rows_first_and_last(emb.first, L);
+    const Tensor & neg_emb = emb.second;
     GemmaPromptPair r{Tensor({2, L, H}), Tensor({2, 1, L})};
     std::copy(neg_emb.data().begin(), neg_emb.data().end(), r.embeddings.data().begin());
     std::copy(pos_sel.data().begin(), pos_sel.data().end(), r.embeddings.data().begin() + L * H);

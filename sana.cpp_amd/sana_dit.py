@@ -104,6 +104,7 @@ PROTOTYPES = {
     "sana_gemma_check_weights": (ctypes.c_int, [_vp]),
     "sana_gemma_load_gguf": (ctypes.c_int, [_vp, ctypes.c_char_p]),
     "sana_gemma_encode": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "sana_gemma_encode_pair": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _vp, _vp]),
     "sana_vae_decode_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "sana_op_gemm_f32": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, ctypes.c_int, _vp, _i64,
                                         _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
@@ -480,3 +481,12 @@ class Gemma:
         out = np.empty((tokens.size, self.cfg["hidden"]), np.float32)
         check(lib().sana_gemma_encode(self.h, ptr(tokens), tokens.size, ptr(out)))
         return out
+
+    def encode_pair(self, tokens_a, tokens_b):
+        """Both sequences in one pass; equals (encode(a), encode(b))."""
+        a = np.ascontiguousarray(tokens_a, np.int32)
+        b = np.ascontiguousarray(tokens_b, np.int32)
+        oa = np.empty((a.size, self.cfg["hidden"]), np.float32)
+        ob = np.empty((b.size, self.cfg["hidden"]), np.float32)
+        check(lib().sana_gemma_encode_pair(self.h, ptr(a), a.size, ptr(b), b.size, ptr(oa), ptr(ob)))
+        return oa, ob

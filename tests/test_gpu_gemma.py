@@ -61,6 +61,30 @@ def test_encode_vs_oracle(name, T):
         dev.close()
 
 
+@pytest.mark.parametrize("name,Ta,Tb", [("gqa_window", 37, 64), ("gqa_window", 20, 20), ("mqa_softcap", 5, 19),
+                                         ("gemma2_2b_2layers", 438, 300)])
+def test_encode_pair_equals_two_encodes(name, Ta, Tb):
+    """Both sequences in one pass share the per-token kernels; every row must
+    equal the separate encode of its own sequence bit for bit (attention stays
+    within a sequence, RoPE positions restart at 0), and match the oracle."""
+    cfg = CONFIGS[name]
+    w, dev = build(cfg)
+    try:
+        rng = np.random.default_rng(Ta * 1000 + Tb)
+        a = rng.integers(0, cfg["vocab"], size=Ta)
+        b = rng.integers(0, cfg["vocab"], size=Tb)
+        ha, hb = dev.encode_pair(a, b)
+        assert np.array_equal(ha, dev.encode(a))
+        assert np.array_equal(hb, dev.encode(b))
+        assert rel_l2(hb, G.forward(w, cfg, b)) < TOL
+        ha2, hb2 = dev.encode_pair(a, b)   # graph replay
+        assert np.array_equal(ha2, ha) and np.array_equal(hb2, hb)
+        hb3, ha3 = dev.encode_pair(b, a)   # the other order: its own graph
+        assert np.array_equal(ha3, ha) and np.array_equal(hb3, hb)
+    finally:
+        dev.close()
+
+
 def test_graph_replays_and_weight_reload():
     """The encoder runs as one cached graph per token count: interleaved
     lengths replay their own graphs with new tokens, and a weight set after a
@@ -123,6 +147,12 @@ def test_rejects_bad_input():
     try:
         with pytest.raises(sana_dit.SanaError) as e:
             dev.encode(np.array([1, cfg["vocab"]]))
+        assert e.value.code == sana_dit.SANA_ERR_INVALID_ARGUMENT
+        with pytest.raises(sana_dit.SanaError) as e:
+            dev.encode_pair(np.array([1, 2]), np.array([3, -1]))
+        assert e.value.code == sana_dit.SANA_ERR_INVALID_ARGUMENT
+        with pytest.raises(sana_dit.SanaError) as e:
+            dev.encode_pair(np.array([1, 2]), np.array([], np.int64))
         assert e.value.code == sana_dit.SANA_ERR_INVALID_ARGUMENT
         with pytest.raises(sana_dit.SanaError) as e:
             dev.set_weight("blk.0.attn_q.weight", np.zeros((3, 3), np.float32))

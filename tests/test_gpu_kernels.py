@@ -147,7 +147,8 @@ def test_ln_modulate(L, C):
 
 
 @pytest.mark.parametrize("B,N,H,D", [(2, 1024, 36, 32), (2, 4096, 16, 72), (1, 256, 16, 72), (1, 5, 1, 2),
-                                     (2, 300, 3, 7), (1, 200, 4, 48), (1, 130, 2, 112), (1, 70, 3, 24)])
+                                     (2, 300, 3, 7), (1, 200, 4, 48), (1, 130, 2, 112), (1, 70, 3, 24),
+                                     (1, 100, 2, 8), (1, 90, 2, 56), (1, 77, 2, 64), (1, 64, 2, 88)])
 def test_linear_attention(L, B, N, H, D):
     rng = np.random.default_rng(N + D)
     C = H * D
