@@ -401,9 +401,10 @@ typedef void (*StageHook)(void *, int);
 // One block on batch rows [b0, b0 + B) of a Btot-row batch (the whole batch
 // by default); co is the number of such launches running concurrently on
 // other streams (tile choice).
-// extra workgroups of each block LN launch that warm the cache (one per CU:
-// 128 measured 0.05 ms slower per forward, 512 the same)
-constexpr int kWarmWorkgroups = 256;
+// extra workgroups of each block LN launch that warm the cache, dispatched
+// before the rows (1024 px forward: 5.67 ms without the warm-up, 5.58 / 5.52 /
+// 5.50 ms with 128 / 256 / 512 workgroups; 256 dispatched after the rows 5.53)
+constexpr int kWarmWorkgroups = 512;
 
 void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * xbias, hipStream_t s,
                    StageHook hook = nullptr, void * hook_ctx = nullptr, int64_t b0 = 0, int64_t Btot = -1,

@@ -96,9 +96,9 @@ const char * last_kernel();
 // `workgroups` extra workgroups stream the n ranges (16-byte multiples,
 // 16-byte aligned) and discard the data.
 struct CacheWarm {
-    static constexpr int kMax = 4;
-    const void * p[kMax] = {nullptr, nullptr, nullptr, nullptr};
-    int64_t bytes[kMax] = {0, 0, 0, 0};
+    static constexpr int kMax = 6;
+    const void * p[kMax] = {};
+    int64_t bytes[kMax] = {};
     int n = 0, workgroups = 0;
 };
 // warm: optional cache warm-up carried by the same launch (vectorised rows only).

@@ -6,6 +6,7 @@
 
 #include "hip_common.h"
 #include "kernels.h"
+#include "warm.h"
 
 namespace sana {
 namespace {
@@ -71,33 +72,6 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(const float * __restri
 // 4: float4 loads of x and of the modulation rows, 8-byte fp16x4 stores.
 // kMax4 = float4 chunks per lane (C <= 256 * kMax4), so the row and its shift /
 // scale vectors stay in registers.
-struct WarmDev {
-    const f32x4 * p[CacheWarm::kMax];
-    int64_t n16[CacheWarm::kMax];
-};
-
-// Workgroup wg of nwg streams its share of the ranges (four 16-byte loads in
-// flight per thread).  The sum only keeps the loads alive: the empty asm
-// consumes it, so nothing is stored.
-__device__ __forceinline__ void warm_ranges(const WarmDev & w, int wg, int nwg) {
-    const int64_t T = (int64_t)nwg * 256;
-    const int64_t g = (int64_t)wg * 256 + threadIdx.x;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int k = 0; k < CacheWarm::kMax; ++k) {
-        const f32x4 * p = w.p[k];
-        const int64_t n = w.n16[k];
-        int64_t i = g;
-        for (; i + 3 * T < n; i += 4 * T) {
-            const f32x4 v0 = p[i], v1 = p[i + T], v2 = p[i + 2 * T], v3 = p[i + 3 * T];
-            acc += (v0 + v1) + (v2 + v3);
-        }
-        for (; i < n; i += T) acc += p[i];
-    }
-    const float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    asm volatile("" ::"v"(s));
-}
-
 template <int kMax4>
 __global__ __launch_bounds__(256) void ln_modulate_vec_kernel(const float * __restrict__ x, int64_t ldx,
                                                               f16 * __restrict__ out, int64_t ldo, int M, int C,
@@ -106,13 +80,14 @@ __global__ __launch_bounds__(256) void ln_modulate_vec_kernel(const float * __re
                                                               const float * __restrict__ mod_a,
                                                               const float * __restrict__ mod_t, int64_t mod_stride,
                                                               int64_t shift_off, int64_t scale_off, WarmDev warm,
-                                                              int row_blocks) {
-    // workgroups past the rows' carry the cache warm-up
-    if ((int)blockIdx.x >= row_blocks) {
-        warm_ranges(warm, (int)blockIdx.x - row_blocks, (int)gridDim.x - row_blocks);
+                                                              int warm_blocks) {
+    // the first warm_blocks workgroups carry the cache warm-up (dispatched
+    // first, so they run beside the rows instead of after them)
+    if ((int)blockIdx.x < warm_blocks) {
+        warm_ranges(warm, (int)blockIdx.x, warm_blocks);
         return;
     }
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = (blockIdx.x - warm_blocks) * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= M) return;
     const int n4 = C >> 2;
@@ -437,19 +412,9 @@ hipError_t ln_modulate(const float * x, int64_t ldx, half_t * out, int64_t ldo, 
                        const CacheWarm * warm) {
     if (M <= 0 || C <= 0 || C > 64 * kMaxPerLane || ldx < C || ldo < C || rpb <= 0 || !mod_a)
         return hipErrorInvalidValue;
-    WarmDev wd{};
-    int wwg = 0;
-    if (warm && warm->workgroups > 0) {
-        if (warm->n < 0 || warm->n > CacheWarm::kMax || warm->workgroups > 4096) return hipErrorInvalidValue;
-        for (int k = 0; k < warm->n; ++k) {
-            if (warm->bytes[k] < 0 || warm->bytes[k] % 16 || (reinterpret_cast<uintptr_t>(warm->p[k]) & 15) ||
-                (warm->bytes[k] && !warm->p[k]))
-                return hipErrorInvalidValue;
-            wd.p[k] = static_cast<const f32x4 *>(warm->p[k]);
-            wd.n16[k] = warm->bytes[k] / 16;
-        }
-        wwg = warm->workgroups;
-    }
+    WarmDev wd;
+    int wwg;
+    if (make_warm(warm, wd, wwg) != hipSuccess) return hipErrorInvalidValue;
     const bool vec = C % 4 == 0 && ldx % 4 == 0 && ldo % 4 == 0 && mod_stride % 4 == 0 && shift_off % 4 == 0 &&
                      scale_off % 4 == 0 &&
                      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
@@ -461,7 +426,7 @@ hipError_t ln_modulate(const float * x, int64_t ldx, half_t * out, int64_t ldo, 
         note_kernel("ln_modulate_vec_kernel<" #n4 ">");                                                            \
         hipLaunchKernelGGL((ln_modulate_vec_kernel<n4>), dim3((M + 3) / 4 + wwg), dim3(256), 0, s, x, ldx,         \
                            reinterpret_cast<f16 *>(out), ldo, M, C, rpb, eps, gamma, beta, mod_a, mod_t,          \
-                           mod_stride, shift_off, scale_off, wd, (M + 3) / 4);                                    \
+                           mod_stride, shift_off, scale_off, wd, wwg);                                            \
     } while (0)
         const int per = (C / 4 + 63) / 64;  // float4 chunks per lane
         if (per <= 2) SANA_LN_VEC(2);
