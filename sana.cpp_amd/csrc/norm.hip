@@ -233,6 +233,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float * __restrict__ in
         float acc[kRows][2];
 #pragma unroll
         for (int r = 0; r < kRows; ++r) acc[r][0] = acc[r][1] = 0.0f;
+        // unrolled so the weight loads of several k steps are in flight at
+        // once (the weights come from HBM on every forward)
+#pragma unroll 6
         for (int k4 = lane; k4 < k4n; k4 += 64) {
             float4 a[2];
 #pragma unroll
