@@ -334,7 +334,7 @@ void ensure_workspace(sana_gemma * g, const std::vector<Seq> & q) {
     const size_t R = (size_t)g->ws_M;
     g->tok.ensure(R * 4, false);
     g->x32.ensure(R * H * 4, false);
-    g->y32.ensure(R * H * 4 * 2, false);  // two split-K partials
+    g->y32.ensure(R * H * 4 * 4, false);  // up to four split-K partials
     g->a16.ensure(R * H * 2, false);
     g->qkv32.ensure(R * (g->Dq + 2 * g->Dkv) * 4, false);
     g->q16.ensure(R * g->Dq * 2, false);
@@ -408,12 +408,18 @@ void norm(const sana_gemma * g, const float * y, int64_t M, const DevMem & w, in
     launch_check(hipGetLastError(), "gemma norm");
 }
 
-// Split-K factor of a T x H output with contraction K: the down and output
-// projections have long K and only T/64 x H/64 tiles, so their K is cut in
-// two halves (each a multiple of 64 and at least 512 deep) whose fp32
-// partials the following norm kernel sums in fixed order (measured on the
-// 2B shapes with 438 + 300 tokens: 14.3 ms unsplit, 10.7 ms in two, 10.9 ms in four).
-int split_k(int64_t K) { return K % 128 == 0 && K / 2 >= 512 ? 2 : 1; }
+// Split-K factor of an M x H output with contraction K: the down and output
+// projections have long K and few output tiles, so their K is cut into parts
+// (multiples of 64) whose fp32 partials the following norm kernel sums in
+// fixed order.  Four parts of at least 2048 (the 2B down projection: 66.6 ->
+// 46.0 us for a 738-row prompt pair, 2 % slower for 438 + 300 rows encoded
+// apart), else two of at least 512 (the output projection; 2B shapes encoded
+// apart: 14.3 ms unsplit, 10.7 ms in two).  The factor depends on K only, so
+// a row's sums do not depend on the other rows of the encode.
+int split_k(int64_t K) {
+    if (K % 256 == 0 && K / 4 >= 2048) return 4;
+    return K % 128 == 0 && K / 2 >= 512 ? 2 : 1;
+}
 
 // decode_embeddings (src/gemma_encoder.cpp:95-152) on device token ids, for
 // one or more independent sequences at once: their rows share every
