@@ -265,7 +265,9 @@ int sana_gguf_tensor_info(const char * path, int64_t i, char * name, size_t name
                           int * type, uint64_t * offset);
 
 /* ---- kernel-level launchers on device pointers (unit tests, op-level API) ---- */
-/* out = act(A . W^T + bias): A fp16 [M, lda], W fp16 [N, ldw], K % 64 == 0. */
+/* out = act(A . W^T + bias): A fp16 [M, lda], W fp16 [N, ldw], K % 64 == 0;
+ * act 0 none, 1 SiLU, 2 GELU-tanh, 3 gated pairs: W rows interleaved as
+ * (gate, up), out16[m, n / 2] = gelu_tanh(gate) * up for even n (fp16 out only). */
 int sana_hip_gemm(const void * A, int64_t lda, const void * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
                   const float * bias, int act, void * out16, int64_t ldo16, float * out32, int64_t ldo32,
                   void * stream);

@@ -1368,7 +1368,7 @@ int sana_dit_time_kernel(sana_dit * c, int which, int iters, float * avg_ms, dou
 int sana_hip_gemm(const void * A, int64_t lda, const void * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
                   const float * bias, int act, void * out16, int64_t ldo16, float * out32, int64_t ldo32,
                   void * stream) {
-    if (act < 0 || act > 2) return set_err(SANA_ERR_INVALID_ARGUMENT, "act must be 0..2");
+    if (act < 0 || act > 3) return set_err(SANA_ERR_INVALID_ARGUMENT, "act must be 0..3");
     return guarded([&] {
         gemm_store(nullptr, static_cast<const half_t *>(A), lda, static_cast<const half_t *>(W), ldw, M, N, K, bias, act,
                    static_cast<half_t *>(out16), ldo16, out32, ldo32, static_cast<hipStream_t>(stream));

@@ -492,7 +492,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
                     const float4 v1 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8 + 4]);
                     float v[8] = {v0.x + bv[0], v0.y + bv[1], v0.z + bv[2], v0.w + bv[3],
                                   v1.x + bv[4], v1.y + bv[5], v1.z + bv[6], v1.w + bv[7]};
-                    if constexpr (MODE == kGemmStore || MODE == kGemmQKV) {
+                    if constexpr (MODE == kGemmStore && ACT == kActGeglu) {
+                        // gate / up column pairs -> 4 gated outputs at column col / 2
+                        f16x4 h;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) h[e] = (f16)(gelu_tanh_f(v[2 * e]) * v[2 * e + 1]);
+                        f16 * o = reinterpret_cast<f16 *>(p.out16) + (int64_t)row * p.ldo16 + col / 2;
+                        if (vec8) {
+                            *reinterpret_cast<f16x4 *>(o) = h;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (2 * e + 1 < nc) o[e] = h[e];
+                        }
+                    } else if constexpr (MODE == kGemmStore || MODE == kGemmQKV) {
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
                             if constexpr (ACT == kActSilu) v[e] = silu_fast(v[e]);
@@ -683,6 +696,7 @@ hipError_t launch(const GemmParams & p, hipStream_t s) {
     if (p.mode == kGemmQKV) return launch_mode<BM, BN, WM, WN, STAGES, kGemmQKV, SCHED, kActNone>(p, tiles, s);
     if (p.act == kActSilu) return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActSilu>(p, tiles, s);
     if (p.act == kActGelu) return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActGelu>(p, tiles, s);
+    if (p.act == kActGeglu) return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActGeglu>(p, tiles, s);
     return launch_mode<BM, BN, WM, WN, STAGES, kGemmStore, SCHED, kActNone>(p, tiles, s);
 }
 
@@ -713,6 +727,10 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
                               p.vt_ld < p.vt_cols || p.N != p.vt_batch * p.vt_cols || p.M % p.vt_rows))
         return hipErrorInvalidValue;
     if (p.mode == kGemmStore && !p.out16 && !p.out32) return hipErrorInvalidValue;
+    if (p.act < kActNone || p.act > kActGeglu) return hipErrorInvalidValue;
+    if (p.act == kActGeglu && (p.mode != kGemmStore || p.conv || !p.out16 || p.out32 || p.N % 8 ||
+                               p.ldo16 < p.N / 2 || p.batch != 1))
+        return hipErrorInvalidValue;
     if (p.mode == kGemmQKV &&
         (!p.out16 || p.out32 || !p.kt16 || !p.vt16 || p.qkv_c <= 0 || p.qkv_c % 8 || p.N != 3 * p.qkv_c ||
          p.qkv_n <= 0 || p.qkv_n % 8 || p.M % p.qkv_n ||

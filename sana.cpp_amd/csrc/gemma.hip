@@ -12,7 +12,8 @@
 //   o16_h = P_h V_kv(h)                                  all heads in one batched GEMM (B = V^T)
 //   x   += rmsnorm(o16 Wo^T) * post_attention_norm       split-K GEMM + gemma_norm_kernel
 //   a16  = rmsnorm(x) * ffn_norm
-//   gu   = a16 [Wgate; Wup]^T; g16 = gelu_tanh(gate) up  GEMM + gemma_geglu_kernel
+//   g16  = gelu_tanh(a16 Wgate^T) * (a16 Wup^T)        one GEMM, gate / up rows
+//                                                        interleaved, gated in its epilogue
 //   x   += rmsnorm(g16 Wdown^T) * post_ffw_norm          split-K GEMM + gemma_norm_kernel
 // The layers of one encode run as one cached graph per token count.
 // out = rmsnorm(x) * output_norm.  Activations are token-major; GEMM operands
@@ -166,17 +167,8 @@ __global__ __launch_bounds__(256) void gemma_softmax_kernel(const float * __rest
         pr[j] = (j >= j0 && j <= t) ? (f16)(expf(cap * tanhf(sr[j] / cap) - mx) * rs) : (f16)0.0f;
 }
 
-// g16 [T][F] = gelu_tanh(gu[t][f]) * gu[t][F + f] (gate columns first).
-__global__ void gemma_geglu_kernel(const float * __restrict__ gu, int T, int F, f16 * __restrict__ g16) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)T * F) return;
-    const int64_t t = i / F, f = i - t * F;
-    const float g = gu[t * 2 * F + f], u = gu[t * 2 * F + F + f];
-    g16[i] = (f16)(gelu_tanh_f(g) * u);
-}
-
 struct LayerDev {
-    DevMem wqkv, wo, wgu, wdown;          // fp16, [out][in]
+    DevMem wqkv, wo, wgu, wdown;          // fp16, [out][in]; wgu rows gate_0, up_0, gate_1, up_1, ...
     DevMem n_attn, n_post_attn, n_ffn, n_post_ffw;  // fp32
 };
 
@@ -193,7 +185,7 @@ struct sana_gemma {
     // workspace: rows of all sequences of one encode, and the per-sequence
     // attention buffers (V^T, scores, probabilities) back to back
     int64_t ws_M = 0, ws_vt = 0, ws_att = 0;
-    DevMem tok, x32, y32, a16, qkv32, q16, k16, vt16, s32, p16, o16, gu32, g16, out32;
+    DevMem tok, x32, y32, a16, qkv32, q16, k16, vt16, s32, p16, o16, g16, out32;
     // the encoder's kernels as one graph per sequence-length list (workspace
     // and weight pointers are baked in: dropped when either is reallocated)
     std::map<std::vector<int64_t>, hipGraphExec_t> graphs;
@@ -220,6 +212,19 @@ void upload_f16_rows(DevMem & d, const float * src, size_t n, size_t total, size
     std::vector<_Float16> h(n);
     for (size_t i = 0; i < n; ++i) h[i] = (_Float16)src[i];
     copy_to_device(static_cast<_Float16 *>(d.p) + offset, h.data(), n * 2, "upload gemma weight");
+}
+
+// Rows r of src ([n_rows][width] fp32) to rows 2 r + parity of d ([2 n_rows][width] fp16).
+void upload_f16_rows_interleaved(DevMem & d, const float * src, size_t n_rows, size_t width, int parity) {
+    if (!d.p) d.ensure(2 * n_rows * width * 2, false);
+    std::vector<_Float16> h(n_rows * width);
+    for (size_t i = 0; i < h.size(); ++i) h[i] = (_Float16)src[i];
+    hip_check(hipMemcpy2D(static_cast<_Float16 *>(d.p) + parity * width, 2 * width * 2, h.data(), width * 2,
+                          width * 2, n_rows, hipMemcpyHostToDevice),
+              "upload gemma weight");
+    // a pageable copy may return before the data lands: h must outlive it, and
+    // the encoder's non-blocking stream is not ordered after the null stream
+    hip_check(hipStreamSynchronize(nullptr), "upload gemma weight");
 }
 
 void expect(const std::string & name, const int64_t * shape, int ndim, std::vector<int64_t> want) {
@@ -276,10 +281,10 @@ void set_weight(sana_gemma * g, const std::string & n, const float * d, const in
             upload_f16_rows(L.wo, d, (size_t)(H * Dq), (size_t)(H * Dq), 0);
         } else if (s == "ffn_gate.weight") {
             expect(n, sh, nd, {F, H});
-            upload_f16_rows(L.wgu, d, (size_t)(F * H), (size_t)(2 * F * H), 0);
+            upload_f16_rows_interleaved(L.wgu, d, (size_t)F, (size_t)H, 0);
         } else if (s == "ffn_up.weight") {
             expect(n, sh, nd, {F, H});
-            upload_f16_rows(L.wgu, d, (size_t)(F * H), (size_t)(2 * F * H), (size_t)(F * H));
+            upload_f16_rows_interleaved(L.wgu, d, (size_t)F, (size_t)H, 1);
         } else if (s == "ffn_down.weight") {
             expect(n, sh, nd, {H, F});
             upload_f16_rows(L.wdown, d, (size_t)(H * F), (size_t)(H * F), 0);
@@ -343,14 +348,14 @@ void ensure_workspace(sana_gemma * g, const std::vector<Seq> & q) {
     g->s32.ensure((size_t)g->ws_att * 4, false);
     g->p16.ensure((size_t)g->ws_att * 2, false);
     g->o16.ensure(R * g->Dq * 2, false);
-    g->gu32.ensure(R * 2 * c.ffn * 4, false);
     g->g16.ensure(R * c.ffn * 2, false);
     g->out32.ensure(R * H * 4, false);
 }
 
 void gemm(const half_t * A, int64_t lda, const half_t * W, int64_t ldw, int64_t M, int64_t N, int64_t K,
-          half_t * o16, int64_t ldo16, float * o32, int64_t ldo32, hipStream_t s) {
+          half_t * o16, int64_t ldo16, float * o32, int64_t ldo32, hipStream_t s, int act = sana::kActNone) {
     sana::GemmParams p;
+    p.act = act;
     p.A = A;
     p.lda = lda;
     p.W = W;
@@ -467,10 +472,7 @@ void encode(sana_gemma * g, const std::vector<Seq> & seqs, hipStream_t s) {
                      0, g->y32.as<float>(), H, M * H, so, s);
         norm(g, g->y32.as<float>(), M, L.n_post_attn, 1, nullptr, g->x32.as<float>(), s, so);
         norm(g, g->x32.as<float>(), M, L.n_ffn, 0, a16, nullptr, s);
-        gemm(a16, H, L.wgu.as<half_t>(), H, M, 2 * F, H, nullptr, 0, g->gu32.as<float>(), 2 * F, s);
-        hipLaunchKernelGGL(gemma_geglu_kernel, dim3(blocks_for(M * F)), dim3(256), 0, s, g->gu32.as<float>(), (int)M,
-                           (int)F, g->g16.as<f16>());
-        launch_check(hipGetLastError(), "gemma geglu");
+        gemm(a16, H, L.wgu.as<half_t>(), H, M, 2 * F, H, g->g16.as<half_t>(), F, nullptr, 0, s, sana::kActGeglu);
         const int sd = split_k(F);
         gemm_batched(g->g16.as<half_t>(), F, F / sd, L.wdown.as<half_t>(), F, F / sd, 1, M, H, F / sd, nullptr, 0, 0,
                      g->y32.as<float>(), H, M * H, sd, s);

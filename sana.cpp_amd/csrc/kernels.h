@@ -17,7 +17,9 @@ enum GemmMode {
     kGemmQKV = 3,       // fused q|k|v split for linear attention (see GemmParams::qkv_*)
 };
 
-enum GemmAct { kActNone = 0, kActSilu = 1, kActGelu = 2 };
+// kActGeglu (plain stores to out16 only): W rows interleaved as gate / up
+// pairs, out16[m, n / 2] = f16(gelu_tanh(acc[m, n]) * acc[m, n + 1]) for even n.
+enum GemmAct { kActNone = 0, kActSilu = 1, kActGelu = 2, kActGeglu = 3 };
 
 // C[m, n] = sum_k A[m, k] * W[n, k]; fp16 operands, fp32 accumulation.
 // K must be a multiple of 64 and both lda and ldw >= K, multiples of 8.

@@ -93,6 +93,27 @@ def test_gemm_activation(L, act):
     assert rel_l2(host(o32), ref) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 200, 128), (738, 2048, 256), (5, 16, 64)])
+def test_gemm_geglu_pairs(L, M, N, K):
+    """act 3: W rows interleaved as gate / up pairs, the epilogue stores
+    f16(gelu_tanh(gate) * up) at column n / 2 (the Gemma FFN's gating)."""
+    rng = np.random.default_rng(M + N)
+    A = f16(rng.standard_normal((M, K)))
+    W = f16(rng.standard_normal((N, K)) * 0.1)
+    z = A.astype(np.float64) @ W.astype(np.float64).T
+    g, u = z[:, 0::2], z[:, 1::2]
+    ref = 0.5 * g * (1 + np.tanh(np.sqrt(2 / np.pi) * (g + 0.044715 * g ** 3))) * u
+    o16 = torch.empty((M, N // 2), device="cuda", dtype=torch.float16)
+    dA, dW = dev(A, torch.float16), dev(W, torch.float16)
+    L.check(L.lib().sana_hip_gemm(dA.data_ptr(), K, dW.data_ptr(), K, M, N, K, None, 3, o16.data_ptr(), N // 2,
+                                  None, 0, stream()))
+    assert rel_l2(host(o16), ref) < 1e-3
+    o32 = torch.empty((M, N), device="cuda", dtype=torch.float32)
+    rc = L.lib().sana_hip_gemm(dA.data_ptr(), K, dW.data_ptr(), K, M, N, K, None, 3, o16.data_ptr(), N // 2,
+                               o32.data_ptr(), N, stream())
+    assert rc != 0   # gated output is fp16 only
+
+
 @pytest.mark.parametrize("B,Ntok,C,K", [(2, 96, 160, 128), (2, 1000, 1152, 2880),
                                          (2, 8192, 1152, 1152)])   # 128x192 residual tiles
 def test_gemm_residual_gate(L, B, Ntok, C, K):
