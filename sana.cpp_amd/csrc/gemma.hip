@@ -55,12 +55,15 @@ __global__ void gemma_embed_kernel(const int32_t * __restrict__ tok, const f16 *
 // v = y / sqrt(mean(y^2) + eps) * w, y the fixed-order sum of `parts` split-K
 // partials part_stride floats apart; the sum of squares is reduced over the
 // four waves through LDS.  mode 0: out16 = fp16(v); 1: x += v (post-norm
-// residual, out32 = x); 2: out32 = v.
+// residual, out32 = x); 2: out32 = v; 3: x += v as mode 1, then the next
+// pre-norm of the new row, out16 = fp16(x / sqrt(mean(x^2) + eps) * w2), with
+// the same summation order as a separate mode-0 launch on x.
 template <int NC4>
 __global__ __launch_bounds__(256) void gemma_norm_kernel(const float * __restrict__ y, int parts,
                                                          int64_t part_stride, int C, int M,
                                                          const float * __restrict__ w, float eps, int mode,
-                                                         f16 * __restrict__ out16, float * __restrict__ out32) {
+                                                         f16 * __restrict__ out16, float * __restrict__ out32,
+                                                         const float * __restrict__ w2) {
     __shared__ float wsum[4];
     const int row = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -84,6 +87,7 @@ __global__ __launch_bounds__(256) void gemma_norm_kernel(const float * __restric
     __syncthreads();
     const float tot = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
     const float inv = 1.0f / sqrtf(tot / (float)C + eps);
+    float ss2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < NC4; ++i) {
         const int c4 = tid + 256 * i;
@@ -97,13 +101,35 @@ __global__ __launch_bounds__(256) void gemma_norm_kernel(const float * __restric
             *reinterpret_cast<f16x4 *>(out16 + (int64_t)row * C + 4 * c4) = h;
         } else {
             float4 * xr = reinterpret_cast<float4 *>(out32 + (int64_t)row * C) + c4;
-            if (mode == 1) {
+            if (mode == 1 || mode == 3) {
                 const float4 x = *xr;
-                *xr = make_float4(x.x + o[0], x.y + o[1], x.z + o[2], x.w + o[3]);
+                const float4 xn = make_float4(x.x + o[0], x.y + o[1], x.z + o[2], x.w + o[3]);
+                *xr = xn;
+                v[i] = xn;  // the new residual row, for mode 3's second norm
+                ss2 += (xn.x * xn.x + xn.y * xn.y) + (xn.z * xn.z + xn.w * xn.w);
             } else {
                 *xr = make_float4(o[0], o[1], o[2], o[3]);
             }
         }
+    }
+    if (mode != 3) return;
+    ss2 = wave_sum(ss2);
+    __syncthreads();  // every wave has read wsum
+    if (lane == 0) wsum[tid >> 6] = ss2;
+    __syncthreads();
+    const float tot2 = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    const float inv2 = 1.0f / sqrtf(tot2 / (float)C + eps);
+#pragma unroll
+    for (int i = 0; i < NC4; ++i) {
+        const int c4 = tid + 256 * i;
+        if (c4 >= n4) continue;
+        const float4 g = reinterpret_cast<const float4 *>(w2)[c4];
+        f16x4 h;
+        h[0] = (f16)(v[i].x * inv2 * g.x);
+        h[1] = (f16)(v[i].y * inv2 * g.y);
+        h[2] = (f16)(v[i].z * inv2 * g.z);
+        h[3] = (f16)(v[i].w * inv2 * g.w);
+        *reinterpret_cast<f16x4 *>(out16 + (int64_t)row * C + 4 * c4) = h;
     }
 }
 
@@ -397,15 +423,16 @@ void gemm_batched(const half_t * A, int64_t lda, int64_t sa, const half_t * W, i
 }
 
 void norm(const sana_gemma * g, const float * y, int64_t M, const DevMem & w, int mode, half_t * o16, float * o32,
-          hipStream_t s, int parts = 1) {
+          hipStream_t s, int parts = 1, const DevMem * w2 = nullptr) {
     const int64_t C = g->cfg.hidden;
     const dim3 grid((unsigned)M), blk(256);
     f16 * h = reinterpret_cast<f16 *>(o16);
     const float eps = g->cfg.rms_eps;
     const int64_t pstride = M * C;
+    const float * w2p = w2 ? w2->as<float>() : nullptr;
 #define SANA_GEMMA_NORM(n4)                                                                                      \
     hipLaunchKernelGGL((gemma_norm_kernel<n4>), grid, blk, 0, s, y, parts, pstride, (int)C, (int)M, w.as<float>(), \
-                       eps, mode, h, o32)
+                       eps, mode, h, o32, w2p)
     if (C <= 1024) SANA_GEMMA_NORM(1);
     else if (C <= 2048) SANA_GEMMA_NORM(2);
     else SANA_GEMMA_NORM(4);
@@ -443,7 +470,9 @@ void encode(sana_gemma * g, const std::vector<Seq> & seqs, hipStream_t s) {
     half_t * a16 = g->a16.as<half_t>();
     for (int64_t l = 0; l < c.layers; ++l) {
         LayerDev & L = *g->layers[l];
-        norm(g, g->x32.as<float>(), M, L.n_attn, 0, a16, nullptr, s);
+        // the pre-attention norm: layer 0 here, later layers in the previous
+        // layer's last norm launch
+        if (l == 0) norm(g, g->x32.as<float>(), M, L.n_attn, 0, a16, nullptr, s);
         gemm(a16, H, L.wqkv.as<half_t>(), H, M, Dqkv, H, nullptr, 0, g->qkv32.as<float>(), Dqkv, s);
         const int window = (c.sliding_window > 0 && l % 2 == 0) ? (int)c.sliding_window : 0;
         for (const Seq & q : seqs) {
@@ -470,13 +499,18 @@ void encode(sana_gemma * g, const std::vector<Seq> & seqs, hipStream_t s) {
         const int so = split_k(Dq);
         gemm_batched(g->o16.as<half_t>(), Dq, Dq / so, L.wo.as<half_t>(), Dq, Dq / so, 1, M, H, Dq / so, nullptr, 0,
                      0, g->y32.as<float>(), H, M * H, so, s);
-        norm(g, g->y32.as<float>(), M, L.n_post_attn, 1, nullptr, g->x32.as<float>(), s, so);
-        norm(g, g->x32.as<float>(), M, L.n_ffn, 0, a16, nullptr, s);
+        // x += post-attention norm of the projection, then the pre-FFN norm
+        norm(g, g->y32.as<float>(), M, L.n_post_attn, 3, a16, g->x32.as<float>(), s, so, &L.n_ffn);
         gemm(a16, H, L.wgu.as<half_t>(), H, M, 2 * F, H, g->g16.as<half_t>(), F, nullptr, 0, s, sana::kActGeglu);
         const int sd = split_k(F);
         gemm_batched(g->g16.as<half_t>(), F, F / sd, L.wdown.as<half_t>(), F, F / sd, 1, M, H, F / sd, nullptr, 0, 0,
                      g->y32.as<float>(), H, M * H, sd, s);
-        norm(g, g->y32.as<float>(), M, L.n_post_ffw, 1, nullptr, g->x32.as<float>(), s, sd);
+        // x += post-FFN norm, then the next layer's pre-attention norm
+        if (l + 1 < c.layers)
+            norm(g, g->y32.as<float>(), M, L.n_post_ffw, 3, a16, g->x32.as<float>(), s, sd,
+                 &g->layers[l + 1]->n_attn);
+        else
+            norm(g, g->y32.as<float>(), M, L.n_post_ffw, 1, nullptr, g->x32.as<float>(), s, sd);
     }
     norm(g, g->x32.as<float>(), M, g->out_norm, 2, nullptr, g->out32.as<float>(), s);
 }
