@@ -370,39 +370,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
     }
 
     // ------------------------------------------------------------ epilogue
-    if constexpr (MODE == kGemmVT) {
-        // Lane owns column (lane & 31) of each 32x32 block and rows
-        // 8*(r/4) + 4*(lane/32) + r%4.  The (batch, key) split of the column and
-        // the (block, channel) split of the block's first row are divided once;
-        // the 16 rows then step through the channel groups without dividing.
-        f16 * o16 = reinterpret_cast<f16 *>(p.out16);
-#pragma unroll
-        for (int j = 0; j < G::TN; ++j) {
-            const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
-            if (col >= p.N) continue;
-            const int b = col / p.vt_cols, jj = col - b * p.vt_cols;
-#pragma unroll
-            for (int i = 0; i < G::TM; ++i) {
-                const int rb = m0 + wm * G::WTM + i * 32 + 4 * (lane >> 5);
-                const int blk0 = rb / p.vt_rows, rr0 = rb - blk0 * p.vt_rows;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int off = 8 * (r >> 2) + (r & 3);
-                    const int row = rb + off;
-                    if (row >= p.M) continue;
-                    int blk = blk0, rr = rr0 + off;
-                    while (rr >= p.vt_rows) {
-                        rr -= p.vt_rows;
-                        ++blk;
-                    }
-                    float v = acc[i][j][r];
-                    if (p.bias) v += p.bias[row];
-                    o16[((int64_t)(blk * p.vt_batch + b) * p.vt_rows + rr) * p.vt_ld + jj] = (f16)v;
-                }
-            }
-        }
-        return;
-    } else {
+    {
         float * ct = reinterpret_cast<float *>(smem);
         constexpr int LDC = BN + G::CPAD;
         constexpr int ER = G::EPI_ROWS;  // tile rows staged per pass
@@ -419,6 +387,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
         const bool vec8 = p.vec && nc == 8;
         float bv[8];
         if (!active) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bv[e] = 0.0f;
+        } else if (MODE == kGemmVT) {  // bias per row, added below
 #pragma unroll
             for (int e = 0; e < 8; ++e) bv[e] = 0.0f;
         } else if (p.bias && vec8) {
@@ -484,7 +455,45 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
                     *reinterpret_cast<f16x8 *>(dst + ((int64_t)b * C3 + ch) * p.qkv_n + t0) = h;
                 }
             }
-            if (active && MODE != kGemmResidual) {
+            if constexpr (MODE == kGemmVT) {
+                // element (m, n), m = blk * vt_rows + r, n = b * vt_cols + j, goes to
+                // out16[((blk * vt_batch + b) * vt_rows + r) * vt_ld + j]; bias per row.
+                // A chunk inside one batch's columns leaves as two 8-byte stores
+                // (vt_cols need not be a multiple of 8, so j is a multiple of 4 at best).
+                const int vb = col / p.vt_cols, vj = col - vb * p.vt_cols;
+                const bool vec4 = p.vec && nc == 8 && vj + 8 <= p.vt_cols && (vj & 3) == 0 && (p.vt_ld & 3) == 0;
+                f16 * o16 = reinterpret_cast<f16 *>(p.out16);
+                if (active) {
+                    for (int rr = tid / CPR; rr < ER; rr += G::NT / CPR) {
+                        const int row = m0 + pass * ER + rr;
+                        if (row >= p.M) break;
+                        const int blk = row / p.vt_rows, r = row - blk * p.vt_rows;
+                        const float bvr = p.bias ? p.bias[row] : 0.0f;
+                        const float4 v0 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8]);
+                        const float4 v1 = *reinterpret_cast<const float4 *>(&ct[rr * LDC + c8 + 4]);
+                        const float v[8] = {v0.x + bvr, v0.y + bvr, v0.z + bvr, v0.w + bvr,
+                                            v1.x + bvr, v1.y + bvr, v1.z + bvr, v1.w + bvr};
+                        if (vec4) {
+                            f16 * dst = o16 + ((int64_t)(blk * p.vt_batch + vb) * p.vt_rows + r) * p.vt_ld + vj;
+                            f16x4 h0, h1;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                h0[e] = (f16)v[e];
+                                h1[e] = (f16)v[4 + e];
+                            }
+                            *reinterpret_cast<f16x4 *>(dst) = h0;
+                            *reinterpret_cast<f16x4 *>(dst + 4) = h1;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {
+                                if (e >= nc) continue;
+                                const int b = (col + e) / p.vt_cols, jj = col + e - b * p.vt_cols;
+                                o16[((int64_t)(blk * p.vt_batch + b) * p.vt_rows + r) * p.vt_ld + jj] = (f16)v[e];
+                            }
+                        }
+                    }
+                }
+            } else if (active && MODE != kGemmResidual) {
                 for (int rr = tid / CPR; rr < ER; rr += G::NT / CPR) {
                     const int row = m0 + pass * ER + rr;
                     if (row >= p.M) break;
