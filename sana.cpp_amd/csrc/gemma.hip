@@ -15,7 +15,8 @@
 //   g16  = gelu_tanh(a16 Wgate^T) * (a16 Wup^T)        one GEMM, gate / up rows
 //                                                        interleaved, gated in its epilogue
 //   x   += rmsnorm(g16 Wdown^T) * post_ffw_norm          split-K GEMM + gemma_norm_kernel
-// The layers of one encode run as one cached graph per token count.
+// Each post-norm residual add and the pre-norm after it are one launch.
+// The layers of one encode run as one cached graph per sequence-length list.
 // out = rmsnorm(x) * output_norm.  Activations are token-major; GEMM operands
 // fp16 with fp32 accumulation; the residual stream, norms, softmax and RoPE
 // in fp32.  RMSNorm weights are taken as stored in the GGUF (1 + w).
@@ -172,7 +173,10 @@ __global__ void gemma_qkv_kernel(const float * __restrict__ qkv, int T, int Tp, 
 
 // Rows (head, t) of S [nh][T][Tp]: s = cap * tanh(S / cap) over keys j <= t
 // (and j > t - window when window > 0), softmax in fp32 -> P fp16 [nh][T][Tp]
-// with zeros for the masked and padding keys.  One wave per row.
+// with zeros for the masked and padding keys.  One wave per row; lane keeps
+// keys lane + 64 k (k < NJ, Tp <= 64 NJ) in registers, so each soft-capped
+// score and its exponential are computed once.
+template <int NJ>
 __global__ __launch_bounds__(256) void gemma_softmax_kernel(const float * __restrict__ S, f16 * __restrict__ P,
                                                             int nh, int T, int Tp, float cap, int window) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -182,15 +186,28 @@ __global__ __launch_bounds__(256) void gemma_softmax_kernel(const float * __rest
     const int j0 = window > 0 ? max(0, t - window + 1) : 0;
     const float * sr = S + (int64_t)row * Tp;
     f16 * pr = P + (int64_t)row * Tp;
+    float v[NJ];
     float mx = -INFINITY;
-    for (int j = j0 + lane; j <= t; j += 64) mx = fmaxf(mx, cap * tanhf(sr[j] / cap));
+#pragma unroll
+    for (int k = 0; k < NJ; ++k) {
+        const int j = lane + 64 * k;
+        v[k] = (j >= j0 && j <= t) ? cap * tanhf(sr[j] / cap) : -INFINITY;
+        mx = fmaxf(mx, v[k]);
+    }
     mx = wave_max(mx);
     float sum = 0.0f;
-    for (int j = j0 + lane; j <= t; j += 64) sum += expf(cap * tanhf(sr[j] / cap) - mx);
+#pragma unroll
+    for (int k = 0; k < NJ; ++k) {
+        v[k] = v[k] == -INFINITY ? 0.0f : expf(v[k] - mx);
+        sum += v[k];
+    }
     sum = wave_sum(sum);
     const float rs = 1.0f / sum;
-    for (int j = lane; j < Tp; j += 64)
-        pr[j] = (j >= j0 && j <= t) ? (f16)(expf(cap * tanhf(sr[j] / cap) - mx) * rs) : (f16)0.0f;
+#pragma unroll
+    for (int k = 0; k < NJ; ++k) {
+        const int j = lane + 64 * k;
+        if (j < Tp) pr[j] = (f16)(v[k] * rs);
+    }
 }
 
 struct LayerDev {
@@ -490,9 +507,21 @@ void encode(sana_gemma * g, const std::vector<Seq> & seqs, hipStream_t s) {
             launch_check(hipGetLastError(), "gemma qkv");
             // scores of all heads in one launch: head h uses K head h / grp
             gemm_batched(q16, Dq, d, k16, Dkv, d, (int)grp, T, T, d, nullptr, 0, 0, s32, Tp, T * Tp, (int)nh, s);
-            hipLaunchKernelGGL(gemma_softmax_kernel, dim3((unsigned)((nh * T + 3) / 4)), dim3(256), 0, s, s32,
-                               reinterpret_cast<f16 *>(p16), (int)nh, (int)T, (int)Tp, c.attn_softcap, window);
-            launch_check(hipGetLastError(), "gemma softmax");
+            {
+                const dim3 sg((unsigned)((nh * T + 3) / 4)), sb(256);
+                f16 * pp = reinterpret_cast<f16 *>(p16);
+#define SANA_GEMMA_SOFTMAX(nj)                                                                                 \
+    hipLaunchKernelGGL((gemma_softmax_kernel<nj>), sg, sb, 0, s, s32, pp, (int)nh, (int)T, (int)Tp, c.attn_softcap, \
+                       window)
+                // Tp <= 64 NJ (token counts up to 8192: Tp <= 8192)
+                if (Tp <= 512) SANA_GEMMA_SOFTMAX(8);
+                else if (Tp <= 1024) SANA_GEMMA_SOFTMAX(16);
+                else if (Tp <= 2048) SANA_GEMMA_SOFTMAX(32);
+                else if (Tp <= 4096) SANA_GEMMA_SOFTMAX(64);
+                else SANA_GEMMA_SOFTMAX(128);
+#undef SANA_GEMMA_SOFTMAX
+                launch_check(hipGetLastError(), "gemma softmax");
+            }
             gemm_batched(p16, Tp, T * Tp, vt16, Tp, d * Tp, (int)grp, T, d, Tp, g->o16.as<half_t>() + q.row0 * Dq,
                          Dq, d, nullptr, 0, 0, (int)nh, s);
         }
