@@ -15,9 +15,13 @@
 //     wait (the loads of later tiles stay outstanding) and one s_barrier per
 //     k-tile, placed after the tile's last MFMAs are issued.
 //   * LDS rows are 128 bytes; 16-byte chunk c of row r is stored in slot
-//     c ^ (r & 7).  The DMA writes lane l to slot l & 7 of row l >> 3, so lane
-//     l fetches chunk (l & 7) ^ (l >> 3); an MFMA operand read (8 consecutive
-//     rows, one chunk) then touches 8 distinct slots: no bank conflicts.
+//     c ^ ((r >> 1) & 7).  The DMA writes lane l to slot l & 7 of row l >> 3 of
+//     its 8-row block, so lane l fetches the chunk that maps there.  gfx950's
+//     LDS serves a 16-byte read 16 lanes (256 bytes, all 64 banks) per cycle;
+//     an MFMA operand read of 16 consecutive rows at one chunk then hits 16
+//     distinct 16-byte bank groups (row parity picks the half of the 256-byte
+//     window, (r >> 1) & 7 the group within it): no bank conflicts.  The
+//     slot c ^ (r & 7) conflicts two ways (rows r and r + 8 share a group).
 //   * Epilogue staged through LDS: the wave tiles are written to LDS in row
 //     order, then every thread moves 8 consecutive columns with 16-byte
 //     global accesses.
@@ -134,7 +138,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
     // Per-lane global source of each wave load (row clamped into range; the
     // rows past M / N are computed but never stored).
     const int lrow = lane >> 3;
-    const int lchunk = (lane & 7) ^ lrow;
+    // chunk fetched by this lane for 8-row block blk (rows 8 blk .. 8 blk + 7)
+    auto lchunk = [&](int blk) { return (lane & 7) ^ ((4 * (blk & 1) + (lrow >> 1)) & 7); };
     const f16 * asrc[G::A_LOADS];
     const f16 * bsrc[G::B_LOADS];
     // conv: output pixel (image, y, x) of each A load row; asrc is the image's bordered input base
@@ -144,20 +149,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
         const int r = (wid + i * G::NW) * 8 + lrow;
         const int m = min(m0 + r, p.M - 1);
         if constexpr (CONV == 0) {
-            asrc[i] = reinterpret_cast<const f16 *>(p.A) + (int64_t)m * p.lda + lchunk * 8;
+            asrc[i] = reinterpret_cast<const f16 *>(p.A) + (int64_t)m * p.lda + lchunk(wid + i * G::NW) * 8;
         } else {
             const int hw = p.conv_h * p.conv_w;
             const int img = m / hw, rem = m - img * hw;
             cy[i] = rem / p.conv_w;
             cx[i] = rem - cy[i] * p.conv_w;
             const int ih = CONV == 2 ? p.conv_h / 2 : p.conv_h, iw = CONV == 2 ? p.conv_w / 2 : p.conv_w;
-            asrc[i] = reinterpret_cast<const f16 *>(p.A) + (int64_t)img * (ih + 2) * (iw + 2) * p.lda + lchunk * 8;
+            asrc[i] = reinterpret_cast<const f16 *>(p.A) + (int64_t)img * (ih + 2) * (iw + 2) * p.lda +
+                      lchunk(wid + i * G::NW) * 8;
         }
     }
 #pragma unroll
     for (int i = 0; i < G::B_LOADS; ++i) {
         const int r = (wid + i * G::NW) * 8 + lrow;
-        bsrc[i] = reinterpret_cast<const f16 *>(p.W) + (int64_t)min(n0 + r, p.N - 1) * p.ldw + lchunk * 8;
+        bsrc[i] = reinterpret_cast<const f16 *>(p.W) + (int64_t)min(n0 + r, p.N - 1) * p.ldw + lchunk(wid + i * G::NW) * 8;
     }
     auto issue = [&](int kt, int st) {
         unsigned char * base = smem + st * G::STAGE_BYTES;
@@ -205,7 +211,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // Operand read offsets within a stage: row R, chunk ch -> R*128 + ((ch ^ (R & 7)) << 4).
+    // Operand read offsets within a stage: row R, chunk ch -> R*128 + ((ch ^ ((R >> 1) & 7)) << 4).
     const int arow0 = wm * G::WTM + (lane & 31);
     const int brow0 = wn * G::WTN + (lane & 31);
     const int khalf = lane >> 5;
@@ -224,12 +230,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
 #pragma unroll
         for (int i = 0; i < G::TM; ++i) {
             const int R = arow0 + i * 32;
-            af[buf][i] = *reinterpret_cast<const f16x8 *>(sa + R * 128 + ((ch ^ (R & 7)) << 4));
+            af[buf][i] = *reinterpret_cast<const f16x8 *>(sa + R * 128 + ((ch ^ ((R >> 1) & 7)) << 4));
         }
 #pragma unroll
         for (int j = 0; j < G::TN; ++j) {
             const int R = brow0 + j * 32;
-            bf[buf][j] = *reinterpret_cast<const f16x8 *>(sb + R * 128 + ((ch ^ (R & 7)) << 4));
+            bf[buf][j] = *reinterpret_cast<const f16x8 *>(sb + R * 128 + ((ch ^ ((R >> 1) & 7)) << 4));
         }
     };
     auto mfmas = [&](int buf) {
