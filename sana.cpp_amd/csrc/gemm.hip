@@ -436,14 +436,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
             }
             __syncthreads();
             if constexpr (MODE == kGemmQKV) {
-                // k and v sections: items (column, 8-row octet), consecutive lanes on
-                // consecutive octets of one column, so each column's 16-byte stores
-                // form one contiguous token run.  Rows of an octet share a batch
-                // (qkv_n % 8 == 0).  The q section is handled below as a plain store.
+                // k and v sections: items (column, 8-row octet).  32 consecutive
+                // items take 32 consecutive columns of one octet and the next 32 the
+                // same columns one octet further: rows 8 apart are 32 banks apart
+                // (LDC = BN + 4), so a wave's fp32 LDS reads hit 64 distinct banks,
+                // and each column's two octets leave as one 32-byte token run.  Rows
+                // of an octet share a batch (qkv_n % 8 == 0).  The q section is
+                // handled below as a plain store.
                 constexpr int OCT = ER / 8;
+                static_assert(BN % 32 == 0, "32-column item groups");
                 const int C3 = p.qkv_c;
                 for (int item = tid; item < BN * OCT; item += G::NT) {
-                    const int oct = item % OCT, cl = item / OCT;
+                    const int c32 = item % 32, rest = item / 32;
+                    const int oct = rest % OCT, cl = (rest / OCT) * 32 + c32;
                     const int col = n0 + cl, row0 = m0 + pass * ER + oct * 8;
                     if (col >= p.N || row0 >= p.M || col < C3) continue;
                     const bool is_k = col < 2 * C3;
