@@ -784,7 +784,8 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     //  * grids of <= 160 128x128 tiles: shared with a concurrent launch (the
     //    two CFG branches), 64x64 tiles with three stages and early release;
     //    alone, 128x64 tiles with early stage release when that makes >= 256
-    //    tiles, else 64x64 tiles;
+    //    tiles, else 64x64 tiles (three stages and early release for K >= 2048:
+    //    600-row caption projection, K = 2304: 20.3 -> 15.8 us);
     //  * grids of 161..256 128x128 tiles: 128x64 tiles with early release
     //    (738-row Gemma q|k|v 36.8 -> 31.3 us, its split output projection
     //    20.6 -> 17.2 us);
@@ -793,6 +794,9 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     //    launches: 5-12 % faster than 128x128);
     //  * plain stores of N >= 3456 whose 128x192 grid fits one round of slots
     //    where the 128x128 grid does not: 128x192 (1024-row inverted FFN);
+    //  * at most 5 row (or column) tiles of 128 against >= 128 of the other
+    //    (the step's cross K 600 x 32256 and V^T 32256 x 600): 128x128 tiles
+    //    of 8 waves (4 x 2, 32 x 64 per wave): 67.4 -> 60.0 us and 63.2 -> 60.8 us;
     //  * otherwise 128x128 tiles with two stages, two workgroups per CU.
     // (tile counts are scaled by the launches that share the CUs, p.co, and
     // by the products of a batched launch)
@@ -802,9 +806,13 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     if (t128 <= 160) {
         if (co >= 2) return launch<64, 64, 2, 2, 3, 3>(p, s);
         if (tm128 * ((p.N + 63) / 64) >= 256) return launch<128, 64, 2, 2, 2, 3>(p, s);
+        if (p.K >= 2048) return launch<64, 64, 2, 2, 3, 3>(p, s);
         return launch<64, 64, 2, 2, 2, 1>(p, s);
     }
     if (t128 <= 256 && tm128 * ((p.N + 63) / 64) * co >= 256) return launch<128, 64, 2, 2, 2, 3>(p, s);
+    const int64_t tn128 = (p.N + 127) / 128;
+    if (co == 1 && std::min(tm128, tn128) <= 5 && std::max(tm128, tn128) >= 128)
+        return launch<128, 128, 4, 2, 2, 1>(p, s);
     const int64_t t192 = p.N % 192 == 0 ? tm128 * (p.N / 192) * co : 0;
     constexpr int64_t kSlots = 512;
     if (t192 >= kSlots * 3 / 2 ||
