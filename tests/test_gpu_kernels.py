@@ -54,6 +54,9 @@ GEMM_SHAPES = [
     (16300, 1152, 1152),  # 128x192 tiles over many rounds, last row tile partial
     (2000, 1152, 2880),   # 128x64 tiles, last row tile partial
     (600, 4608, 1152),    # cross K of 4 blocks
+    (300, 16384, 256),    # <= 5 row tiles against >= 128 column tiles: 8-wave 128x128 tiles
+    (16384, 300, 256),    # the same with rows and columns swapped
+    (600, 1152, 2304),    # small grid, K >= 2048: 64x64 tiles, 3 stages, early release
     (100, 70, 64),        # ragged M and N
     (7, 3, 64),           # tiny
 ]
@@ -77,9 +80,9 @@ def test_gemm_store(L, M, N, K):
     assert np.abs(got32 - ref).max() < 1e-3 * max(1.0, np.abs(ref).max())
 
 
-@pytest.mark.parametrize("act", [1, 2])
-def test_gemm_activation(L, act):
-    M, N, K = 300, 200, 128
+@pytest.mark.parametrize("act,M,N,K", [(1, 300, 200, 128), (2, 300, 200, 128),
+                                       (2, 600, 1152, 2304)])   # the caption projection's GELU GEMM
+def test_gemm_activation(L, act, M, N, K):
     rng = np.random.default_rng(act)
     A = f16(rng.standard_normal((M, K)))
     W = f16(rng.standard_normal((N, K)) * 0.1)
