@@ -377,7 +377,12 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
     __shared__ __attribute__((aligned(16))) f16 sh[2][2][32][kLfSrow];  // [S|ksum tile][hi|lo][row][d]
     __shared__ __attribute__((aligned(16))) f16 ost[kLfWaves][32][32];  // per-wave output staging [token][dim chunk]
     __shared__ float pmax[kLfWaves];                                   // max |entry| of each wave's partial
-    const int bh = blockIdx.x / splits, sp = blockIdx.x - bh * splits, b = bh / H, h = bh - b * H;
+    // XCD-aware order: workgroup ids are dealt round-robin to the 8 XCDs, so id
+    // goes to position (id % 8) * (n / 8) + id / 8 and the `splits` workgroups of
+    // one (b, h), which read the same K^T / V^T, run on one XCD and share its L2.
+    const int nwg = (int)gridDim.x, per = nwg / 8, id = (int)blockIdx.x;
+    const int pos = id < per * 8 ? (id % 8) * per + id / 8 : id;
+    const int bh = pos / splits, sp = pos - bh * splits, b = bh / H, h = bh - b * H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5;
     const f16 * K = kt + ((int64_t)b * H + h) * 32 * N;  // rows d = 0..31, N tokens each
     const f16 * V = vt + ((int64_t)b * H + h) * 32 * N;
