@@ -97,6 +97,7 @@ struct sana_dit {
     // its fork / join events; same (default) priority as `stream`
     hipStream_t stream2 = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    hipEvent_t ev_head_fork = nullptr, ev_head_join = nullptr;  // forward head beside the step's context
     // recorded on the stream of the last denoise loop after its last step, so
     // sana_dit_loop_model_outputs reads loop_x0 only once the loop has written it
     hipEvent_t ev_loop = nullptr;
@@ -135,6 +136,8 @@ struct sana_dit {
             if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
         if (ev_fork) (void)hipEventDestroy(ev_fork);
         if (ev_join) (void)hipEventDestroy(ev_join);
+        if (ev_head_fork) (void)hipEventDestroy(ev_head_fork);
+        if (ev_head_join) (void)hipEventDestroy(ev_head_join);
         if (ev_loop) (void)hipEventDestroy(ev_loop);
         if (stream2) (void)hipStreamDestroy(stream2);
         if (stream) (void)hipStreamDestroy(stream);
@@ -505,13 +508,53 @@ void enqueue_block(sana_dit * c, int64_t i, int64_t B, int64_t N, const float * 
 }
 
 
-void enqueue_forward(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh, int64_t Ww, const float * xbias,
-                     float * out, hipStream_t s) {
-    const int64_t B = 2 * Bl, N = Hh * Ww;
-    launch_check(sana::patch_embed(latent, (int)Bl, (int)B, (int)c->Cl, (int)N, c->w_patch_t.as<float>(),
+void enqueue_patch_embed(sana_dit * c, const float * latent, int64_t Bl, int64_t N, hipStream_t s) {
+    launch_check(sana::patch_embed(latent, (int)Bl, (int)(2 * Bl), (int)c->Cl, (int)N, c->w_patch_t.as<float>(),
                                    c->b_patch.as<float>(), c->x32.as<float>(), (int)c->C, s),
                  "patch_embed");
-    enqueue_time(c, B, s);
+}
+
+// Start `s2` after the work queued so far on s, and `s` after what is then queued on s2.
+void fork_to(hipEvent_t ev, hipStream_t s, hipStream_t s2) {
+    hip_check(hipEventRecord(ev, s), "hipEventRecord");
+    hip_check(hipStreamWaitEvent(s2, ev, 0), "hipStreamWaitEvent");
+}
+void join_from(hipEvent_t ev, hipStream_t s, hipStream_t s2) {
+    hip_check(hipEventRecord(ev, s2), "hipEventRecord");
+    hip_check(hipStreamWaitEvent(s, ev, 0), "hipStreamWaitEvent");
+}
+
+void enqueue_body(sana_dit * c, int64_t Bl, int64_t Hh, int64_t Ww, const float * xbias, float * out,
+                  hipStream_t s);
+
+// The forward: patch and time embeddings, then the blocks and the final layer.
+// (Running the patch embedding on the second stream beside the time embedding
+// measured no faster.)
+void enqueue_forward(sana_dit * c, const float * latent, int64_t Bl, int64_t Hh, int64_t Ww, const float * xbias,
+                     float * out, hipStream_t s) {
+    enqueue_patch_embed(c, latent, Bl, Hh * Ww, s);
+    enqueue_time(c, 2 * Bl, s);
+    enqueue_body(c, Bl, Hh, Ww, xbias, out, s);
+}
+
+// The step: the caption projection and cross K/V on s, and beside them on the
+// second stream the forward's head (patch and time embeddings), which needs
+// neither; the blocks start when both are done (step 5.564 -> 5.518 ms in one
+// process; the head's ~60 us of small kernels hide behind the context GEMMs).
+void enqueue_step(sana_dit * c, const float * caption, int64_t L, const float * latent, int64_t Bl, int64_t Hh,
+                  int64_t Ww, const float * xbias, float * out, hipStream_t s) {
+    fork_to(c->ev_head_fork, s, c->stream2);
+    enqueue_patch_embed(c, latent, Bl, Hh * Ww, c->stream2);
+    enqueue_time(c, 2 * Bl, c->stream2);
+    enqueue_context(c, caption, false, 2 * Bl, L, s);
+    join_from(c->ev_head_join, s, c->stream2);
+    enqueue_body(c, Bl, Hh, Ww, xbias, out, s);
+}
+
+// Blocks (the CFG pair as two concurrent chains) and the final layer.
+void enqueue_body(sana_dit * c, int64_t Bl, int64_t Hh, int64_t Ww, const float * xbias, float * out,
+                  hipStream_t s) {
+    const int64_t B = 2 * Bl, N = Hh * Ww;
     // The CFG pair runs its two batch rows as two concurrent chains (graph
     // branches): each kernel then covers half the rows, and the two chains fill
     // each other's launch gaps and tails and share the weights through the caches.
@@ -709,6 +752,8 @@ int sana_dit_create(const sana_dit_config * cfg, sana_dit ** out) {
         hip_check(hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking), "hipStreamCreate");
         hip_check(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "hipEventCreate");
         hip_check(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "hipEventCreate");
+        hip_check(hipEventCreateWithFlags(&c->ev_head_fork, hipEventDisableTiming), "hipEventCreate");
+        hip_check(hipEventCreateWithFlags(&c->ev_head_join, hipEventDisableTiming), "hipEventCreate");
         hip_check(hipEventCreateWithFlags(&c->ev_loop, hipEventDisableTiming), "hipEventCreate");
         for (int64_t i = 0; i < c->L_; ++i) c->blocks.emplace_back(new BlockDev());
         // sinusoid frequencies exactly as the reference computes them in fp32
@@ -1004,10 +1049,7 @@ int sana_dit_step_device(sana_dit * c, const float * d_caption, int64_t L, const
         set_t(c, B, t, s);
         run_graph(c, std::make_tuple(2, Bl, Hh, Ww, L, (const void *)d_caption, (const void *)d_bias,
                                      (const void *)d_latent, (const void *)d_out),
-                  s, [&](hipStream_t gs) {
-                      enqueue_context(c, d_caption, false, B, L, gs);
-                      enqueue_forward(c, d_latent, Bl, Hh, Ww, d_bias, d_out, gs);
-                  });
+                  s, [&](hipStream_t gs) { enqueue_step(c, d_caption, L, d_latent, Bl, Hh, Ww, d_bias, d_out, gs); });
         // keep the context state consistent for later sana_dit_forward* calls
         c->ctx_bias = d_bias != nullptr;
         if (d_bias)
