@@ -98,6 +98,7 @@ struct sana_dit {
     hipStream_t stream2 = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     hipEvent_t ev_head_fork = nullptr, ev_head_join = nullptr;  // forward head beside the step's context
+    hipEvent_t ev_ctx = nullptr;                                 // context rows ready (cross V^T on stream2)
     // recorded on the stream of the last denoise loop after its last step, so
     // sana_dit_loop_model_outputs reads loop_x0 only once the loop has written it
     hipEvent_t ev_loop = nullptr;
@@ -138,6 +139,7 @@ struct sana_dit {
         if (ev_join) (void)hipEventDestroy(ev_join);
         if (ev_head_fork) (void)hipEventDestroy(ev_head_fork);
         if (ev_head_join) (void)hipEventDestroy(ev_head_join);
+        if (ev_ctx) (void)hipEventDestroy(ev_ctx);
         if (ev_loop) (void)hipEventDestroy(ev_loop);
         if (stream2) (void)hipStreamDestroy(stream2);
         if (stream) (void)hipStreamDestroy(stream);
@@ -307,8 +309,8 @@ void ensure_context_buffers(sana_dit * c, int64_t B, int64_t L) {
     c->ctx_L = L;
 }
 
-// Caption projection (optional) + cross K/V of all blocks, enqueued on s.
-void enqueue_context(sana_dit * c, const float * caption, bool projected, int64_t B, int64_t L, hipStream_t s) {
+// Caption projection (optional): the normalized fp16 context rows.
+void enqueue_context_rows(sana_dit * c, const float * caption, bool projected, int64_t B, int64_t L, hipStream_t s) {
     const int64_t R = B * L, C = c->C;
     if (!projected) {
         launch_check(sana::to_f16_padded(caption, (int)R, (int)c->Ccap, c->cap16.as<half_t>(), c->Ccap_p, s), "to_f16");
@@ -322,10 +324,18 @@ void enqueue_context(sana_dit * c, const float * caption, bool projected, int64_
     } else {
         launch_check(sana::to_f16_padded(caption, (int)R, (int)C, c->ctx16.as<half_t>(), c->Cp, s), "to_f16");
     }
-    // K of all blocks: [B*L, layers*C]
+}
+
+// Cross K of all blocks: [B*L, layers*C].
+void enqueue_context_k(sana_dit * c, int64_t B, int64_t L, hipStream_t s) {
+    const int64_t R = B * L, C = c->C;
     gemm_store(c, c->ctx16.as<half_t>(), c->Cp, c->w_k_all.as<half_t>(), c->Cp, R, c->L_ * C, c->Cp,
                c->b_k_all.as<float>(), sana::kActNone, c->kc.as<half_t>(), c->L_ * C, nullptr, 0, s);
-    // V^T of all blocks: rows (blk, channel), columns (b, key)
+}
+
+// Cross V^T of all blocks: rows (blk, channel), columns (b, key).
+void enqueue_context_vt(sana_dit * c, int64_t B, int64_t L, hipStream_t s) {
+    const int64_t R = B * L, C = c->C;
     sana::GemmParams p;
     p.A = c->w_v_all.as<half_t>();
     p.lda = c->Cp;
@@ -342,6 +352,13 @@ void enqueue_context(sana_dit * c, const float * caption, bool projected, int64_
     p.vt_batch = (int)B;
     p.vt_ld = c->ctx_Lp;
     launch_check(sana::gemm(p, s), "gemm_vt");
+}
+
+// Caption projection (optional) + cross K/V of all blocks, enqueued on s.
+void enqueue_context(sana_dit * c, const float * caption, bool projected, int64_t B, int64_t L, hipStream_t s) {
+    enqueue_context_rows(c, caption, projected, B, L, s);
+    enqueue_context_k(c, B, L, s);
+    enqueue_context_vt(c, B, L, s);
 }
 
 void ensure_forward_buffers(sana_dit * c, int64_t B, int64_t N) {
@@ -546,7 +563,11 @@ void enqueue_step(sana_dit * c, const float * caption, int64_t L, const float * 
     fork_to(c->ev_head_fork, s, c->stream2);
     enqueue_patch_embed(c, latent, Bl, Hh * Ww, c->stream2);
     enqueue_time(c, 2 * Bl, c->stream2);
-    enqueue_context(c, caption, false, 2 * Bl, L, s);
+    enqueue_context_rows(c, caption, false, 2 * Bl, L, s);
+    // cross K on s and cross V^T on the second stream (after the head)
+    fork_to(c->ev_ctx, s, c->stream2);
+    enqueue_context_k(c, 2 * Bl, L, s);
+    enqueue_context_vt(c, 2 * Bl, L, c->stream2);
     join_from(c->ev_head_join, s, c->stream2);
     enqueue_body(c, Bl, Hh, Ww, xbias, out, s);
 }
@@ -754,6 +775,7 @@ int sana_dit_create(const sana_dit_config * cfg, sana_dit ** out) {
         hip_check(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "hipEventCreate");
         hip_check(hipEventCreateWithFlags(&c->ev_head_fork, hipEventDisableTiming), "hipEventCreate");
         hip_check(hipEventCreateWithFlags(&c->ev_head_join, hipEventDisableTiming), "hipEventCreate");
+        hip_check(hipEventCreateWithFlags(&c->ev_ctx, hipEventDisableTiming), "hipEventCreate");
         hip_check(hipEventCreateWithFlags(&c->ev_loop, hipEventDisableTiming), "hipEventCreate");
         for (int64_t i = 0; i < c->L_; ++i) c->blocks.emplace_back(new BlockDev());
         // sinusoid frequencies exactly as the reference computes them in fp32
