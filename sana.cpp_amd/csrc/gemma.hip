@@ -225,6 +225,11 @@ struct sana_gemma {
     std::map<std::string, bool> loaded;
     std::vector<std::string> required;
     hipStream_t stream = nullptr;
+    // second stream: the attention of every other sequence runs on it, beside
+    // the first sequence's (fork after the q|k|v projection, join before the
+    // output projection of each layer)
+    hipStream_t stream2 = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     // workspace: rows of all sequences of one encode, and the per-sequence
     // attention buffers (V^T, scores, probabilities) back to back
     int64_t ws_M = 0, ws_vt = 0, ws_att = 0;
@@ -234,6 +239,9 @@ struct sana_gemma {
     std::map<std::vector<int64_t>, hipGraphExec_t> graphs;
     ~sana_gemma() {
         for (auto & kv : graphs) (void)hipGraphExecDestroy(kv.second);
+        if (ev_fork) (void)hipEventDestroy(ev_fork);
+        if (ev_join) (void)hipEventDestroy(ev_join);
+        if (stream2) (void)hipStreamDestroy(stream2);
         if (stream) (void)hipStreamDestroy(stream);
     }
 };
@@ -492,7 +500,15 @@ void encode(sana_gemma * g, const std::vector<Seq> & seqs, hipStream_t s) {
         if (l == 0) norm(g, g->x32.as<float>(), M, L.n_attn, 0, a16, nullptr, s);
         gemm(a16, H, L.wqkv.as<half_t>(), H, M, Dqkv, H, nullptr, 0, g->qkv32.as<float>(), Dqkv, s);
         const int window = (c.sliding_window > 0 && l % 2 == 0) ? (int)c.sliding_window : 0;
-        for (const Seq & q : seqs) {
+        // sequences 1, 3, ... on the second stream (their buffers are disjoint)
+        const bool two = seqs.size() > 1;
+        if (two) {
+            hip_check(hipEventRecord(g->ev_fork, s), "hipEventRecord");
+            hip_check(hipStreamWaitEvent(g->stream2, g->ev_fork, 0), "hipStreamWaitEvent");
+        }
+        for (size_t si = 0; si < seqs.size(); ++si) {
+            const Seq & q = seqs[si];
+            const hipStream_t ss = (si & 1) ? g->stream2 : s;
             const int64_t T = q.T, Tp = q.Tp;
             half_t * q16 = g->q16.as<half_t>() + q.row0 * Dq;
             half_t * k16 = g->k16.as<half_t>() + q.row0 * Dkv;
@@ -500,18 +516,18 @@ void encode(sana_gemma * g, const std::vector<Seq> & seqs, hipStream_t s) {
             float * s32 = g->s32.as<float>() + q.att_off;
             half_t * p16 = g->p16.as<half_t>() + q.att_off;
             const int64_t n = T * (nh + nkv) * (d / 2) + nkv * d * Tp;
-            hipLaunchKernelGGL(gemma_qkv_kernel, dim3(blocks_for(n)), dim3(256), 0, s,
+            hipLaunchKernelGGL(gemma_qkv_kernel, dim3(blocks_for(n)), dim3(256), 0, ss,
                                g->qkv32.as<float>() + q.row0 * Dqkv, (int)T, (int)Tp, (int)nh, (int)nkv, (int)d,
                                c.rope_theta, c.query_scale, reinterpret_cast<f16 *>(q16),
                                reinterpret_cast<f16 *>(k16), reinterpret_cast<f16 *>(vt16));
             launch_check(hipGetLastError(), "gemma qkv");
             // scores of all heads in one launch: head h uses K head h / grp
-            gemm_batched(q16, Dq, d, k16, Dkv, d, (int)grp, T, T, d, nullptr, 0, 0, s32, Tp, T * Tp, (int)nh, s);
+            gemm_batched(q16, Dq, d, k16, Dkv, d, (int)grp, T, T, d, nullptr, 0, 0, s32, Tp, T * Tp, (int)nh, ss);
             {
                 const dim3 sg((unsigned)((nh * T + 3) / 4)), sb(256);
                 f16 * pp = reinterpret_cast<f16 *>(p16);
 #define SANA_GEMMA_SOFTMAX(nj)                                                                                 \
-    hipLaunchKernelGGL((gemma_softmax_kernel<nj>), sg, sb, 0, s, s32, pp, (int)nh, (int)T, (int)Tp, c.attn_softcap, \
+    hipLaunchKernelGGL((gemma_softmax_kernel<nj>), sg, sb, 0, ss, s32, pp, (int)nh, (int)T, (int)Tp, c.attn_softcap, \
                        window)
                 // Tp <= 64 NJ (token counts up to 8192: Tp <= 8192)
                 if (Tp <= 512) SANA_GEMMA_SOFTMAX(8);
@@ -523,7 +539,11 @@ void encode(sana_gemma * g, const std::vector<Seq> & seqs, hipStream_t s) {
                 launch_check(hipGetLastError(), "gemma softmax");
             }
             gemm_batched(p16, Tp, T * Tp, vt16, Tp, d * Tp, (int)grp, T, d, Tp, g->o16.as<half_t>() + q.row0 * Dq,
-                         Dq, d, nullptr, 0, 0, (int)nh, s);
+                         Dq, d, nullptr, 0, 0, (int)nh, ss);
+        }
+        if (two) {
+            hip_check(hipEventRecord(g->ev_join, g->stream2), "hipEventRecord");
+            hip_check(hipStreamWaitEvent(s, g->ev_join, 0), "hipStreamWaitEvent");
         }
         const int so = split_k(Dq);
         gemm_batched(g->o16.as<half_t>(), Dq, Dq / so, L.wo.as<half_t>(), Dq, Dq / so, 1, M, H, Dq / so, nullptr, 0,
@@ -627,6 +647,9 @@ int sana_gemma_create(const sana_gemma_config * cfg, sana_gemma ** out) {
         for (int64_t l = 0; l < cfg->layers; ++l) g->layers.push_back(std::make_unique<LayerDev>());
         g->required = required_names(g.get());
         hip_check(hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking), "hipStreamCreate");
+        hip_check(hipStreamCreateWithFlags(&g->stream2, hipStreamNonBlocking), "hipStreamCreate");
+        hip_check(hipEventCreateWithFlags(&g->ev_fork, hipEventDisableTiming), "hipEventCreate");
+        hip_check(hipEventCreateWithFlags(&g->ev_join, hipEventDisableTiming), "hipEventCreate");
         *out = g.release();
     });
 }
