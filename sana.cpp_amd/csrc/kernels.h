@@ -133,7 +133,8 @@ hipError_t patch_embed(const float * latent, int Bl, int B, int Cl, int S, const
 
 // Final layer: LN(eps, no affine) + modulate(shift = emb + T[0], scale = emb + T[1])
 // into y [B*S, C] fp32 (workspace), then proj (Wt [C, Cl] fp32, bias [Cl],
-// Cl <= 32) stored NCHW [B, Cl, S].
+// Cl <= 32) stored NCHW [B, Cl, S].  With C % 384 == 0 and S % 32 == 0 both
+// run in one kernel and y is not written.
 hipError_t final_layer(const float * x, const float * emb, const float * table, const float * Wt, const float * bias,
                        float * y, float * out, int B, int S, int C, int Cl, float eps, hipStream_t s);
 

@@ -393,6 +393,130 @@ __global__ __launch_bounds__(256) void proj_out_kernel(const float * __restrict_
     }
 }
 
+// The final layer in one pass (C % 384 == 0, S % 32 == 0, Cl <= 32): a
+// workgroup of NW waves takes 32 rows of one image, computes their LayerNorm
+// statistics as final_norm_kernel does (one wave per row, the same order of
+// sums) and the image's shift / scale per channel into LDS, then feeds the
+// modulated rows ((x - mean) * inv) * (1 + scale) + shift to
+// v_mfma_f32_32x32x2_f32 as proj_out_kernel does, without the fp32 round trip
+// of the normalized rows.  Wave w takes C / NW channels in 32-channel blocks,
+// the next block's loads issued before the current block's MFMAs; the NW
+// partial tiles are summed in LDS in fixed order.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void final_proj_kernel(const float * __restrict__ x,
+                                                              const float * __restrict__ emb,
+                                                              const float * __restrict__ T,
+                                                              const float * __restrict__ Wt,
+                                                              const float * __restrict__ bias,
+                                                              float * __restrict__ out, int B, int S, int C, int Cl,
+                                                              float eps) {
+    __shared__ float part[NW][32][33];
+    __shared__ float stat[32][2];
+    __shared__ __attribute__((aligned(16))) float mods[2][kMaxPerLane * 64];  // shift, scale per channel
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * 32;
+    const int rows = B * S;
+    {
+        const float * e = emb + (int64_t)(r0 / S) * C;
+        for (int c = threadIdx.x; c < C; c += 64 * NW) {
+            mods[0][c] = e[c] + T[c];
+            mods[1][c] = e[c] + T[C + c];
+        }
+    }
+    // 1. statistics (two-pass mean and variance, as final_norm_kernel)
+    for (int r = w; r < 32; r += NW) {
+        const float * xr = x + (int64_t)min(r0 + r, rows - 1) * C;
+        float v[kMaxPerLane];
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxPerLane; ++i) {
+            const int c = lane + 64 * i;
+            v[i] = c < C ? xr[c] : 0.0f;
+            sum += v[i];
+        }
+        const float mean = wave_sum(sum) / (float)C;
+        float q = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxPerLane; ++i) {
+            const int c = lane + 64 * i;
+            if (c < C) {
+                const float d = v[i] - mean;
+                q += d * d;
+            }
+        }
+        const float inv = 1.0f / sqrtf(wave_sum(q) / (float)C + eps);
+        if (lane == 0) {
+            stat[r][0] = mean;
+            stat[r][1] = inv;
+        }
+    }
+    __syncthreads();
+    // 2. projection: lane (row l % 32, half h = l / 32) feeds channels c + 4 h .. c + 4 h + 3
+    const int rr = min(r0 + (lane & 31), rows - 1);
+    const int h = lane >> 5, n = lane & 31;
+    const float mean = stat[lane & 31][0], inv = stat[lane & 31][1];
+    const float * xr = x + (int64_t)rr * C;
+    const int q = C / NW;  // channels per wave, a multiple of 32
+    const int cb = w * q;
+    float4 xa[2][4];
+    float bw[2][4][4];
+    int cbuf[2] = {0, 0};
+    auto load = [&](int buf, int c0) {
+        cbuf[buf] = c0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = c0 + 8 * u + 4 * h;
+            xa[buf][u] = *reinterpret_cast<const float4 *>(xr + c);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) bw[buf][u][k] = n < Cl ? Wt[(int64_t)(c + k) * Cl + n] : 0.0f;
+        }
+    };
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    auto step = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = cbuf[buf] + 8 * u + 4 * h;
+            const float xv[4] = {xa[buf][u].x, xa[buf][u].y, xa[buf][u].z, xa[buf][u].w};
+            const float4 sh4 = *reinterpret_cast<const float4 *>(&mods[0][c]);
+            const float4 sc4 = *reinterpret_cast<const float4 *>(&mods[1][c]);
+            const float sv[4] = {sh4.x, sh4.y, sh4.z, sh4.w}, cv[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float sh = sv[k], sc = cv[k];
+                const float yv = ((xv[k] - mean) * inv) * (1.0f + sc) + sh;
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(yv, bw[buf][u][k], acc, 0, 0, 0);
+            }
+        }
+    };
+    load(0, cb);
+    for (int c0 = cb; c0 < cb + q; c0 += 64) {
+        const bool second = c0 + 32 < cb + q;
+        if (second) load(1, c0 + 32);
+        step(0);
+        if (second) {
+            if (c0 + 64 < cb + q) load(0, c0 + 64);
+            step(1);
+        }
+    }
+    // lane holds output column n, rows 8*(i/4) + 4*h + i%4
+#pragma unroll
+    for (int i = 0; i < 16; ++i) part[w][8 * (i >> 2) + 4 * h + (i & 3)][n] = acc[i];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 32 * 32; idx += 64 * NW) {
+        const int r = idx >> 5, o = idx & 31;
+        const int row = r0 + r;
+        if (row >= rows || o >= Cl) continue;
+        float v = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) v += part[ww][r][o];
+        v += bias ? bias[o] : 0.0f;
+        const int b = row / S, sidx = row - b * S;
+        out[((int64_t)b * Cl + o) * S + sidx] = v;
+    }
+}
+
 // Plain fp32 proj_out for hidden sizes that are not a multiple of 32.
 __global__ __launch_bounds__(256) void proj_out_scalar_kernel(const float * __restrict__ y,
                                                               const float * __restrict__ Wt,
@@ -500,6 +624,12 @@ hipError_t final_layer(const float * x, const float * emb, const float * table, 
         (reinterpret_cast<uintptr_t>(y) & 15))
         return hipErrorInvalidValue;
     const int rows = B * S;
+    if (C % 384 == 0 && S % 32 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        // one pass: y is not written
+        hipLaunchKernelGGL(final_proj_kernel<12>, dim3((rows + 31) / 32), dim3(64 * 12), 0, s, x, emb, table, Wt,
+                           bias, out, B, S, C, Cl, eps);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(final_norm_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, emb, table, y, B, S, C, eps);
     if (C % 128 == 0)
         hipLaunchKernelGGL(proj_out_kernel, dim3((rows + 31) / 32), dim3(256), 0, s, y, Wt, bias, out, B, S, C, Cl);
