@@ -114,7 +114,7 @@ struct sana_dit {
     // forward workspace
     int64_t ws_M = 0, ws_B = 0;
     DevMem la_kt, la_vt;  // relu(K)^T and V^T per channel, token-contiguous (fused linear attention)
-    DevMem x32, fin32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, la_ws2, d_t, tp, e1, emb, tmod, mod_all,
+    DevMem x32, fin32, xa16, qkv16, o16, r16, q16, hid16, glu16, la_ws, la_ws2, d_t, e1, emb, tmod, mod_all,
         lat_in, np_out;
     DevMem loop_lat[2], loop_x0[2];  // denoise loop: latent ping-pong and converted-output history
     // graphs keyed by (kind, Bl, H, W, L, pointers)
@@ -380,7 +380,6 @@ void ensure_forward_buffers(sana_dit * c, int64_t B, int64_t N) {
         c->la_ws.ensure(sana::linattn_workspace_floats((int)B, (int)N, (int)c->Hs, (int)c->Ds) * 4);
         c->la_ws2.ensure(sana::linattn_workspace_floats(1, (int)N, (int)c->Hs, (int)c->Ds) * 4);
         c->d_t.ensure((size_t)B * 4);
-        c->tp.ensure((size_t)B * 256 * 4);
         c->e1.ensure((size_t)B * C * 4);
         c->emb.ensure((size_t)B * C * 4);
         c->tmod.ensure((size_t)B * 6 * C * 4);
@@ -401,18 +400,18 @@ void enqueue_mod(sana_dit * c, int64_t B, hipStream_t s) {
 
 void enqueue_time(sana_dit * c, int64_t B, hipStream_t s) {
     const int64_t C = c->C;
-    launch_check(sana::timestep_sinusoid(c->d_t.as<float>(), c->freq.as<float>(), (int)B, 128, c->tp.as<float>(), s),
-                 "sinusoid");
-    launch_check(sana::gemv_f32(c->tp.as<float>(), c->w_t1.as<float>(), c->b_t1.as<float>(), c->e1.as<float>(), (int)B,
-                                256, (int)C, 0, s),
+    // the sinusoid is computed inside linear_1, and the per-block modulation
+    // tables are added in the time projection's epilogue
+    launch_check(sana::gemv_sinusoid_f32(c->d_t.as<float>(), c->freq.as<float>(), c->w_t1.as<float>(),
+                                         c->b_t1.as<float>(), c->e1.as<float>(), (int)B, 256, (int)C, s),
                  "time linear_1");
     launch_check(sana::gemv_f32(c->e1.as<float>(), c->w_t2.as<float>(), c->b_t2.as<float>(), c->emb.as<float>(),
                                 (int)B, (int)C, (int)C, 1, s),
                  "time linear_2");
-    launch_check(sana::gemv_f32(c->emb.as<float>(), c->w_tp.as<float>(), c->b_tp.as<float>(), c->tmod.as<float>(),
-                                (int)B, (int)C, (int)(6 * C), 1, s),
+    launch_check(sana::gemv_comb_f32(c->emb.as<float>(), c->w_tp.as<float>(), c->b_tp.as<float>(),
+                                     c->tmod.as<float>(), c->sst_all.as<float>(), (int)c->L_, c->mod_all.as<float>(),
+                                     (int)B, (int)C, (int)(6 * C), 1, s),
                  "time projection");
-    enqueue_mod(c, B, s);
 }
 
 // Stage hook: called after each stage of a block (0 self, 1 cross, 2 ff).

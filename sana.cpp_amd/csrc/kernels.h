@@ -120,12 +120,17 @@ hipError_t rms_norm_f16(const float * x, int64_t ldx, const float * weight, half
 // (columns C..ldo-1 are written as zero).
 hipError_t to_f16_padded(const float * x, int M, int C, half_t * out, int64_t ldo, hipStream_t s);
 
-// Time MLP pieces (fp32): sinusoid [cos(t f_i), sin(t f_i)] of B timesteps read
-// from device memory, f_i = freq[i] for i < half.
-hipError_t timestep_sinusoid(const float * t, const float * freq, int B, int half, float * out, hipStream_t s);
+// Time MLP pieces (fp32).
 // out[b, n] = bias[n] + sum_k act_in(in[b, k]) * W[n, k] (W fp32 [N, K]); act_in: 0 none, 1 silu.
 hipError_t gemv_f32(const float * in, const float * W, const float * bias, float * out, int B, int K, int N,
                     int act_in, hipStream_t s);
+// gemv_f32 of the sinusoid [cos(t_b f_i), sin(t_b f_i)] of B timesteps t read
+// from device memory, f_i = freq[i] for i < K / 2 (K % 8 == 0).
+hipError_t gemv_sinusoid_f32(const float * t, const float * freq, const float * W, const float * bias, float * out,
+                             int B, int K, int N, hipStream_t s);
+// gemv_f32 that also writes comb[l][b][n] = out[b, n] + tables[l][n] for the L tables.
+hipError_t gemv_comb_f32(const float * in, const float * W, const float * bias, float * out, const float * tables,
+                         int L, float * comb, int B, int K, int N, int act_in, hipStream_t s);
 
 // Patch embed: NCHW latent [Bl, Cl, S] (batch b reads latent batch b % Bl) -> tokens [B, S, C] fp32.
 hipError_t patch_embed(const float * latent, int Bl, int B, int Cl, int S, const float * W, const float * bias,

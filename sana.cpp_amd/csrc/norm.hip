@@ -207,23 +207,20 @@ __global__ void to_f16_kernel(const float * __restrict__ x, int M, int C, f16 * 
     out[i] = c < C ? (f16)x[m * C + c] : (f16)0.0f;
 }
 
-// src/transformer.cpp:96-115: [cos(t * f_i), sin(t * f_i)], f_i precomputed on the host.
-__global__ void sinusoid_kernel(const float * __restrict__ t, const float * __restrict__ freq, int B, int half,
-                                float * __restrict__ out) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= B * half) return;
-    const int b = i / half, j = i - b * half;
-    const float v = t[b] * freq[j];
-    out[b * 2 * half + j] = cosf(v);
-    out[b * 2 * half + half + j] = sinf(v);
-}
-
 // out[b, n] = bias[n] + sum_k act(in[b, k]) * W[n, k] (linear_2d,
 // src/common_ops.cpp:114-143); one wave per output n, float4 loads along k,
 // up to 8 batch rows per pass.  K % 4 == 0.
+// SIN: in[b] is the timestep t_b and the row multiplied is its sinusoid
+// [cos(t_b f_j), sin(t_b f_j)] (K = 2 half; src/transformer.cpp:96-115), computed
+// in place.  COMB: the epilogue also writes comb[(l B + b) N + n] = out[b, n] +
+// tables[l N + n] for the L tables (mod_combine_kernel's sums), lane l storing
+// table l.
+template <bool SIN = false, bool COMB = false>
 __global__ __launch_bounds__(256) void gemv_kernel(const float * __restrict__ in, const float * __restrict__ W,
                                                    const float * __restrict__ bias, float * __restrict__ out, int B,
-                                                   int K, int N, int act_in) {
+                                                   int K, int N, int act_in, const float * __restrict__ freq = nullptr,
+                                                   const float * __restrict__ tables = nullptr, int L = 0,
+                                                   float * __restrict__ comb = nullptr) {
     constexpr int kRows = 4;  // outputs per wave: their weight rows are streamed together
     const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kRows;
     const int lane = threadIdx.x & 63;
@@ -240,8 +237,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float * __restrict__ in
             float4 a[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                a[j] = b0 + j < B ? reinterpret_cast<const float4 *>(in + (int64_t)(b0 + j) * K)[k4]
-                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if constexpr (SIN) {
+                    // in = t: element k of the sinusoid is cos (k < half) or sin of t_b * freq[k mod half]
+                    const int half = K >> 1, k0 = 4 * k4;
+                    const bool second = k0 >= half;
+                    const int f0 = second ? k0 - half : k0;
+                    const float tb = b0 + j < B ? in[b0 + j] : 0.0f;
+                    float e4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float v = tb * freq[f0 + e];
+                        e4[e] = second ? sinf(v) : cosf(v);
+                    }
+                    a[j] = b0 + j < B ? make_float4(e4[0], e4[1], e4[2], e4[3]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                } else {
+                    a[j] = b0 + j < B ? reinterpret_cast<const float4 *>(in + (int64_t)(b0 + j) * K)[k4]
+                                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
                 if (act_in == 1) {
                     a[j].x = silu_f(a[j].x); a[j].y = silu_f(a[j].y); a[j].z = silu_f(a[j].z); a[j].w = silu_f(a[j].w);
                 }
@@ -261,7 +273,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float * __restrict__ in
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const float v = wave_sum(acc[r][j]);
-                if (lane == 0 && n0 + r < N && b0 + j < B) out[(int64_t)(b0 + j) * N + n0 + r] = v + (bias ? bias[n0 + r] : 0.0f);
+                const float o = v + (bias ? bias[n0 + r] : 0.0f);
+                if (lane == 0 && n0 + r < N && b0 + j < B) out[(int64_t)(b0 + j) * N + n0 + r] = o;
+                if constexpr (COMB) {
+                    if (n0 + r < N && b0 + j < B)
+                        for (int l = lane; l < L; l += 64)
+                            comb[((int64_t)l * B + b0 + j) * N + n0 + r] = o + tables[(int64_t)l * N + n0 + r];
+                }
             }
     }
 }
@@ -594,18 +612,31 @@ hipError_t to_f16_padded(const float * x, int M, int C, half_t * out, int64_t ld
     return hipGetLastError();
 }
 
-hipError_t timestep_sinusoid(const float * t, const float * freq, int B, int half, float * out, hipStream_t s) {
-    if (B <= 0 || half <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(sinusoid_kernel, dim3((B * half + 255) / 256), dim3(256), 0, s, t, freq, B, half, out);
-    return hipGetLastError();
-}
-
 hipError_t gemv_f32(const float * in, const float * W, const float * bias, float * out, int B, int K, int N,
                     int act_in, hipStream_t s) {
     if (B <= 0 || K <= 0 || N <= 0 || K % 4 ||
         ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemv_kernel, dim3((N + 15) / 16), dim3(256), 0, s, in, W, bias, out, B, K, N, act_in);
+    hipLaunchKernelGGL((gemv_kernel<false, false>), dim3((N + 15) / 16), dim3(256), 0, s, in, W, bias, out, B, K, N,
+                       act_in, nullptr, nullptr, 0, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t gemv_sinusoid_f32(const float * t, const float * freq, const float * W, const float * bias, float * out,
+                             int B, int K, int N, hipStream_t s) {
+    if (B <= 0 || K <= 0 || N <= 0 || K % 8 || (reinterpret_cast<uintptr_t>(W) & 15)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_kernel<true, false>), dim3((N + 15) / 16), dim3(256), 0, s, t, W, bias, out, B, K, N, 0,
+                       freq, nullptr, 0, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t gemv_comb_f32(const float * in, const float * W, const float * bias, float * out, const float * tables,
+                         int L, float * comb, int B, int K, int N, int act_in, hipStream_t s) {
+    if (B <= 0 || K <= 0 || N <= 0 || K % 4 || L <= 0 || !tables || !comb ||
+        ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(W)) & 15))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_kernel<false, true>), dim3((N + 15) / 16), dim3(256), 0, s, in, W, bias, out, B, K, N,
+                       act_in, nullptr, tables, L, comb);
     return hipGetLastError();
 }
 
