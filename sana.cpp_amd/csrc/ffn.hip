@@ -10,6 +10,8 @@
 // one 16-byte load and consecutive lanes read consecutive 16-byte channel
 // groups of the same token (coalesced).  Depthwise weights are stored
 // tap-major [9][E] so the 8 weights of a tap are two float4 loads.
+#include <type_traits>
+
 #include "hip_common.h"
 #include "kernels.h"
 
@@ -145,14 +147,32 @@ hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const flo
     const f16 * xx = reinterpret_cast<const f16 *>(x);
     f16 * oo = reinterpret_cast<f16 *>(out);
     if (vec) {
-        // row segments of 4 tokens: 1024 tokens x 2880 channels take 10.0 us against
-        // 11.3, 10.8 and 17.3 us with segments of 2, 8 and 16 (inputs cycled through 8 buffers)
-        constexpr int XS = 4;
-        const int nseg = (Ww + XS - 1) / XS;
-        if ((int64_t)Hh * nseg > 2147483647 || B > 65535) return hipErrorInvalidValue;
-        note_kernel("dwglu_row_kernel<4>");
-        hipLaunchKernelGGL((dwglu_row_kernel<XS>), dim3((F / 8 + 63) / 64, Hh * nseg, B), dim3(64), 0, s, xx, ldx, wt,
-                           bias, oo, ldo, Hh, Ww, F);
+        // Row segment length by the launch's token count (2880 channels, inputs
+        // cycled through several buffers): short segments keep small grids wide,
+        // long ones load each weight register set once for more tokens.
+        //   tokens           XS = 4     8        16
+        //   1024 (32x32)     11.2 us    12.1     19.0
+        //   2048 (2x32x32)   18.8       18.4     23.0
+        //   4096 (64x64)     35.9       32.3     32.6
+        //   9216 (96x96)     75.1       66.6     66.5
+        //   16384 (128x128)  127.4      112.6    102.0
+        //   32768            242.5      211.9    193.1
+        const int64_t tokens = (int64_t)B * Hh * Ww;
+        if (B > 65535) return hipErrorInvalidValue;
+        auto launch = [&](auto xs_tag, const char * name) {
+            constexpr int XS = decltype(xs_tag)::value;
+            const int64_t nseg = (Ww + XS - 1) / XS;
+            if ((int64_t)Hh * nseg > 2147483647) return hipErrorInvalidValue;
+            note_kernel(name);
+            hipLaunchKernelGGL((dwglu_row_kernel<XS>), dim3((F / 8 + 63) / 64, (unsigned)(Hh * nseg), B), dim3(64), 0,
+                               s, xx, ldx, wt, bias, oo, ldo, Hh, Ww, F);
+            return hipSuccess;
+        };
+        hipError_t e;
+        if (tokens <= 1024) e = launch(std::integral_constant<int, 4>{}, "dwglu_row_kernel<4>");
+        else if (tokens < 12288) e = launch(std::integral_constant<int, 8>{}, "dwglu_row_kernel<8>");
+        else e = launch(std::integral_constant<int, 16>{}, "dwglu_row_kernel<16>");
+        if (e != hipSuccess) return e;
     } else {
         const int64_t total = (int64_t)B * Hh * Ww * F;
         note_kernel("dwglu_scalar_kernel");
