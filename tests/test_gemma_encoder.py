@@ -16,6 +16,7 @@ prefix, padding, the first-and-last row selection and the padding bias of
 src/gemma_encoder.cpp:186-244, with sentencepiece ids and the pinned oracle
 forward (oracle/gemma_oracle.py).  Tolerance 2e-3.
 """
+import glob
 import os
 import struct
 import subprocess
@@ -70,8 +71,11 @@ def run_exe(*args, timeout=300):
 def sp_model(tmp_path_factory):
     d = tmp_path_factory.mktemp("spm")
     corpus = d / "corpus.txt"
+    # the prompts plus the text of the test sources: varied English and code
+    # (any fixed text works: the checks compare two tokenizers on one model)
+    sources = sorted(glob.glob(os.path.join(ROOT, "tests", "*.py")))
     corpus.write_text((CHI + "\n" + "\n".join(CASES[:6]) + "\n") * 3 +
-                      open(os.path.join(ROOT, "DESIGN.md"), encoding="utf-8").read())
+                      "".join(open(f, encoding="utf-8").read() for f in sources))
     spm.SentencePieceTrainer.train(
         input=str(corpus), model_prefix=str(d / "bpe"), vocab_size=700, model_type="bpe", byte_fallback=True,
         add_dummy_prefix=False, remove_extra_whitespaces=False, normalization_rule_name="identity",
