@@ -782,7 +782,9 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     // ~110 GB/s from L2, so larger tiles (fewer operand bytes per flop) win as
     // long as the grid still covers the 256 CUs:
     //  * grids of <= 160 128x128 tiles: shared with a concurrent launch (the
-    //    two CFG branches), 64x64 tiles with three stages and early release;
+    //    two CFG branches), 64x64 tiles with three stages, early release for
+    //    stores and the plain schedule for the residual GEMMs (1024 px forward
+    //    5.055 -> 5.037 ms in one process);
     //    alone, 128x64 tiles with early stage release when that makes >= 256
     //    tiles, else 64x64 tiles (three stages and early release for K >= 2048:
     //    600-row caption projection, K = 2304: 20.3 -> 15.8 us);
@@ -807,7 +809,8 @@ hipError_t gemm(const GemmParams & p_in, hipStream_t s) {
     const int64_t tm128 = (p.M + 127) / 128;
     const int64_t t128 = tm128 * ((p.N + 127) / 128) * co;
     if (t128 <= 160) {
-        if (co >= 2) return launch<64, 64, 2, 2, 3, 3>(p, s);
+        if (co >= 2)
+            return p.mode == kGemmResidual ? launch<64, 64, 2, 2, 3, 1>(p, s) : launch<64, 64, 2, 2, 3, 3>(p, s);
         if (tm128 * ((p.N + 63) / 64) >= 256) return launch<128, 64, 2, 2, 2, 3>(p, s);
         if (p.K >= 2048) return launch<64, 64, 2, 2, 3, 3>(p, s);
         return launch<64, 64, 2, 2, 2, 1>(p, s);
