@@ -26,12 +26,15 @@ Prints ONE JSON line (rank 0, N = 1 only):
                            per forward; roles that share one kernel
                            instantiation are one kernel, as in a trace)
   cpu_baseline             the reference's own CPU code (compiled from source
-                           into oracle/_ref, 1 thread): one full CFG step at
+                           into oracle/_ref, 1 thread, CPU model named) on the
+                           same seeded weights and inputs: one full CFG step at
                            this workload (caption projection + 28-block
                            forward); beside it the single-block configuration
-                           (B=1, 256 tokens, 16x72 heads, median of 3) and the
+                           (B=1, 256 tokens, 16x72 heads, median of 3), the
                            4096-token linear attention + Mix-FFN
-                           microbenchmark (median of 3)
+                           microbenchmark (median of 3), the 20-step loop
+                           (extrapolated from the step) and the 4096 px forward
+                           (extrapolated from one 16384-token block)
   peaks_measured           the dense fp16 MFMA rate of independent MFMA
                            accumulators (sana_hip_mfma_peak, one workgroup per
                            CU) and the HBM rate of 4 GiB streaming reads and
@@ -52,6 +55,8 @@ Prints ONE JSON line (rank 0, N = 1 only):
   gemma_encode_prompt_pair the Gemma-2 2B text encoder over the prompt
                            pair's two sequences (the stage before the loop),
                            ms and TFLOP/s
+  model_load_gguf          seconds to load the 28-block model from a GGUF
+                           file (F32 and F16 payloads) into a fresh context
 
 --pmc-calib adds, before the timed region, three launches of a plain copy
 kernel over 256 MiB (torch.neg: 256 MiB read + 256 MiB written), the known
@@ -202,22 +207,40 @@ def _harness(*args, timeout=600):
     return vals
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(quick=False):
     """The reference's own CPU code (oracle/_ref/ref_harness, built from the
-    reference's sources), 1 thread pinned to core 0: one full CFG step of this
+    reference's sources), 1 thread pinned to core 0, on the same seeded weights
+    (0.02 * randn_torch_cpu(shape, 1000 + sorted index)) and inputs (latent
+    seed 42, caption seed 43) as the GPU leg: one full CFG step of this
     workload (caption projection + 28-block forward), plus the single-block
-    configuration and the 4096-token microbenchmark.  quick: one block x 28
-    instead of the full step."""
+    configuration, the 4096-token microbenchmark and one block at 16384
+    tokens; the 20-step loop and the 4096 px forward are extrapolated from
+    them.  quick: one block x 28 instead of the full step."""
     exe = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
     if not os.path.exists(exe):
         return None
     t0 = time.time()
-    res = {"unit": "ms/step", "cores": 1, "kind": "reference", "host_nproc": os.cpu_count()}
+    res = {"unit": "ms/step", "cores": 1, "kind": "reference", "host_nproc": os.cpu_count(),
+           "cpu_model": cpu_model()}
     if quick:
         blk = _harness("time-block", DIMS["self_heads"], DIMS["cross_heads"], 2, SIDE, CPU_REPS)["median_block_ms"]
         res["value"] = round(blk * DIMS["layers"], 1)
         res["sample"] = (f"extrapolated: one reference block_forward at B=2, N=1024, L=300, 36x32/16x72 heads, "
                          f"median of {CPU_REPS} ({blk:.0f} ms), x28 blocks")
+        fwd_ms, cap_ms = res["value"], 0.0
     else:
         v = _harness("time-forward", DIMS["self_heads"], DIMS["cross_heads"], SIDE, timeout=900)
         res["value"] = round(v["step_ms"], 1)
@@ -226,6 +249,18 @@ def cpu_baseline(quick=False):
         res["sample"] = ("one full CFG step as the reference runs it: caption projection (300x2304 -> 1152) + "
                          "the 28-block forward of run_full_denoising_step_with_cfg at 1024 px, batch 2, t=999, "
                          "36x32/16x72 heads, seeded N(0,0.02) weights, 1 thread")
+        fwd_ms, cap_ms = v["forward_ms"], v["caption_projection_ms"]
+    # config 3: the reference's loop projects the caption once and runs 20 CFG
+    # forwards (src/transformer.cpp:692-724); the solver update is negligible
+    res["config3_loop_20_steps_ms"] = round(20 * fwd_ms + cap_ms, 1)
+    res["config3_note"] = "extrapolated: 20 x the forward above + one caption projection"
+    # config 5: one block at 16384 tokens (B=1), x 2 batch rows x 28 blocks
+    c5 = _harness("time-block", DIMS["self_heads"], DIMS["cross_heads"], 1, 128, 1, timeout=900)
+    res["config5_block_16384_tokens_ms"] = round(c5["median_block_ms"], 1)
+    res["config5_forward_4096px_ms"] = round(c5["median_block_ms"] * 2 * DIMS["layers"], 1)
+    res["config5_note"] = ("extrapolated: one reference block_forward at B=1, 128x128 latent (16384 tokens), "
+                           "36x32/16x72 heads, L=300 (1 run), x 2 CFG batch rows x 28 blocks; the caption "
+                           "projection is left out (context resident, as the GPU forward_4096px line)")
     c1 = _harness("time-block", 16, 16, 1, 16, CPU_REPS)
     res["config1_block_ms"] = round(c1["median_block_ms"], 1)
     c4 = _harness("time-micro", 64, CPU_REPS, timeout=900)
@@ -236,6 +271,41 @@ def cpu_baseline(quick=False):
                            f"and glumb_conv on [2,1152,64,64], median of {CPU_REPS}")
     res["wall_s"] = round(time.time() - t0, 1)
     return res
+
+
+def model_load_times(sana_dit, torch, weights):
+    """GGUF -> device load of the 28-block model through sana_dit_load_gguf: one
+    file holding every tensor (model, caption and denoiser names), written as
+    F32 (the reference's payload type) and as F16 (the linear weights go to the
+    fp16 operand buffers as stored, no fp32 round trip), each into a fresh
+    context.  The file was just written, so it is read from the page cache:
+    this is the host-side conversion + upload cost, not disk speed."""
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from gguf_writer import GGML_F16, GGML_F32, write_gguf
+    out = {}
+    tmp = tempfile.mkdtemp(prefix="sana_bench_")
+    try:
+        for tag, ty in (("f32", GGML_F32), ("f16", GGML_F16)):
+            path = os.path.join(tmp, f"model_{tag}.gguf")
+            write_gguf(path, weights, ggml_type=ty)
+            size = os.path.getsize(path)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            d = sana_dit.Dit(**DIMS, device=0)
+            d.load_gguf(path, path, path)
+            d.check_weights()
+            torch.cuda.synchronize()
+            sec = time.perf_counter() - t0
+            d.close()
+            os.remove(path)
+            out[tag] = {"s": round(sec, 3), "file_gb": round(size / 1e9, 3), "gb_per_s": round(size / 1e9 / sec, 2)}
+            progress(f"GGUF load ({tag}) {sec:.2f} s")
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    out["note"] = ("sana_dit_load_gguf of the 28 blocks + caption + denoiser tensors from one GGUF file in the page "
+                   "cache into a fresh context (context creation included)")
+    return out
 
 
 def microbench_4096(sana_dit, torch, dev, stream):
@@ -487,16 +557,17 @@ def main():
     dev = torch.device("cuda:0")
     d = sana_dit.Dit(**DIMS, device=0)
     rng = np.random.default_rng(1234)
-    for name, shape in sana_dit.manifest(DIMS["layers"], DIMS["hidden"], DIMS["ffn"], DIMS["caption_dim"],
-                                         DIMS["latent_channels"]).items():
-        w = np.ones(shape, np.float32) if name == "caption_norm.weight" else \
-            (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02))
+    # the reference CPU baseline's seeded weights and inputs (torch.randn CPU generator)
+    weights = dict(sana_dit.seeded_weights(DIMS["layers"], DIMS["hidden"], DIMS["ffn"], DIMS["caption_dim"],
+                                           DIMS["latent_channels"]))
+    for name, w in weights.items():
         d.set_weight(name, w)
     d.check_weights()
+    progress("seeded weights uploaded")
 
     B, N, L = 2, SIDE * SIDE, CAPTION_LEN
-    latent = torch.from_numpy(rng.standard_normal((1, DIMS["latent_channels"], SIDE, SIDE), dtype=np.float32)).to(dev)
-    caption = torch.from_numpy(rng.standard_normal((B, L, DIMS["caption_dim"]), dtype=np.float32)).to(dev)
+    latent = torch.from_numpy(sana_dit.randn((1, DIMS["latent_channels"], SIDE, SIDE), 42)).to(dev)
+    caption = torch.from_numpy(sana_dit.randn((B, L, DIMS["caption_dim"]), 43)).to(dev)
     out = torch.empty((B, DIMS["latent_channels"], SIDE, SIDE), device=dev, dtype=torch.float32)
     stream = torch.cuda.Stream(device=dev)      # default priority; every launch and event below uses it
     sp = stream.cuda_stream
@@ -576,6 +647,10 @@ def main():
             extras["microbench_4096_tokens"] = microbench_4096(sana_dit, torch, dev, stream)
             extras["vae_decode_1024px"] = vae_decode_1024px(sana_dit, torch, dev, stream, rng)
             extras["gemma_encode_prompt_pair"] = gemma_prompt_pair(sana_dit, rng)
+            try:
+                extras["model_load_gguf"] = model_load_times(sana_dit, torch, weights)
+            except (OSError, RuntimeError) as e:  # e.g. no room for the 2.4 GB file: report, keep the line
+                extras["model_load_gguf"] = {"error": str(e)[:300]}
 
     peaks = measured_peaks(sana_dit, torch, dev, stream)
     progress("peaks measured")
@@ -596,7 +671,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) latent and caption)",
+        "data": "synthetic: the reference CPU baseline's seeded weights (0.02 x torch.randn CPU generator, seed "
+                "1000 + sorted tensor index; caption_norm ones) and inputs (latent seed 42, caption seed 43)",
         "config": {"workload": "Sana-0.6B DiT forward, 28 blocks, 1024px (latent 32x32x32, 1024 tokens), "
                                "CFG batch 2, 300x2304 caption projected in-step, t=999, heads 36x32 self / 16x72 cross",
                    "global_batch": B, "tokens": N, "caption_len": L},

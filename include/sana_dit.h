@@ -69,6 +69,23 @@ int sana_dit_set_weight(sana_dit * ctx, const char * name, const float * data, c
  * src/transformer.cpp:361-362; SanaBlockWeights built in memory may set them). */
 int sana_dit_set_block_weight(sana_dit * ctx, int64_t block, const char * suffix, const float * data,
                               const int64_t * shape, int ndim, int transposed);
+/* The linear weights run as fp16 GEMM operands: an fp32 value that fp16
+ * cannot hold (|w| > 65504, inf or NaN) fails sana_dit_set_weight and
+ * sana_dit_set_block_weight with SANA_ERR_FORMAT naming the tensor (the
+ * reference keeps every weight in fp32, src/weights_io.cpp:340-355). */
+/* The same two uploads for a linear weight given as IEEE fp16 bits, e.g. a
+ * GGUF F16 payload as stored (the reference reads payloads as F32,
+ * src/weights_io.cpp:325-365): the bits are copied into the fp16 operand
+ * buffer with no fp32 round trip.  Only the 16-bit operand weights are
+ * accepted -- attn1.to_{q,k,v,out.0}.weight, attn2.to_{q,k,v,out.0}.weight,
+ * ff.conv_inverted.weight, ff.conv_point.weight and
+ * caption_projection.linear_{1,2}.weight -- in their PyTorch-order shape (not
+ * transposed); other names fail with SANA_ERR_INVALID_ARGUMENT, inf / NaN
+ * with SANA_ERR_FORMAT. */
+int sana_dit_set_weight_f16(sana_dit * ctx, const char * name, const uint16_t * data, const int64_t * shape,
+                            int ndim);
+int sana_dit_set_block_weight_f16(sana_dit * ctx, int64_t block, const char * suffix, const uint16_t * data,
+                                  const int64_t * shape, int ndim);
 /* Optional LayerNorm affine of a block (which = 0: attn norm, 1: mlp norm).
  * The reference loader injects gamma = 1, beta = 0 (src/transformer.cpp:364-398),
  * which is also the default here; NULL restores the default. */
@@ -77,9 +94,12 @@ int sana_dit_set_block_norm(sana_dit * ctx, int64_t block, int which, const floa
  * src/transformer.cpp:807-884 checks the shapes; set_* already did). */
 int sana_dit_check_weights(sana_dit * ctx);
 /* Loads the three GGUF files of download_weights.sh (model, caption, denoiser)
- * (src/weights_io.cpp:134-164, :325-365).  Payloads may be F32, F16 or BF16;
- * 16-bit payloads are widened exactly to fp32 before the upload (the reference
- * reads every payload as F32).  Other ggml types fail with SANA_ERR_FORMAT. */
+ * (src/weights_io.cpp:134-164, :325-365) from a read-only mapping.  Payloads
+ * may be F32, F16 or BF16 (the reference reads every payload as F32).  F16
+ * linear weights are copied straight into the fp16 operand buffers
+ * (sana_dit_set_*_f16); other 16-bit payloads are widened exactly to fp32 and
+ * BF16 linear weights are then narrowed to fp16 under the range check above.
+ * Other ggml types fail with SANA_ERR_FORMAT. */
 int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * caption_path,
                        const char * denoiser_path);
 
@@ -256,6 +276,12 @@ int sana_hip_mfma_peak(int64_t workgroups, int64_t iters, int zero_operands, flo
  * larger than the 256 MB last-level cache. */
 int sana_hip_hbm_peak(const void * src, void * dst, int64_t bytes, float * sink, int64_t * sink_floats,
                       void * stream);
+
+/* torch.randn(shape, generator seeded with `seed`) on the CPU generator, into
+ * out[0 .. n) (n >= 16; row-major over the shape): the seeded normals of
+ * randn_torch_cpu (src/torch_rng.h:14, src/torch_rng.cpp:14-68), which
+ * sana_infer uses for the initial latent.  Host only, no GPU needed. */
+int sana_randn_torch_cpu(float * out, int64_t n, uint64_t seed);
 
 /* GGUF index inspection (no GPU needed): number of tensors, and the name,
  * PyTorch-order shape (up to 4 dims), ggml type and absolute payload offset of

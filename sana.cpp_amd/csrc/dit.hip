@@ -162,16 +162,37 @@ void drop_graphs(sana_dit * c) {
 }
 
 // Host fp32 -> device fp16 [rows, ld] with zero padding; src is [rows, cols]
-// (or [cols, rows] when transposed).
+// (or [cols, rows] when transposed).  A value fp16 cannot hold is refused
+// (SANA_ERR_FORMAT naming `tensor`) before anything is copied.
 void upload_f16(DevMem & dst, const float * src, int64_t rows, int64_t cols, int64_t ld, bool transposed,
-                int64_t row_offset = 0, int64_t total_rows = -1) {
+                const std::string & tensor, int64_t row_offset = 0, int64_t total_rows = -1) {
     if (total_rows < 0) total_rows = rows;
     std::vector<half_t> h((size_t)rows * ld, (half_t)0.0f);
     for (int64_t r = 0; r < rows; ++r)
-        for (int64_t c = 0; c < cols; ++c)
-            h[(size_t)r * ld + c] = (half_t)(transposed ? src[c * rows + r] : src[r * cols + c]);
+        for (int64_t c = 0; c < cols; ++c) {
+            const size_t i = transposed ? (size_t)(c * rows + r) : (size_t)(r * cols + c);
+            h[(size_t)r * ld + c] = to_f16_checked(src[i], tensor, i);
+        }
     if (!dst.p) dst.ensure((size_t)total_rows * ld * sizeof(half_t));
     copy_to_device(dst.as<half_t>() + (size_t)row_offset * ld, h.data(), h.size() * sizeof(half_t), "upload");
+}
+
+// Host fp16 bits [rows, cols] -> device fp16 [rows, ld]: one copy straight
+// from `src` (e.g. a mapped GGUF F16 payload) when ld == cols, else a padded
+// staging copy.  Non-finite values are refused.
+void upload_f16_bits(DevMem & dst, const uint16_t * src, int64_t rows, int64_t cols, int64_t ld,
+                     const std::string & tensor, int64_t row_offset = 0, int64_t total_rows = -1) {
+    if (total_rows < 0) total_rows = rows;
+    check_f16_bits_finite(src, (size_t)rows * cols, tensor);
+    if (!dst.p) dst.ensure((size_t)total_rows * ld * sizeof(half_t));
+    half_t * d = dst.as<half_t>() + (size_t)row_offset * ld;
+    if (ld == cols) {
+        copy_to_device(d, src, (size_t)rows * cols * 2, "upload");
+        return;
+    }
+    std::vector<uint16_t> h((size_t)rows * ld, 0);
+    for (int64_t r = 0; r < rows; ++r) std::memcpy(&h[(size_t)r * ld], src + (size_t)r * cols, (size_t)cols * 2);
+    copy_to_device(d, h.data(), h.size() * 2, "upload");
 }
 
 void upload_f32(DevMem & dst, const float * src, size_t n, size_t offset = 0, size_t total = 0) {
@@ -701,6 +722,69 @@ struct BlockSuffix {
 
 }  // namespace
 
+namespace {
+
+// Where a linear weight goes among the fp16 GEMM operands: rows [row_off,
+// row_off + rows) of a [total, ld] buffer, from a [rows, cols] weight (cols <
+// ld are zero padding); conv1x1 weights arrive as [rows, cols, 1, 1].
+struct OperandSlot {
+    DevMem * dst = nullptr;
+    int64_t rows = 0, cols = 0, ld = 0, row_off = 0, total = 0;
+    bool conv1x1 = false;
+};
+
+bool block_operand(sana_dit * c, int64_t blk, const std::string & s, OperandSlot & o) {
+    BlockDev & w = *c->blocks[blk];
+    const int64_t C = c->C, E = c->E, F = c->F, Cp = c->Cp;
+    auto set = [&](DevMem & d, int64_t rows, int64_t cols, int64_t ld, int64_t off, int64_t total, bool conv) {
+        o.dst = &d;
+        o.rows = rows;
+        o.cols = cols;
+        o.ld = ld;
+        o.row_off = off;
+        o.total = total;
+        o.conv1x1 = conv;
+        return true;
+    };
+    if (s == "attn1.to_q.weight") return set(w.w_qkv, C, C, Cp, 0, 3 * C, false);
+    if (s == "attn1.to_k.weight") return set(w.w_qkv, C, C, Cp, C, 3 * C, false);
+    if (s == "attn1.to_v.weight") return set(w.w_qkv, C, C, Cp, 2 * C, 3 * C, false);
+    if (s == "attn1.to_out.0.weight") return set(w.w_out, C, C, Cp, 0, C, false);
+    if (s == "attn2.to_q.weight") return set(w.w_cq, C, C, Cp, 0, C, false);
+    if (s == "attn2.to_k.weight") return set(c->w_k_all, C, C, Cp, blk * C, c->L_ * C, false);
+    if (s == "attn2.to_v.weight") return set(c->w_v_all, C, C, Cp, blk * C, c->L_ * C, false);
+    if (s == "attn2.to_out.0.weight") return set(w.w_co, C, C, Cp, 0, C, false);
+    if (s == "ff.conv_inverted.weight") return set(w.w_inv, E, C, Cp, 0, E, true);
+    if (s == "ff.conv_point.weight") return set(w.w_pt, C, F, c->Fp, 0, C, true);
+    return false;
+}
+
+bool top_operand(sana_dit * c, const std::string & n, OperandSlot & o) {
+    const int64_t C = c->C;
+    o = OperandSlot{};
+    if (n == "caption_projection.linear_1.weight") {
+        o.dst = &c->w_cap1;
+        o.rows = C;
+        o.cols = c->Ccap;
+        o.ld = c->Ccap_p;
+    } else if (n == "caption_projection.linear_2.weight") {
+        o.dst = &c->w_cap2;
+        o.rows = C;
+        o.cols = C;
+        o.ld = c->Cp;
+    } else {
+        return false;
+    }
+    o.total = C;
+    return true;
+}
+
+std::string block_tensor_name(int64_t blk, const std::string & s) {
+    return "transformer_blocks." + std::to_string(blk) + "." + s;
+}
+
+}  // namespace
+
 // Scratch of sana_hip_linear_attention_noalloc: the chunk partial states, the
 // fp16 hi/lo state pair and the partial maxima of the three-kernel linear
 // attention (what the allocating entry point takes as its workspace).  Each GPU
@@ -842,13 +926,13 @@ int sana_dit_set_weight(sana_dit * c, const char * name, const float * data, con
             upload_f32(c->b_proj, data, Cl);
         } else if (n == "caption_projection.linear_1.weight") {
             expect_shape(name, shape, ndim, tr ? std::vector<int64_t>{Ccap, C} : std::vector<int64_t>{C, Ccap});
-            upload_f16(c->w_cap1, data, C, Ccap, c->Ccap_p, tr);
+            upload_f16(c->w_cap1, data, C, Ccap, c->Ccap_p, tr, n);
         } else if (n == "caption_projection.linear_1.bias") {
             expect_shape(name, shape, ndim, {C});
             upload_f32(c->b_cap1, data, C);
         } else if (n == "caption_projection.linear_2.weight") {
             expect_shape(name, shape, ndim, {C, C});
-            upload_f16(c->w_cap2, data, C, C, c->Cp, tr);
+            upload_f16(c->w_cap2, data, C, C, c->Cp, tr, n);
         } else if (n == "caption_projection.linear_2.bias") {
             expect_shape(name, shape, ndim, {C});
             upload_f32(c->b_cap2, data, C);
@@ -867,22 +951,21 @@ int sana_dit_set_block_weight(sana_dit * c, int64_t blk, const char * suffix, co
     return guarded([&] {
         const std::string s = suffix;
         BlockDev & w = *c->blocks[blk];
-        const int64_t C = c->C, E = c->E, F = c->F;
+        const int64_t C = c->C, E = c->E;
         const bool tr = transposed != 0;
-        auto lin = [&](DevMem & dst, int64_t out_rows, int64_t in_cols, int64_t ld, int64_t row_off, int64_t total) {
-            expect_shape(suffix, shape, ndim,
-                         tr ? std::vector<int64_t>{in_cols, out_rows} : std::vector<int64_t>{out_rows, in_cols});
-            upload_f16(dst, data, out_rows, in_cols, ld, tr, row_off, total);
-        };
-        if (s == "scale_shift_table") {
+        OperandSlot o;
+        if (block_operand(c, blk, s, o)) {
+            if (o.conv1x1) {
+                expect_shape(suffix, shape, ndim, {o.rows, o.cols, 1, 1});
+                upload_f16(*o.dst, data, o.rows, o.cols, o.ld, false, block_tensor_name(blk, s), o.row_off, o.total);
+            } else {
+                expect_shape(suffix, shape, ndim,
+                             tr ? std::vector<int64_t>{o.cols, o.rows} : std::vector<int64_t>{o.rows, o.cols});
+                upload_f16(*o.dst, data, o.rows, o.cols, o.ld, tr, block_tensor_name(blk, s), o.row_off, o.total);
+            }
+        } else if (s == "scale_shift_table") {
             expect_shape(suffix, shape, ndim, {6, C});
             upload_f32(c->sst_all, data, 6 * C, (size_t)blk * 6 * C, (size_t)c->L_ * 6 * C);
-        } else if (s == "attn1.to_q.weight") {
-            lin(w.w_qkv, C, C, c->Cp, 0, 3 * C);
-        } else if (s == "attn1.to_k.weight") {
-            lin(w.w_qkv, C, C, c->Cp, C, 3 * C);
-        } else if (s == "attn1.to_v.weight") {
-            lin(w.w_qkv, C, C, c->Cp, 2 * C, 3 * C);
         } else if (s == "attn1.to_q.bias" || s == "attn1.to_k.bias" || s == "attn1.to_v.bias") {
             // not in any checkpoint (the reference loader injects zeros, src/transformer.cpp:361-362);
             // accepted for weights built in memory
@@ -890,34 +973,21 @@ int sana_dit_set_block_weight(sana_dit * c, int64_t blk, const char * suffix, co
             const int64_t part = s == "attn1.to_q.bias" ? 0 : (s == "attn1.to_k.bias" ? 1 : 2);
             upload_f32(w.b_qkv, data, C, (size_t)part * C, (size_t)3 * C);
             w.has_qkv_bias = true;
-        } else if (s == "attn1.to_out.0.weight") {
-            lin(w.w_out, C, C, c->Cp, 0, C);
         } else if (s == "attn1.to_out.0.bias") {
             expect_shape(suffix, shape, ndim, {C});
             upload_f32(w.b_out, data, C);
-        } else if (s == "attn2.to_q.weight") {
-            lin(w.w_cq, C, C, c->Cp, 0, C);
         } else if (s == "attn2.to_q.bias") {
             expect_shape(suffix, shape, ndim, {C});
             upload_f32(w.b_cq, data, C);
-        } else if (s == "attn2.to_k.weight") {
-            lin(c->w_k_all, C, C, c->Cp, blk * C, c->L_ * C);
         } else if (s == "attn2.to_k.bias") {
             expect_shape(suffix, shape, ndim, {C});
             upload_f32(c->b_k_all, data, C, blk * C, c->L_ * C);
-        } else if (s == "attn2.to_v.weight") {
-            lin(c->w_v_all, C, C, c->Cp, blk * C, c->L_ * C);
         } else if (s == "attn2.to_v.bias") {
             expect_shape(suffix, shape, ndim, {C});
             upload_f32(c->b_v_all, data, C, blk * C, c->L_ * C);
-        } else if (s == "attn2.to_out.0.weight") {
-            lin(w.w_co, C, C, c->Cp, 0, C);
         } else if (s == "attn2.to_out.0.bias") {
             expect_shape(suffix, shape, ndim, {C});
             upload_f32(w.b_co, data, C);
-        } else if (s == "ff.conv_inverted.weight") {
-            expect_shape(suffix, shape, ndim, {E, C, 1, 1});
-            upload_f16(w.w_inv, data, E, C, c->Cp, false);
         } else if (s == "ff.conv_inverted.bias") {
             expect_shape(suffix, shape, ndim, {E});
             upload_f32(w.b_inv, data, E);
@@ -930,12 +1000,40 @@ int sana_dit_set_block_weight(sana_dit * c, int64_t blk, const char * suffix, co
         } else if (s == "ff.conv_depth.bias") {
             expect_shape(suffix, shape, ndim, {E});
             upload_f32(w.b_dw, data, E);
-        } else if (s == "ff.conv_point.weight") {
-            expect_shape(suffix, shape, ndim, {C, F, 1, 1});
-            upload_f16(w.w_pt, data, C, F, c->Fp, false);
         } else {
             throw_err(SANA_ERR_INVALID_ARGUMENT, "unknown block weight suffix: " + s);
         }
+        c->have["blk" + std::to_string(blk) + "." + s] = 1;
+        drop_graphs(c);
+    });
+}
+
+int sana_dit_set_weight_f16(sana_dit * c, const char * name, const uint16_t * data, const int64_t * shape, int ndim) {
+    if (!c || !name || !data || !shape) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] {
+        const std::string n = name;
+        OperandSlot o;
+        if (!top_operand(c, n, o)) throw_err(SANA_ERR_INVALID_ARGUMENT, "not a 16-bit operand weight: " + n);
+        expect_shape(name, shape, ndim, {o.rows, o.cols});
+        upload_f16_bits(*o.dst, data, o.rows, o.cols, o.ld, n, o.row_off, o.total);
+        c->have[n] = 1;
+        drop_graphs(c);
+    });
+}
+
+int sana_dit_set_block_weight_f16(sana_dit * c, int64_t blk, const char * suffix, const uint16_t * data,
+                                  const int64_t * shape, int ndim) {
+    if (!c || !suffix || !data || !shape) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    if (blk < 0 || blk >= c->L_) return set_err(SANA_ERR_INVALID_ARGUMENT, "block index out of range");
+    return guarded([&] {
+        const std::string s = suffix;
+        OperandSlot o;
+        if (!block_operand(c, blk, s, o)) throw_err(SANA_ERR_INVALID_ARGUMENT, "not a 16-bit operand weight: " + s);
+        if (o.conv1x1)
+            expect_shape(suffix, shape, ndim, {o.rows, o.cols, 1, 1});
+        else
+            expect_shape(suffix, shape, ndim, {o.rows, o.cols});
+        upload_f16_bits(*o.dst, data, o.rows, o.cols, o.ld, block_tensor_name(blk, s), o.row_off, o.total);
         c->have["blk" + std::to_string(blk) + "." + s] = 1;
         drop_graphs(c);
     });

@@ -258,18 +258,21 @@ void upload_bytes(DevMem & d, const void * src, size_t bytes) {
     copy_to_device(d.p, src, bytes, "upload gemma weight");
 }
 
-void upload_f16_rows(DevMem & d, const float * src, size_t n, size_t total, size_t offset) {
+// fp32 -> fp16 operand rows; a value fp16 cannot hold fails with
+// SANA_ERR_FORMAT naming the tensor.
+void upload_f16_rows(DevMem & d, const float * src, size_t n, size_t total, size_t offset, const std::string & tensor) {
     if (!d.p) d.ensure(total * 2, false);
     std::vector<_Float16> h(n);
-    for (size_t i = 0; i < n; ++i) h[i] = (_Float16)src[i];
+    for (size_t i = 0; i < n; ++i) h[i] = to_f16_checked(src[i], tensor, i);
     copy_to_device(static_cast<_Float16 *>(d.p) + offset, h.data(), n * 2, "upload gemma weight");
 }
 
 // Rows r of src ([n_rows][width] fp32) to rows 2 r + parity of d ([2 n_rows][width] fp16).
-void upload_f16_rows_interleaved(DevMem & d, const float * src, size_t n_rows, size_t width, int parity) {
+void upload_f16_rows_interleaved(DevMem & d, const float * src, size_t n_rows, size_t width, int parity,
+                                 const std::string & tensor) {
     if (!d.p) d.ensure(2 * n_rows * width * 2, false);
     std::vector<_Float16> h(n_rows * width);
-    for (size_t i = 0; i < h.size(); ++i) h[i] = (_Float16)src[i];
+    for (size_t i = 0; i < h.size(); ++i) h[i] = to_f16_checked(src[i], tensor, i);
     hip_check(hipMemcpy2D(static_cast<_Float16 *>(d.p) + parity * width, 2 * width * 2, h.data(), width * 2,
                           width * 2, n_rows, hipMemcpyHostToDevice),
               "upload gemma weight");
@@ -304,7 +307,7 @@ void set_weight(sana_gemma * g, const std::string & n, const float * d, const in
     const int64_t H = c.hidden, F = c.ffn, Dq = g->Dq, Dkv = g->Dkv;
     if (n == "token_embd.weight") {
         expect(n, sh, nd, {c.vocab, H});
-        upload_f16_rows(g->emb16, d, (size_t)(c.vocab * H), (size_t)(c.vocab * H), 0);
+        upload_f16_rows(g->emb16, d, (size_t)(c.vocab * H), (size_t)(c.vocab * H), 0, n);
     } else if (n == "output_norm.weight") {
         expect(n, sh, nd, {H});
         upload_bytes(g->out_norm, d, (size_t)H * 4);
@@ -320,25 +323,25 @@ void set_weight(sana_gemma * g, const std::string & n, const float * d, const in
         const size_t qkv_rows = (size_t)(Dq + 2 * Dkv);
         if (s == "attn_q.weight") {
             expect(n, sh, nd, {Dq, H});
-            upload_f16_rows(L.wqkv, d, (size_t)(Dq * H), qkv_rows * H, 0);
+            upload_f16_rows(L.wqkv, d, (size_t)(Dq * H), qkv_rows * H, 0, n);
         } else if (s == "attn_k.weight") {
             expect(n, sh, nd, {Dkv, H});
-            upload_f16_rows(L.wqkv, d, (size_t)(Dkv * H), qkv_rows * H, (size_t)(Dq * H));
+            upload_f16_rows(L.wqkv, d, (size_t)(Dkv * H), qkv_rows * H, (size_t)(Dq * H), n);
         } else if (s == "attn_v.weight") {
             expect(n, sh, nd, {Dkv, H});
-            upload_f16_rows(L.wqkv, d, (size_t)(Dkv * H), qkv_rows * H, (size_t)((Dq + Dkv) * H));
+            upload_f16_rows(L.wqkv, d, (size_t)(Dkv * H), qkv_rows * H, (size_t)((Dq + Dkv) * H), n);
         } else if (s == "attn_output.weight") {
             expect(n, sh, nd, {H, Dq});
-            upload_f16_rows(L.wo, d, (size_t)(H * Dq), (size_t)(H * Dq), 0);
+            upload_f16_rows(L.wo, d, (size_t)(H * Dq), (size_t)(H * Dq), 0, n);
         } else if (s == "ffn_gate.weight") {
             expect(n, sh, nd, {F, H});
-            upload_f16_rows_interleaved(L.wgu, d, (size_t)F, (size_t)H, 0);
+            upload_f16_rows_interleaved(L.wgu, d, (size_t)F, (size_t)H, 0, n);
         } else if (s == "ffn_up.weight") {
             expect(n, sh, nd, {F, H});
-            upload_f16_rows_interleaved(L.wgu, d, (size_t)F, (size_t)H, 1);
+            upload_f16_rows_interleaved(L.wgu, d, (size_t)F, (size_t)H, 1, n);
         } else if (s == "ffn_down.weight") {
             expect(n, sh, nd, {H, F});
-            upload_f16_rows(L.wdown, d, (size_t)(H * F), (size_t)(H * F), 0);
+            upload_f16_rows(L.wdown, d, (size_t)(H * F), (size_t)(H * F), 0, n);
         } else {
             DevMem * dst = s == "attn_norm.weight"             ? &L.n_attn
                            : s == "post_attention_norm.weight" ? &L.n_post_attn

@@ -58,6 +58,28 @@ const float * payload(const sana::gguf::MappedFile & f, const sana::gguf::Tensor
     }
 }
 
+// Linear weights held as fp16 GEMM operands on the device: an F16 payload of
+// one of these is copied as stored (sana_dit_set_*_f16).
+bool is_block_operand(const std::string & s) {
+    static const char * const k[] = {"attn1.to_q.weight", "attn1.to_k.weight",     "attn1.to_v.weight",
+                                     "attn1.to_out.0.weight", "attn2.to_q.weight", "attn2.to_k.weight",
+                                     "attn2.to_v.weight", "attn2.to_out.0.weight", "ff.conv_inverted.weight",
+                                     "ff.conv_point.weight"};
+    for (const char * n : k)
+        if (s == n) return true;
+    return false;
+}
+bool is_top_operand(const std::string & s) {
+    return s == "caption_projection.linear_1.weight" || s == "caption_projection.linear_2.weight";
+}
+
+// The F16 payload in place (bounds checked against the mapping).
+const uint16_t * f16_payload(const sana::gguf::MappedFile & f, const sana::gguf::TensorInfo & t) {
+    if (t.offset + t.nbytes > f.size() || t.nbytes == 0 || (t.offset & 1))
+        throw Err{SANA_ERR_FORMAT, "unsupported or truncated gguf tensor: " + t.name};
+    return reinterpret_cast<const uint16_t *>(f.data() + t.offset);
+}
+
 const sana::gguf::TensorInfo & find(const sana::gguf::Index & idx, const std::string & n) {
     for (const auto & t : idx.tensors)
         if (t.name == n) return t;
@@ -120,8 +142,11 @@ int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * cap
                 for (const char * s : kBlockSuffixes) {
                     const std::string full = pre[b].empty() ? std::string(s) : pre[b] + "." + s;
                     const TensorInfo & t = find(idx, full);
-                    int rc = sana_dit_set_block_weight(ctx, (int64_t)b, s, payload(f, t, tmp), t.shape.data(),
-                                                       (int)t.shape.size(), 0);
+                    int rc = t.type == kF16 && is_block_operand(s)
+                                 ? sana_dit_set_block_weight_f16(ctx, (int64_t)b, s, f16_payload(f, t), t.shape.data(),
+                                                                 (int)t.shape.size())
+                                 : sana_dit_set_block_weight(ctx, (int64_t)b, s, payload(f, t, tmp), t.shape.data(),
+                                                             (int)t.shape.size(), 0);
                     if (rc == SANA_ERR_INVALID_ARGUMENT && b > 0)
                         throw Err{SANA_ERR_SHAPE, "gguf holds more blocks than the model's layer count"};
                     call(rc);
@@ -138,7 +163,10 @@ int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * cap
             for (size_t i = 0; i < n; ++i) {
                 const char * name = which == 0 ? kCaptionNames[i] : kDenoiserNames[i];
                 const TensorInfo & t = find(idx, name);
-                call(sana_dit_set_weight(ctx, name, payload(f, t, tmp), t.shape.data(), (int)t.shape.size(), 0));
+                if (t.type == kF16 && is_top_operand(name))
+                    call(sana_dit_set_weight_f16(ctx, name, f16_payload(f, t), t.shape.data(), (int)t.shape.size()));
+                else
+                    call(sana_dit_set_weight(ctx, name, payload(f, t, tmp), t.shape.data(), (int)t.shape.size(), 0));
             }
         }
         call(sana_dit_check_weights(ctx));

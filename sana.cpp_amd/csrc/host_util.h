@@ -47,6 +47,29 @@ inline void launch_check(hipError_t e, const char * what) {
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// Largest finite fp16 value: the GEMM operands are fp16, so a weight outside
+// [-65504, 65504] (or not finite) cannot be represented.  Magnitudes below
+// fp16's smallest subnormal (2^-24) round to zero, like any rounding.
+constexpr float kF16Max = 65504.0f;
+
+// fp32 -> fp16 operand conversion that refuses a value fp16 cannot hold
+// (SANA_ERR_FORMAT naming the tensor and the element).
+inline _Float16 to_f16_checked(float v, const std::string & tensor, size_t i) {
+    if (!(v <= kF16Max && v >= -kF16Max)) {  // NaN fails both comparisons
+        char buf[96];
+        snprintf(buf, sizeof(buf), "%g at element %zu", (double)v, i);
+        throw_err(SANA_ERR_FORMAT, tensor + ": weight value " + buf + " is outside the fp16 operand range (|w| <= 65504)");
+    }
+    return (_Float16)v;
+}
+
+// IEEE fp16 bit patterns: refuse inf and NaN (exponent field all ones).
+inline void check_f16_bits_finite(const uint16_t * h, size_t n, const std::string & tensor) {
+    for (size_t i = 0; i < n; ++i)
+        if ((h[i] & 0x7c00u) == 0x7c00u)
+            throw_err(SANA_ERR_FORMAT, tensor + ": fp16 weight at element " + std::to_string(i) + " is not finite");
+}
+
 // Device allocation owned by the context.
 struct DevMem {
     void * p = nullptr;

@@ -285,19 +285,24 @@ void upload(DevMem & d, const void * src, size_t bytes) {
 
 void upload_f32(DevMem & d, const float * src, size_t n) { upload(d, src, n * 4); }
 
-void upload_f16(DevMem & d, const std::vector<float> & v) {
-    std::vector<_Float16> h(v.size());
-    for (size_t i = 0; i < v.size(); ++i) h[i] = (_Float16)v[i];
+// fp32 -> fp16 GEMM operand; a value fp16 cannot hold fails with
+// SANA_ERR_FORMAT naming the tensor.
+void upload_f16(DevMem & d, const float * v, size_t n, const std::string & tensor) {
+    std::vector<_Float16> h(n);
+    for (size_t i = 0; i < n; ++i) h[i] = to_f16_checked(v[i], tensor, i);
     upload(d, h.data(), h.size() * 2);
 }
 
 // [Cout, Cin, 3, 3] -> tap-major fp16 [Cout][9][cin_pad] (zero past Cin).
-void upload_conv3(DevMem & d, const float * w, int64_t Cout, int64_t Cin, int64_t cin_pad) {
-    std::vector<float> t((size_t)Cout * 9 * cin_pad, 0.0f);
+void upload_conv3(DevMem & d, const float * w, int64_t Cout, int64_t Cin, int64_t cin_pad, const std::string & tensor) {
+    std::vector<_Float16> t((size_t)Cout * 9 * cin_pad, (_Float16)0.0f);
     for (int64_t o = 0; o < Cout; ++o)
         for (int64_t c = 0; c < Cin; ++c)
-            for (int k = 0; k < 9; ++k) t[((size_t)o * 9 + k) * cin_pad + c] = w[((size_t)o * Cin + c) * 9 + k];
-    upload_f16(d, t);
+            for (int k = 0; k < 9; ++k) {
+                const size_t i = ((size_t)o * Cin + c) * 9 + k;
+                t[((size_t)o * 9 + k) * cin_pad + c] = to_f16_checked(w[i], tensor, i);
+            }
+    upload(d, t.data(), t.size() * 2);
 }
 
 // Physical position of channel `lc` of concat(q, k, v) (3C channels, heads of
@@ -324,7 +329,7 @@ void set_weight(sana_vae * v, const std::string & n, const float * d, const int6
     auto need = [&](std::vector<int64_t> s) { expect(n.c_str(), sh, nd, std::move(s)); };
     if (n == "decoder.conv_in.weight") {
         need({top, v->Cl, 3, 3});
-        upload_conv3(v->cin_w, d, top, v->Cl, round_up(v->Cl, 64));
+        upload_conv3(v->cin_w, d, top, v->Cl, round_up(v->Cl, 64), n);
     } else if (n == "decoder.conv_in.bias") {
         need({top});
         upload_f32(v->cin_b, d, top);
@@ -336,7 +341,7 @@ void set_weight(sana_vae * v, const std::string & n, const float * d, const int6
         upload_f32(v->nout_b, d, C0);
     } else if (n == "decoder.conv_out.weight") {
         need({3, C0, 3, 3});
-        upload_conv3(v->cout_w, d, 3, C0, C0);
+        upload_conv3(v->cout_w, d, 3, C0, C0, n);
     } else if (n == "decoder.conv_out.bias") {
         need({3});
         upload_f32(v->cout_b, d, 3);
@@ -357,7 +362,7 @@ void set_weight(sana_vae * v, const std::string & n, const float * d, const int6
             const int64_t Cp = v->lv[li + 1]->C;
             if (rest == "conv.weight") {
                 need({C, Cp, 3, 3});
-                upload_conv3(lvd.up_w, d, C, Cp, Cp);
+                upload_conv3(lvd.up_w, d, C, Cp, Cp, n);
             } else if (rest == "conv.bias") {
                 need({C});
                 upload_f32(lvd.up_b, d, C);
@@ -369,9 +374,9 @@ void set_weight(sana_vae * v, const std::string & n, const float * d, const int6
             if (k < 0 || k > 2) throw_err(SANA_ERR_INVALID_ARGUMENT, "vae layer index out of range: " + n);
             if (!lvd.attn) {
                 ResDev & r = lvd.res[k];
-                if (rest == "conv1.weight") { need({C, C, 3, 3}); upload_conv3(r.w1, d, C, C, C); }
+                if (rest == "conv1.weight") { need({C, C, 3, 3}); upload_conv3(r.w1, d, C, C, C, n); }
                 else if (rest == "conv1.bias") { need({C}); upload_f32(r.b1, d, C); }
-                else if (rest == "conv2.weight") { need({C, C, 3, 3}); upload_conv3(r.w2, d, C, C, C); }
+                else if (rest == "conv2.weight") { need({C, C, 3, 3}); upload_conv3(r.w2, d, C, C, C, n); }
                 else if (rest == "norm.weight") { need({C}); upload_f32(r.nw, d, C); }
                 else if (rest == "norm.bias") { need({C}); upload_f32(r.nb, d, C); }
                 else throw_err(SANA_ERR_INVALID_ARGUMENT, "unknown vae weight " + n);
@@ -391,7 +396,7 @@ void set_weight(sana_vae * v, const std::string & n, const float * d, const int6
                     }
                     for (int64_t o = 0; o < C; ++o) {
                         const int64_t ph = qkv_perm(t * C + o, heads);
-                        for (int64_t i = 0; i < C; ++i) all[(size_t)ph * C + i] = (_Float16)d[o * C + i];
+                        for (int64_t i = 0; i < C; ++i) all[(size_t)ph * C + i] = to_f16_checked(d[o * C + i], n, (size_t)(o * C + i));
                     }
                     upload(a.wqkv, all.data(), all.size() * 2);
                 } else if (rest == "attn.to_qkv_multiscale.0.proj_in.weight") {
@@ -410,12 +415,12 @@ void set_weight(sana_vae * v, const std::string & n, const float * d, const int6
                     upload_f32(a.grp, t.data(), t.size());
                 } else if (rest == "attn.to_out.weight") {
                     need({C, 2 * C});
-                    upload_f16(a.wout, std::vector<float>(d, d + 2 * C * C));
+                    upload_f16(a.wout, d, (size_t)(2 * C * C), n);
                 } else if (rest == "attn.norm_out.weight") { need({C}); upload_f32(a.anw, d, C); }
                 else if (rest == "attn.norm_out.bias") { need({C}); upload_f32(a.anb, d, C); }
                 else if (rest == "conv_out.conv_inverted.weight") {
                     need({2 * Hd, C, 1, 1});
-                    upload_f16(a.winv, std::vector<float>(d, d + 2 * Hd * C));
+                    upload_f16(a.winv, d, (size_t)(2 * Hd * C), n);
                 } else if (rest == "conv_out.conv_inverted.bias") { need({2 * Hd}); upload_f32(a.binv, d, 2 * Hd); }
                 else if (rest == "conv_out.conv_depth.weight") {
                     need({2 * Hd, 1, 3, 3});
@@ -426,7 +431,7 @@ void set_weight(sana_vae * v, const std::string & n, const float * d, const int6
                 } else if (rest == "conv_out.conv_depth.bias") { need({2 * Hd}); upload_f32(a.bdw, d, 2 * Hd); }
                 else if (rest == "conv_out.conv_point.weight") {
                     need({C, Hd, 1, 1});
-                    upload_f16(a.wpt, std::vector<float>(d, d + C * Hd));
+                    upload_f16(a.wpt, d, (size_t)(C * Hd), n);
                 } else if (rest == "conv_out.norm.weight") { need({C}); upload_f32(a.gnw, d, C); }
                 else if (rest == "conv_out.norm.bias") { need({C}); upload_f32(a.gnb, d, C); }
                 else throw_err(SANA_ERR_INVALID_ARGUMENT, "unknown vae weight " + n);

@@ -57,6 +57,9 @@ PROTOTYPES = {
     "sana_dit_set_block_weight": (ctypes.c_int, [_vp, _i64, ctypes.c_char_p, _vp, ctypes.POINTER(_i64),
                                                  ctypes.c_int, ctypes.c_int]),
     "sana_dit_set_block_norm": (ctypes.c_int, [_vp, _i64, ctypes.c_int, _vp, _vp]),
+    "sana_dit_set_weight_f16": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, ctypes.POINTER(_i64), ctypes.c_int]),
+    "sana_dit_set_block_weight_f16": (ctypes.c_int, [_vp, _i64, ctypes.c_char_p, _vp, ctypes.POINTER(_i64),
+                                                     ctypes.c_int]),
     "sana_dit_check_weights": (ctypes.c_int, [_vp]),
     "sana_dit_load_gguf": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
     "sana_dit_set_context": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
@@ -74,6 +77,7 @@ PROTOTYPES = {
     "sana_hip_hbm_peak": (ctypes.c_int, [_vp, _vp, _i64, _vp, ctypes.POINTER(_i64), _vp]),
     "sana_dit_time_kernel": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _fp, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_double), ctypes.c_char_p, ctypes.c_size_t]),
+    "sana_randn_torch_cpu": (ctypes.c_int, [_vp, _i64, ctypes.c_uint64]),
     "sana_gguf_num_tensors": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_i64)]),
     "sana_gguf_tensor_info": (ctypes.c_int, [ctypes.c_char_p, _i64, ctypes.c_char_p, ctypes.c_size_t,
                                              ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_int),
@@ -190,6 +194,17 @@ class Dit:
         else:
             check(lib().sana_dit_set_weight(self.h, name.encode(), ptr(arr), shape, arr.ndim, int(transposed)))
 
+    def set_weight_f16(self, name, arr):
+        """A linear weight as fp16 (numpy float16, PyTorch-order shape): its
+        bits go to the device's fp16 operand buffer unchanged."""
+        arr = np.ascontiguousarray(arr, dtype=np.float16)
+        shape = (_i64 * arr.ndim)(*arr.shape)
+        if name.startswith("transformer_blocks."):
+            _, idx, suffix = name.split(".", 2)
+            check(lib().sana_dit_set_block_weight_f16(self.h, int(idx), suffix.encode(), ptr(arr), shape, arr.ndim))
+        else:
+            check(lib().sana_dit_set_weight_f16(self.h, name.encode(), ptr(arr), shape, arr.ndim))
+
     def set_block_norm(self, block, which, gamma=None, beta=None):
         g = None if gamma is None else _f32(gamma)
         b = None if beta is None else _f32(beta)
@@ -295,6 +310,28 @@ def gguf_index(path):
                                           ctypes.byref(off)))
         out.append((name.value.decode(), tuple(shape[:nd.value]), ty.value, off.value))
     return out
+
+
+def randn(shape, seed):
+    """torch.randn(shape) on the CPU generator seeded with `seed` (float32)."""
+    out = np.empty(shape, np.float32)
+    check(lib().sana_randn_torch_cpu(ptr(out), out.size, seed))
+    return out
+
+
+def seeded_weights(layers=28, hidden=1152, ffn=5760, caption_dim=2304, latent_channels=32, scale=0.02):
+    """The seeded synthetic weights the reference CPU baseline builds: tensor i
+    of the byte-wise sorted names of the three weight files is scale *
+    randn(shape, 1000 + i), except caption_norm.weight, which is all ones.
+    Yields (name, float32 array) in that order."""
+    m = manifest(layers, hidden, ffn, caption_dim, latent_channels)
+    for i, name in enumerate(sorted(m)):
+        if name == "caption_norm.weight":
+            yield name, np.ones(m[name], np.float32)
+        else:
+            w = randn(m[name], 1000 + i)
+            w *= np.float32(scale)
+            yield name, w
 
 
 def manifest(layers=28, hidden=1152, ffn=5760, caption_dim=2304, latent_channels=32, time_freq=256):

@@ -530,6 +530,17 @@ void gpu_small_model_tests() {
           "block-level invalidate uploads the edit");
     invalidate_all_device_weights();
     check(run_model_blocks(x, ctx, tmod, we, 0, 2).data() == r1.data(), "re-upload after invalidate_all");
+
+    // The linear weights become fp16 GEMM operands: a value fp16 cannot hold
+    // is refused at upload (std::runtime_error) instead of running as inf.
+    SanaDenoiserWeights wbig = sm.weights();
+    wbig.blocks[0].out_weight.data()[7] = 1.0e5f;
+    throws<std::runtime_error>([&] { run_model_blocks(x, ctx, tmod, wbig, 0, 2); }, "linear weight of 1e5");
+    SanaDenoiserWeights wnan = sm.weights();
+    wnan.blocks[1].cross_q_weight.data()[3] = std::nanf("");
+    throws<std::runtime_error>([&] { block_forward(x, ctx, tmod, wnan.blocks[1]); }, "NaN linear weight");
+    check(run_model_blocks(x, ctx, tmod, w, 0, 2).data() == run_model_blocks(x, ctx, tmod, w, 0, 2).data(),
+          "valid weights still run after the refusals");
 }
 
 // ---------------------------------------------------------------- op-level API

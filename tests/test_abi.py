@@ -71,3 +71,31 @@ def test_vae_manifest_matches_the_reference_weight_set():
     for cfg in (O.FULL_VAE, O.SMALL_VAE):
         got = sana_dit.vae_manifest(cfg["channels"], cfg["attn"], cfg["latent"])
         assert got == {k: tuple(v) for k, v in O.vae_manifest(cfg).items()}
+
+
+def test_randn_torch_cpu_entry_point():
+    """sana_randn_torch_cpu (host only): the oracle's generator bit for bit --
+    itself pinned to torch.randn and, through the golden weight digests, to the
+    reference's randn_torch_cpu -- including a ragged tail (n % 16 != 0)."""
+    import numpy as np
+    import oracle_lib as O
+    for shape, seed in (((16,), 1), ((1, 32, 32, 32), 42), ((2, 300, 2304), 43), ((37,), 5), ((1152, 2880), 1007)):
+        assert np.array_equal(sana_dit.randn(shape, seed), O.randn(shape, seed)), (shape, seed)
+    # torch.manual_seed(42); torch.randn(3): the well-known first draws
+    assert np.allclose(sana_dit.randn((16,), 42)[:3], [1.9269, 1.4873, 0.9007], atol=1e-4)
+    rc = sana_dit.lib().sana_randn_torch_cpu(sana_dit.ptr(np.empty(8, np.float32)), 8, 0)
+    assert rc == sana_dit.SANA_ERR_INVALID_ARGUMENT
+
+
+def test_seeded_weights_follow_the_reference_harness_rule():
+    """sana_dit.seeded_weights: 0.02 * randn(shape, 1000 + sorted index), caption_norm ones
+    (the rule of the reference CPU baseline's weights), checked on a small manifest."""
+    import numpy as np
+    import oracle_lib as O
+    w = dict(sana_dit.seeded_weights(2, 128, 256, 96, 16))
+    names = sorted(sana_dit.manifest(2, 128, 256, 96, 16))
+    assert list(w) == names
+    for i, n in enumerate(names):
+        want = (np.ones(w[n].shape, np.float32) if n == "caption_norm.weight"
+                else O.randn(w[n].shape, 1000 + i) * np.float32(0.02))
+        assert np.array_equal(w[n], want), n

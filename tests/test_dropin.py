@@ -58,6 +58,35 @@ def test_dropin_vae_loaders(tmp_path):
     assert res.returncode == 0 and " 0 failures" in res.stdout
 
 
+REF_SRC = "/root/reference/src"
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_SRC), reason="the reference tree is not present on this host")
+def test_option_a_sources_compile_against_reference_headers(tmp_path):
+    """INTEGRATION.md Option A: host/transformer.cpp and host/vae.cpp replace the
+    reference's src/transformer.cpp and src/vae.cpp inside its own build, so they
+    must compile against the reference's transformer.h, vae.h, tensor.h,
+    scheduler.h and weights_io.h (copied next to them, so the quoted includes
+    resolve to the reference's headers), plus the three files of ours they also
+    include: host/fingerprint.h, csrc/gguf.h and include/sana_dit.h."""
+    import glob
+    import shutil
+    host = tmp_path / "sana.cpp_amd" / "host"
+    host.mkdir(parents=True)
+    (tmp_path / "sana.cpp_amd" / "csrc").mkdir()
+    (tmp_path / "include").mkdir()
+    for h in glob.glob(os.path.join(REF_SRC, "*.h")):
+        shutil.copy(h, host)
+    for f in ("transformer.cpp", "vae.cpp", "fingerprint.h"):
+        shutil.copy(os.path.join(ROOT, "sana.cpp_amd", "host", f), host)
+    shutil.copy(os.path.join(ROOT, "sana.cpp_amd", "csrc", "gguf.h"), tmp_path / "sana.cpp_amd" / "csrc")
+    shutil.copy(os.path.join(ROOT, "include", "sana_dit.h"), tmp_path / "include")
+    for src in ("transformer.cpp", "vae.cpp"):
+        res = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-Wall", str(host / src)], capture_output=True,
+                             text=True, timeout=120)
+        assert res.returncode == 0, res.stderr[-3000:]
+
+
 def test_dropin_host_api():
     res = run_exe("cpu", timeout=120)
     assert res.returncode == 0 and " 0 failures" in res.stdout
