@@ -104,6 +104,93 @@ __global__ __launch_bounds__(64) void dwglu_row_kernel(const f16 * __restrict__ 
     }
 }
 
+// Pipelined variant: a thread owns 4 data channels (and the matching 4 gate
+// channels) of a row segment of XS output tokens, so its weights (9 taps x 8
+// channels, fp32) and input window fit in ~150 VGPRs (three waves per SIMD
+// instead of two).  The window is a ring of 3 + PD input columns: the column
+// token i + PD needs is requested before token i's arithmetic, so each load
+// has PD tokens' worth of math to land behind.  Taps are summed in (ky, kx)
+// order with zero padding, then the bias, as in dwglu_row_kernel (same
+// per-channel arithmetic, same results).
+template <int XS, int PD = 1>
+__global__ __launch_bounds__(64) void dwglu_pipe_kernel(const f16 * __restrict__ x, int64_t ldx,
+                                                        const float * __restrict__ wt,
+                                                        const float * __restrict__ bias, f16 * __restrict__ out,
+                                                        int64_t ldo, int Hh, int Ww, int F) {
+    const int G = F / 4;
+    const int g = blockIdx.x * 64 + threadIdx.x;
+    const int nseg = (Ww + XS - 1) / XS;
+    const int y = blockIdx.y / nseg, seg = blockIdx.y - (blockIdx.y / nseg) * nseg;
+    const int b = blockIdx.z;
+    if (g >= G) return;
+    const int c0 = g * 4, E = 2 * F;
+    float wd[9][4], wg[9][4];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        const float4 a = *reinterpret_cast<const float4 *>(wt + (int64_t)k * E + c0);
+        const float4 q = *reinterpret_cast<const float4 *>(wt + (int64_t)k * E + F + c0);
+        wd[k][0] = a.x; wd[k][1] = a.y; wd[k][2] = a.z; wd[k][3] = a.w;
+        wg[k][0] = q.x; wg[k][1] = q.y; wg[k][2] = q.z; wg[k][3] = q.w;
+    }
+    const float4 bdv = *reinterpret_cast<const float4 *>(bias + c0);
+    const float4 bgv = *reinterpret_cast<const float4 *>(bias + F + c0);
+    const float bd[4] = {bdv.x, bdv.y, bdv.z, bdv.w}, bg[4] = {bgv.x, bgv.y, bgv.z, bgv.w};
+    const f16 * xb = x + (int64_t)b * Hh * Ww * ldx + c0;
+    f16 * ob = out + (int64_t)b * Hh * Ww * ldo + c0;
+    const int x0 = seg * XS;
+    constexpr int NS = 3 + PD;  // ring of input columns: column x0 - 1 + j lives in slot j % NS
+    f16x4 vd[3][NS], vg[3][NS];
+    auto load = [&](int ky, int xx, int slot) {
+        const int yy = y + ky - 1;
+        if (yy >= 0 && yy < Hh && xx >= 0 && xx < Ww) {
+            const f16 * p = xb + ((int64_t)yy * Ww + xx) * ldx;
+            vd[ky][slot] = *reinterpret_cast<const f16x4 *>(p);
+            vg[ky][slot] = *reinterpret_cast<const f16x4 *>(p + F);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) vd[ky][slot][e] = vg[ky][slot][e] = (f16)0.0f;
+        }
+    };
+    // columns x0 - 1 .. x0 + PD before the first token
+#pragma unroll
+    for (int j = 0; j < 2 + PD; ++j)
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky) load(ky, x0 - 1 + j, j);
+#pragma unroll
+    for (int i = 0; i < XS; ++i) {
+        const int xx = x0 + i;
+        if (xx < Ww) {
+            // the column token i + PD needs (x0 + i + PD + 1), PD tokens ahead
+            if (i + PD < XS) {
+#pragma unroll
+                for (int ky = 0; ky < 3; ++ky) load(ky, xx + PD + 1, (i + PD + 2) % NS);
+            }
+            float ad[4], ag[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ad[e] = ag[e] = 0.0f;
+#pragma unroll
+            for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx) {
+                    const int slot = (i + kx) % NS;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        ad[e] += (float)vd[ky][slot][e] * wd[ky * 3 + kx][e];
+                        ag[e] += (float)vg[ky][slot][e] * wg[ky * 3 + kx][e];
+                    }
+                }
+            f16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float d = ad[e] + bd[e];
+                const float gt = ag[e] + bg[e];
+                o[e] = (f16)(d * silu_fast(gt));
+            }
+            *reinterpret_cast<f16x4 *>(ob + ((int64_t)y * Ww + xx) * ldo) = o;
+        }
+    }
+}
+
 // Scalar variant for channel counts that are not a multiple of 8.
 __global__ __launch_bounds__(256) void dwglu_scalar_kernel(const f16 * __restrict__ x, int64_t ldx,
                                                            const float * __restrict__ wt,
@@ -147,31 +234,50 @@ hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const flo
     const f16 * xx = reinterpret_cast<const f16 *>(x);
     f16 * oo = reinterpret_cast<f16 *>(out);
     if (vec) {
-        // Row segment length by the launch's token count (2880 channels, inputs
-        // cycled through several buffers): short segments keep small grids wide,
-        // long ones load each weight register set once for more tokens.
-        //   tokens           XS = 4     8        16
-        //   1024 (32x32)     11.2 us    12.1     19.0
-        //   2048 (2x32x32)   18.8       18.4     23.0
-        //   4096 (64x64)     35.9       32.3     32.6
-        //   9216 (96x96)     75.1       66.6     66.5
-        //   16384 (128x128)  127.4      112.6    102.0
-        //   32768            242.5      211.9    193.1
         const int64_t tokens = (int64_t)B * Hh * Ww;
         if (B > 65535) return hipErrorInvalidValue;
-        auto launch = [&](auto xs_tag, const char * name) {
+        auto launch = [&](auto xs_tag, const char * name, auto pipe_tag) {
             constexpr int XS = decltype(xs_tag)::value;
+            constexpr bool PIPE = decltype(pipe_tag)::value;
             const int64_t nseg = (Ww + XS - 1) / XS;
             if ((int64_t)Hh * nseg > 2147483647) return hipErrorInvalidValue;
             note_kernel(name);
-            hipLaunchKernelGGL((dwglu_row_kernel<XS>), dim3((F / 8 + 63) / 64, (unsigned)(Hh * nseg), B), dim3(64), 0,
-                               s, xx, ldx, wt, bias, oo, ldo, Hh, Ww, F);
+            if constexpr (PIPE)
+                hipLaunchKernelGGL((dwglu_pipe_kernel<XS>), dim3((F / 4 + 63) / 64, (unsigned)(Hh * nseg), B),
+                                   dim3(64), 0, s, xx, ldx, wt, bias, oo, ldo, Hh, Ww, F);
+            else
+                hipLaunchKernelGGL((dwglu_row_kernel<XS>), dim3((F / 8 + 63) / 64, (unsigned)(Hh * nseg), B),
+                                   dim3(64), 0, s, xx, ldx, wt, bias, oo, ldo, Hh, Ww, F);
             return hipSuccess;
         };
+        using P = std::true_type;
         hipError_t e;
-        if (tokens <= 1024) e = launch(std::integral_constant<int, 4>{}, "dwglu_row_kernel<4>");
-        else if (tokens < 12288) e = launch(std::integral_constant<int, 8>{}, "dwglu_row_kernel<8>");
-        else e = launch(std::integral_constant<int, 16>{}, "dwglu_row_kernel<16>");
+        if (F % 4 == 0 && ((reinterpret_cast<uintptr_t>(bias) & 15) == 0)) {
+            // Pipelined 4-channel kernel (bit-identical to the 8-channel row
+            // kernel), row segment by token count; alone on the GPU, 2880
+            // channels, inputs cycled through buffers past the last-level
+            // cache, us (8-channel row kernel at its best XS in brackets):
+            //   tokens           XS = 4    8      16     32
+            //   1024 (32x32)     9.55     9.86   11.23  18.09   (10.28)
+            //   4096 (64x64)     28.50    24.17  22.08  27.42   (24.34)
+            //   9216 (96x96)     77.06    63.19  59.30  66.31   (61.53)
+            //   16384 (128x128)  139.89   112.18 99.65  92.83   (97.83)
+            if (tokens <= 1024) e = launch(std::integral_constant<int, 4>{}, "dwglu_pipe_kernel<4>", P{});
+            else if (tokens <= 2048) e = launch(std::integral_constant<int, 8>{}, "dwglu_pipe_kernel<8>", P{});
+            else if (tokens < 12288) e = launch(std::integral_constant<int, 16>{}, "dwglu_pipe_kernel<16>", P{});
+            else e = launch(std::integral_constant<int, 32>{}, "dwglu_pipe_kernel<32>", P{});
+        } else {
+            // 8-channel row kernel: row segment by token count (inputs cycled)
+            //   tokens           XS = 4     8        16
+            //   1024 (32x32)     11.2 us    12.1     19.0
+            //   2048 (2x32x32)   18.8       18.4     23.0
+            //   4096 (64x64)     35.9       32.3     32.6
+            //   16384 (128x128)  127.4      112.6    102.0
+            using R = std::false_type;
+            if (tokens <= 1024) e = launch(std::integral_constant<int, 4>{}, "dwglu_row_kernel<4>", R{});
+            else if (tokens < 12288) e = launch(std::integral_constant<int, 8>{}, "dwglu_row_kernel<8>", R{});
+            else e = launch(std::integral_constant<int, 16>{}, "dwglu_row_kernel<16>", R{});
+        }
         if (e != hipSuccess) return e;
     } else {
         const int64_t total = (int64_t)B * Hh * Ww * F;
