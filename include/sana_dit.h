@@ -322,7 +322,10 @@ size_t sana_hip_linear_attention_workspace(int64_t B, int64_t N, int64_t H, int6
  * exceeds it fail with SANA_ERR_INVALID_ARGUMENT (B=2, H=16, D=72 needs 11.7 MB
  * at any N).  Every call on a GPU shares that GPU's array: calls that overlap
  * on one GPU (two streams, two threads) race.  Runs on the current device; the
- * stream must belong to it.  Results equal sana_hip_linear_attention's. */
+ * stream must belong to it.  Results equal sana_hip_linear_attention's.  The
+ * array's device address is looked up once per device, on the first call; after
+ * a hipDeviceReset the code object (and the array) is loaded anew, so this
+ * entry point must not be called across a device reset in one process. */
 int sana_hip_linear_attention_noalloc(const void * q, const void * k, const void * v, int64_t ld, void * out,
                                       int64_t ldo, int64_t B, int64_t N, int64_t H, int64_t D, void * stream);
 int sana_hip_cross_attention(const void * q, int64_t ldq, const void * k, int64_t ldk, const void * vt,

@@ -1155,12 +1155,16 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
                     sum *= a;
                 }
                 f16x8 pf[LTH][2];
+                // one fma per score on both paths: raw scores are scaled here,
+                // biased ones were scaled above and fma(s, 1, -m) rounds as s - m
+                // (a per-score select between the two forms costs a v_sub and a
+                // v_cndmask per score once the compiler if-converts it)
+                const float esc = raw ? scale2 : 1.0f;
 #pragma unroll
                 for (int t = 0; t < LTH; ++t)
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
-                        const float e = raw ? __builtin_amdgcn_exp2f(fmaf(st[t][i], scale2, -mref))
-                                            : __builtin_amdgcn_exp2f(st[t][i] - mref);
+                        const float e = __builtin_amdgcn_exp2f(fmaf(st[t][i], esc, -mref));
                         if constexpr (!ones_row) sum += e;
                         pf[t][i >> 3][i & 7] = (f16)e;
                     }

@@ -800,6 +800,8 @@ float * scratch_addr[kScratchDevices] = {};
 
 // Device address of `scratch` on the current device `dev`, looked up on the
 // first call for that device (the array's name is only a host-side stand-in).
+// The address is kept for the life of the process: a hipDeviceReset, which
+// reloads the code object and its static array, is not supported in between.
 float * device_scratch(int dev) {
     if (dev < 0 || dev >= kScratchDevices) throw_err(SANA_ERR_INVALID_ARGUMENT, "scratch: device index out of range");
     std::lock_guard<std::mutex> lock(scratch_mu);

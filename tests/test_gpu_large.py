@@ -57,6 +57,17 @@ def test_block_16384_tokens(one_block):
     _check_block(m, d, x, tmod, ctx, "N=16384 heads=36")
 
 
+def test_block_10000_tokens_short_last_chunk(one_block):
+    # 100 x 100 tokens: the chunked linear attention (above 8192 tokens per
+    # image) splits 10000 tokens into 15 chunks of 640 and a short last chunk
+    # of 400, which the 16384-token case (16 full chunks) never exercises
+    heads, m, d, tmod, ctx = one_block
+    if heads != 36:
+        pytest.skip("production head layout only on the chunked path")
+    x = O.randn((2, 10000, 1152), 10) * np.float32(0.5)
+    _check_block(m, d, x, tmod, ctx, "N=10000 heads=36")
+
+
 def test_block_4096_tokens_large_state(one_block):
     # scale_msa + 31 multiplies the self-attention q, k and v by 32, so the
     # linear-attention state reaches ~1.5e5 at 4096 tokens, past fp16's range
