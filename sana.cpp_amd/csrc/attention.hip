@@ -1018,7 +1018,9 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
         }
     };
     const int q0 = blockIdx.y * kXaQ + g * 32;  // key-split path: this wave's query group
-    if constexpr (!FLASH) load_q(q0);
+    // this wave's first query block (online-softmax path: of the first 256-query block)
+    const int qw0 = FLASH ? (blockIdx.y * qblocks * 8 + w) * 32 : q0;
+    load_q(qw0);  // in flight during the K/V staging (rows clamped into range)
 
     // K staging: thread -> chunk kc = tid & 15 (8 dims), rows kr0 + 32 j.  Every
     // load is in bounds and unconditional: rows past L repeat row L - 1 and
@@ -1095,7 +1097,10 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
         for (int qb = 0; qb < qblocks; ++qb) {
             const int qw = ((blockIdx.y * qblocks + qb) * 8 + w) * 32;
             if (qw >= N) break;
-            load_q(qw);
+            // qf holds this block's queries: requested before the staging for
+            // the first block, during the previous block's softmax otherwise
+            const int qn = qw + 8 * 32;  // this wave's queries in the next 256-query block
+            const bool next = qb + 1 < qblocks && qn < N;
             f32x16 o[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
@@ -1120,6 +1125,9 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
                         st[t] = mfma_32x32x16(kf, qf[ks], st[t]);
                     }
                 }
+                // the second half's scores are the last use of qf: the next
+                // block's queries load into it behind this block's softmax and P.V
+                if (half == 1 && next) load_q(qn);
                 float mh = -INFINITY;
                 const bool raw = ONES && !bias;
                 if (raw) {

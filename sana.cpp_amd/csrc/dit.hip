@@ -168,11 +168,22 @@ void upload_f16(DevMem & dst, const float * src, int64_t rows, int64_t cols, int
                 const std::string & tensor, int64_t row_offset = 0, int64_t total_rows = -1) {
     if (total_rows < 0) total_rows = rows;
     std::vector<half_t> h((size_t)rows * ld, (half_t)0.0f);
-    for (int64_t r = 0; r < rows; ++r)
-        for (int64_t c = 0; c < cols; ++c) {
-            const size_t i = transposed ? (size_t)(c * rows + r) : (size_t)(r * cols + c);
-            h[(size_t)r * ld + c] = to_f16_checked(src[i], tensor, i);
-        }
+    // rows converted on several host threads (a 28-block model is 600M values);
+    // the lowest source index fp16 cannot hold is reported
+    std::atomic<size_t> bad(SIZE_MAX);
+    host_parallel((size_t)rows, 16, [&](size_t r0, size_t r1) {
+        for (size_t r = r0; r < r1; ++r)
+            for (int64_t c = 0; c < cols; ++c) {
+                const size_t i = transposed ? (size_t)(c * rows + (int64_t)r) : r * (size_t)cols + (size_t)c;
+                const float v = src[i];
+                if (!(v <= kF16Max && v >= -kF16Max)) {
+                    atomic_min(bad, i);
+                    continue;
+                }
+                h[r * (size_t)ld + (size_t)c] = (half_t)v;
+            }
+    });
+    if (bad.load() != SIZE_MAX) (void)to_f16_checked(src[bad.load()], tensor, bad.load());  // throws
     if (!dst.p) dst.ensure((size_t)total_rows * ld * sizeof(half_t));
     copy_to_device(dst.as<half_t>() + (size_t)row_offset * ld, h.data(), h.size() * sizeof(half_t), "upload");
 }

@@ -6,9 +6,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <atomic>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <string>
+#include <thread>
+#include <vector>
 
 #include "../../include/sana_dit.h"
 
@@ -61,6 +66,41 @@ inline _Float16 to_f16_checked(float v, const std::string & tensor, size_t i) {
         throw_err(SANA_ERR_FORMAT, tensor + ": weight value " + buf + " is outside the fp16 operand range (|w| <= 65504)");
     }
     return (_Float16)v;
+}
+
+// Runs f(lo, hi) over contiguous ranges covering [0, n) on up to 16 host
+// threads (one range per thread, none smaller than `grain`); f must not throw.
+template <class F>
+inline void host_parallel(size_t n, size_t grain, F f) {
+    const size_t hw = std::max(1u, std::thread::hardware_concurrency());
+    size_t nt = std::min<size_t>(std::min<size_t>(16, hw), (n + grain - 1) / std::max<size_t>(grain, 1));
+    if (nt <= 1) {
+        f((size_t)0, n);
+        return;
+    }
+    const size_t per = (n + nt - 1) / nt;
+    std::vector<std::thread> th;
+    size_t t = 1;
+    try {
+        for (; t < nt; ++t) {
+            const size_t lo = t * per, hi = std::min(n, lo + per);
+            if (lo < hi) th.emplace_back(f, lo, hi);
+        }
+    } catch (...) {  // no thread to spare: range t and the ones after it run here
+        for (; t < nt; ++t) {
+            const size_t lo = t * per, hi = std::min(n, lo + per);
+            if (lo < hi) f(lo, hi);
+        }
+    }
+    f((size_t)0, std::min(n, per));
+    for (auto & x : th) x.join();
+}
+
+// Lowest index recorded by concurrent ranges (SIZE_MAX when none).
+inline void atomic_min(std::atomic<size_t> & a, size_t v) {
+    size_t cur = a.load();
+    while (v < cur && !a.compare_exchange_weak(cur, v)) {
+    }
 }
 
 // IEEE fp16 bit patterns: refuse inf and NaN (exponent field all ones).
