@@ -14,8 +14,46 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: long CPU oracle run")
 
 
+# Relative L2 errors computed by each test, printed at the end of the session
+# (also under -q), so a run's record carries the parity figures, not only pass
+# counts.  Every test still asserts against its own tolerance.
+_current = {"test": None}
+_record = {}
+
+
+@pytest.fixture(autouse=True)
+def _parity_record(request):
+    _current["test"] = request.node.nodeid
+    yield
+    _current["test"] = None
+
+
 def rel_l2(a, b):
     import numpy as np
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
-    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+    v = float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+    if _current["test"]:
+        _record.setdefault(_current["test"], []).append(v)
+    return v
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not _record:
+        return
+    # per test function (parameter sets folded): largest relative L2 and count
+    agg = {}
+    for nodeid, vals in _record.items():
+        key = nodeid.split("[")[0].split("::")[-1]
+        m, n = agg.get(key, (0.0, 0))
+        agg[key] = (max(m, max(vals)), n + len(vals))
+    terminalreporter.write_sep("-", "relative L2 per test function: max over its comparisons (count)")
+    line = ""
+    for k, (m, n) in agg.items():
+        item = f"{k} {m:.2e} ({n})"
+        if line and len(line) + len(item) + 2 > 160:
+            terminalreporter.write_line(line)
+            line = ""
+        line = f"{line}; {item}" if line else item
+    if line:
+        terminalreporter.write_line(line)
