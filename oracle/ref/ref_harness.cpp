@@ -282,6 +282,7 @@ int usage() {
         "  ref_harness digest\n"
         "  ref_harness block SELF_HEADS CROSS_HEADS SIDE T OUTDIR\n"
         "  ref_harness forward SELF_HEADS CROSS_HEADS SIDE T MASK CHECK_STEP OUTDIR\n"
+        "  ref_harness forward-hw SELF_HEADS CROSS_HEADS H W T OUTDIR\n"
         "  ref_harness loop SELF_HEADS CROSS_HEADS SIDE STEPS GUIDANCE MASK OUTDIR\n"
         "  ref_harness time-block SELF_HEADS CROSS_HEADS BATCH SIDE REPS\n"
         "  ref_harness time-forward SELF_HEADS CROSS_HEADS SIDE\n"
@@ -362,6 +363,23 @@ int main(int argc, char ** argv) {
                 dump(out, "step0", ref_step);
                 if (!same) return 1;
             }
+            return 0;
+        }
+        if (mode == "forward-hw" && argc == 8) {
+            // forward_noise_pred on an H x W latent (any H * W the reference
+            // accepts: a perfect square), no mask
+            const size_t sh = std::stoul(argv[2]), ch = std::stoul(argv[3]);
+            const size_t hh = std::stoul(argv[4]), ww = std::stoul(argv[5]);
+            const float t = std::stof(argv[6]);
+            const std::string out = argv[7];
+            SanaDenoiserWeights w = make_denoiser(g, d, d.layers, sh, ch);
+            Tensor latent = randn_torch_cpu({1, d.latent, hh, ww}, 42);
+            Tensor caption = randn_torch_cpu({2, 300, d.caption}, 43);
+            Tensor ctx = project_caption_context(caption, w.caption.linear_1_weight, &w.caption.linear_1_bias,
+                                                 w.caption.linear_2_weight, &w.caption.linear_2_bias,
+                                                 w.caption_norm_weight);
+            Tensor np = forward_noise_pred(latent, ctx, t, w, nullptr);
+            dump(out, "noise_pred", np);
             return 0;
         }
         if (mode == "loop" && argc == 9) {

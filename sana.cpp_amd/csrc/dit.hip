@@ -1114,8 +1114,14 @@ int sana_dit_get_context(sana_dit * c, float * out) {
 
 static int check_forward_args(sana_dit * c, int64_t Bl, int64_t Hh, int64_t Ww) {
     if (Bl <= 0 || Hh <= 0 || Ww <= 0) return set_err(SANA_ERR_INVALID_ARGUMENT, "latent dims must be positive");
-    if (Hh != Ww) return set_err(SANA_ERR_INVALID_ARGUMENT, "token count must form a square grid");
     if (Hh * Ww > 65535) return set_err(SANA_ERR_INVALID_ARGUMENT, "grid too large");
+    // Any H x W whose token count is a perfect square, as infer_square_side
+    // (src/transformer.cpp:18-24): the patch embedding and the final layer only
+    // see the flattened NCHW pixel index y * W + x, and the depthwise conv of
+    // every block runs on the side x side grid of the tokens
+    // (src/transformer.cpp:765-767), whatever H and W are.
+    const int64_t N = Hh * Ww, side = (int64_t)std::llround(std::sqrt((double)N));
+    if (side * side != N) return set_err(SANA_ERR_INVALID_ARGUMENT, "token count must form a square grid");
     (void)c;
     return SANA_OK;
 }

@@ -11,7 +11,7 @@
 //
 // Limits of the device path (std::invalid_argument when exceeded): hidden size
 // <= 2048, self head_dim <= 100, latent channels <= 32, caption length <= 512,
-// square latents (H == W), the same head counts in every block.
+// the same head counts in every block.
 #include "transformer.h"
 
 #include <algorithm>

@@ -15,6 +15,9 @@ Cases (one .npz each):
                (checked bit-exact against forward + CFG + scheduler)
   cfg2_mask    same forward with the Gemma padding mask (1 / 40 real tokens)
   cfg3         20-step DPM-Solver++ loop, guidance 4.5, final latent
+  nonsquare    full 28-block forward on a 4x16 latent (64 tokens, which the
+               reference runs through each block's depthwise conv as an 8x8
+               grid), t=999, no mask
   cfg5         full 28-block forward at 4096 px (latent 128x128, 16384
                tokens), t=999, no mask
   vae_small    the reference's run_vae_decode on the small synthetic DC-AE
@@ -54,6 +57,7 @@ CASES = {
     "cfg2_mask": (["forward", "36", "16", "32", "999", "1", "0"],
                   {"context": (2, 300, 1152), "noise_pred": (2, 32, 32, 32), "guided": (1, 32, 32, 32)}),
     "cfg3": (["loop", "36", "16", "32", "20", "4.5", "0"], {"final_latent": (1, 32, 32, 32)}),
+    "nonsquare": (["forward-hw", "36", "16", "4", "16", "999"], {"noise_pred": (2, 32, 4, 16)}),
     "cfg5": (["forward", "36", "16", "128", "999", "0", "0"],
              {"context": (2, 300, 1152), "noise_pred": (2, 32, 128, 128), "guided": (1, 32, 128, 128)}),
     "vae_small": (["vae", "small", "8"],

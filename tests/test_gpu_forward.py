@@ -62,6 +62,20 @@ def test_forward_1024px_vs_reference(full_model, case, masked):
     assert gerr < TOL_FORWARD
 
 
+def test_forward_nonsquare_vs_reference(full_model):
+    """A 4x16 latent (64 tokens) against the reference's own forward of it:
+    the reference runs each block's depthwise conv on the 8x8 token grid
+    (src/transformer.cpp:765-767), and so does the device path."""
+    m, d = full_model
+    fx = golden("nonsquare")
+    latent = O.randn((1, 32, 4, 16), 42)
+    d.set_context(O.randn((2, 300, 2304), 43), projected=False)
+    got = d.forward(latent, 999.0)
+    err = rel_l2(got, fx["noise_pred"])
+    print(f"nonsquare 4x16: noise_pred rel_l2 {err:.2e}")
+    assert err < TOL_FORWARD
+
+
 def test_forward_4096px_vs_reference(full_model):
     """4096 px (latent 128x128, 16384 image tokens): the reference's CPU forward
     is too large to store whole, so the fixture keeps a strided subsample of
@@ -183,6 +197,34 @@ def test_small_forward_batch2_vs_oracle(small_model):
     err = rel_l2(got, ref)
     print(f"small forward, latent batch 2: rel_l2 {err:.2e}")
     assert err < TOL_FORWARD
+
+
+def test_small_forward_nonsquare_latent(small_model):
+    """A 4x16 latent (64 tokens): the reference accepts any H x W whose token
+    count is a perfect square and runs each block's depthwise conv on the
+    side x side token grid (src/transformer.cpp:18-24, 765-767).  The device
+    forward matches the oracle there, equals the 8x8 view of the same data bit
+    for bit (patch embedding and final layer see only the flattened index), and
+    a 4x8 latent (32 tokens) is refused with the reference's message."""
+    import sana_dit
+    m, d = small_model
+    latent = O.randn((1, 8, 4, 16), 21)
+    caption = O.randn((2, 16, 96), 22)
+    ref = m.forward(latent, m.project_caption(caption), 420.0)
+    d.set_context(caption, projected=False)
+    got = d.forward(latent, 420.0)
+    assert got.shape == (2, 8, 4, 16)
+    err = rel_l2(got, ref)
+    print(f"small forward, 4x16 latent: rel_l2 {err:.2e}")
+    assert err < TOL_FORWARD
+    sq = d.forward(latent.reshape(1, 8, 8, 8), 420.0)
+    assert np.array_equal(got.reshape(sq.shape), sq)
+    ts, sg = O.scheduler_timesteps(3)
+    loop_ns = d.denoise_loop(latent, ts, sg, 4.5)
+    loop_sq = d.denoise_loop(latent.reshape(1, 8, 8, 8), ts, sg, 4.5)
+    assert np.array_equal(loop_ns.reshape(loop_sq.shape), loop_sq)
+    with pytest.raises(sana_dit.SanaError, match="token count must form a square grid"):
+        d.forward(O.randn((1, 8, 4, 8), 23), 420.0)
 
 
 def test_small_loop_batch2_vs_oracle(small_model):

@@ -89,6 +89,21 @@ def test_full_forward_1024px(model, case, masked):
     check_tensor(fx, "guided", guided)
 
 
+def test_full_forward_nonsquare_latent(model):
+    """A 4x16 latent: the reference accepts any H x W whose token count is a
+    perfect square and runs each block's depthwise conv on the side x side
+    token grid (src/transformer.cpp:18-24, 765-767); the oracle does the same,
+    so its 4x16 forward is the reference's bit for bit and equals its own 8x8
+    forward of the same flattened data."""
+    fx = load("nonsquare")
+    latent = O.randn((1, 32, 4, 16), 42)
+    ctx = model.project_caption(O.randn((2, 300, 2304), 43))
+    np_ = model.forward(latent, ctx, 999.0)
+    check_tensor(fx, "noise_pred", np_)
+    sq = model.forward(latent.reshape(1, 32, 8, 8), ctx, 999.0)
+    assert np.array_equal(np_.reshape(sq.shape), sq)
+
+
 @pytest.mark.skipif(os.environ.get("SANA_SLOW_ORACLE") != "1",
                     reason="20 full forwards on the CPU (~10 min); set SANA_SLOW_ORACLE=1")
 def test_denoise_loop_1024px(model):
