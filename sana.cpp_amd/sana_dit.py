@@ -3,6 +3,10 @@
 This is the Python-side stub a caller binds; tests and bench.py use it.  It
 never falls back to anything: if the library is missing or a call fails, it
 raises.
+
+Callers that also pass torch tensors must import torch before the first call
+here loads the library: torch carries its own HIP runtime, which finds no GPU
+when the system ROCm runtime that libsana_dit.so links was loaded first.
 """
 import ctypes
 import os

@@ -8,6 +8,15 @@ for p in (os.path.join(ROOT, "tests"), os.path.join(ROOT, "sana.cpp_amd")):
     if p not in sys.path:
         sys.path.insert(0, p)
 
+# torch ships its own HIP runtime; loaded after libsana_dit.so (which links
+# the system ROCm's), it finds no GPU.  Importing torch first, before any test
+# loads the library, keeps the tests that hand torch tensors to the C ABI
+# working in any order or selection.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through libsana_dit.so on cuda:0)")
@@ -36,6 +45,18 @@ def rel_l2(a, b):
     if _current["test"]:
         _record.setdefault(_current["test"], []).append(v)
     return v
+
+
+def spread_subsample(arr, fx, name):
+    """(got, want) at the fixture's spread indices (k * step) mod size, or None
+    when the fixture has no spread subsample of `name`."""
+    import numpy as np
+    if name + "__spread" not in fx:
+        return None
+    want = fx[name + "__spread"]
+    flat = np.asarray(arr).reshape(-1)
+    idx = (np.arange(want.size, dtype=np.int64) * int(fx[name + "__spread_step"])) % flat.size
+    return flat[idx], want
 
 
 def pytest_terminal_summary(terminalreporter):

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from conftest import rel_l2
+from conftest import rel_l2, spread_subsample
 
 pytestmark = pytest.mark.gpu
 
@@ -78,8 +78,9 @@ def test_forward_nonsquare_vs_reference(full_model):
 
 def test_forward_4096px_vs_reference(full_model):
     """4096 px (latent 128x128, 16384 image tokens): the reference's CPU forward
-    is too large to store whole, so the fixture keeps a strided subsample of
-    noise_pred and guided plus their L2 norms."""
+    is too large to store whole, so the fixture keeps, of noise_pred and
+    guided, a strided subsample, 65536 values spread over every row and column
+    of the grid, and their L2 norms."""
     path = os.path.join(GOLDEN, "cfg5.npz")
     if not os.path.exists(path):
         pytest.skip("cfg5 golden not generated")
@@ -98,6 +99,36 @@ def test_forward_4096px_vs_reference(full_model):
         print(f"cfg5 {name}: subsample rel_l2 {res[name]:.2e}, L2 norm rel diff {norm_err:.2e}")
         assert res[name] < TOL_FORWARD
         assert norm_err < TOL_FORWARD
+        sp = spread_subsample(arr, fx, name)
+        if sp is not None:
+            serr = rel_l2(*sp)
+            print(f"cfg5 {name}: spread subsample ({sp[1].size} values) rel_l2 {serr:.2e}")
+            assert serr < TOL_FORWARD
+
+
+@pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
+def test_step_device_matches_context_then_forward(full_model, masked):
+    """sana_dit_step_device (caption projection, cross K/V and forward in one
+    graph, the forward's head beside the context GEMMs) gives the noise
+    prediction of sana_dit_set_context + sana_dit_forward bit for bit."""
+    import torch
+    m, d = full_model
+    latent = O.randn((1, 32, 32, 32), 42)
+    caption = O.randn((2, 300, 2304), 43)
+    bias = O.mask_bias(300, 1, 40) if masked else None
+    d.set_context(caption, projected=False, bias=bias)
+    ref = d.forward(latent, 999.0)
+    dev = torch.device("cuda:0")
+    d_cap = torch.from_numpy(caption).to(dev)
+    d_lat = torch.from_numpy(latent).to(dev)
+    d_bias = torch.from_numpy(np.ascontiguousarray(bias, np.float32)).to(dev) if masked else None
+    out = torch.empty((2, 32, 32, 32), device=dev)
+    for _ in range(2):  # the second call replays the captured graph
+        out.fill_(float("nan"))
+        d.step_device(d_cap, 300, d_bias, d_lat, (1, 32, 32, 32), 999.0, out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert np.array_equal(got, ref)
 
 
 def test_forward_deterministic(full_model):
