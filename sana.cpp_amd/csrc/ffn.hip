@@ -262,7 +262,19 @@ hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const flo
             //   4096 (64x64)     28.50    24.17  22.08  27.42   (24.34)
             //   9216 (96x96)     77.06    63.19  59.30  66.31   (61.53)
             //   16384 (128x128)  139.89   112.18 99.65  92.83   (97.83)
-            if (tokens <= 1024) e = launch(std::integral_constant<int, 4>{}, "dwglu_pipe_kernel<4>", P{});
+            // The VAE's power-of-two channel counts put the rows of the token
+            // grid a power of two of bytes apart (2F halves per token), and
+            // there the row kernel with 16-token segments wins from 16M
+            // outputs on: F = 2048 at 16384 tokens 62.6 us against 65.2 /
+            // 71.8 (pipe16 / pipe32), F = 4096 at 4096 tokens 27.2 against
+            // 30.1 / 29.7; F = 4096 at 1024 tokens pipe8 10.5 against pipe4
+            // 11.7.  F = 2048 at 4096 tokens keeps pipe16 (17.0 against 19.6).
+            const bool pow2 = (F & (F - 1)) == 0;
+            if (pow2 && tokens * F >= (int64_t)1 << 24)
+                e = launch(std::integral_constant<int, 16>{}, "dwglu_row_kernel<16>", std::false_type{});
+            else if (tokens <= 1024 && F >= 4096)
+                e = launch(std::integral_constant<int, 8>{}, "dwglu_pipe_kernel<8>", P{});
+            else if (tokens <= 1024) e = launch(std::integral_constant<int, 4>{}, "dwglu_pipe_kernel<4>", P{});
             else if (tokens <= 2048) e = launch(std::integral_constant<int, 8>{}, "dwglu_pipe_kernel<8>", P{});
             else if (tokens < 12288) e = launch(std::integral_constant<int, 16>{}, "dwglu_pipe_kernel<16>", P{});
             else e = launch(std::integral_constant<int, 32>{}, "dwglu_pipe_kernel<32>", P{});
