@@ -279,7 +279,10 @@ def model_load_times(sana_dit, torch, weights):
     F32 (the reference's payload type) and as F16 (the linear weights go to the
     fp16 operand buffers as stored, no fp32 round trip), each into a fresh
     context.  The file was just written, so it is read from the page cache:
-    this is the host-side conversion + upload cost, not disk speed."""
+    this is the host-side conversion + upload cost, not disk speed.  Then the
+    same F32 file through sana_dit_load_gguf_cached: the first call loads the
+    GGUF and writes the packed device-layout cache, the second loads the cache
+    (both into fresh contexts)."""
     import tempfile
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from gguf_writer import GGML_F16, GGML_F32, write_gguf
@@ -298,13 +301,31 @@ def model_load_times(sana_dit, torch, weights):
             torch.cuda.synchronize()
             sec = time.perf_counter() - t0
             d.close()
-            os.remove(path)
             out[tag] = {"s": round(sec, 3), "file_gb": round(size / 1e9, 3), "gb_per_s": round(size / 1e9 / sec, 2)}
             progress(f"GGUF load ({tag}) {sec:.2f} s")
+            if tag == "f32":
+                cache = os.path.join(tmp, "model.sanapk")
+                for key in ("f32_cache_write", "packed_cache"):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    d = sana_dit.Dit(**DIMS, device=0)
+                    used = d.load_gguf_cached(path, path, path, cache)
+                    d.check_weights()
+                    torch.cuda.synchronize()
+                    sec = time.perf_counter() - t0
+                    d.close()
+                    if used != (key == "packed_cache"):
+                        raise RuntimeError(f"packed cache {'not ' if used is False else ''}used in {key}")
+                    out[key] = {"s": round(sec, 3), "file_gb": round(os.path.getsize(cache) / 1e9, 3)}
+                    progress(f"GGUF load through the packed cache ({key}) {sec:.2f} s")
+                os.remove(cache)
+            os.remove(path)
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
     out["note"] = ("sana_dit_load_gguf of the 28 blocks + caption + denoiser tensors from one GGUF file in the page "
-                   "cache into a fresh context (context creation included)")
+                   "cache into a fresh context (context creation included); f32_cache_write: the same F32 file "
+                   "through sana_dit_load_gguf_cached with no cache (GGUF load + packed image written); "
+                   "packed_cache: the second such call, from the packed device-layout image")
     return out
 
 

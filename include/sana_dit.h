@@ -103,6 +103,36 @@ int sana_dit_check_weights(sana_dit * ctx);
 int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * caption_path,
                        const char * denoiser_path);
 
+/* Pre-packed device layouts cached on disk (the GGUF row's packed-layout
+ * cache; no counterpart in the reference, which converts on every load).
+ *
+ * sana_dit_save_packed writes every weight of a fully loaded context, as the
+ * device holds it (fp16 GEMM operands K-padded and fused, cross K/V stacked
+ * over blocks, fp32 vectors), with the model dimensions, the caller's 64-bit
+ * key of the source weights and a checksum per buffer.  The file appears
+ * under `path` only when complete (written under a temporary name, then
+ * renamed).  SANA_ERR_STATE if a weight is missing, SANA_ERR_IO on a write
+ * failure.
+ *
+ * sana_dit_load_packed maps such a file and uploads it with one copy per
+ * buffer.  The dimensions must equal the context's and `key` the saved one;
+ * every buffer's size and checksum is verified before anything is uploaded,
+ * so a refused image leaves the context unchanged.  SANA_ERR_IO if the file
+ * cannot be opened, SANA_ERR_FORMAT for any mismatch or damage.  Set the
+ * conditioning again after loading weights. */
+int sana_dit_save_packed(sana_dit * ctx, const char * path, uint64_t key);
+int sana_dit_load_packed(sana_dit * ctx, const char * path, uint64_t key);
+
+/* sana_dit_load_gguf through a packed cache at cache_path: the key is derived
+ * from the three GGUF files (path, size, modification time and the first MiB
+ * of each).  A cache whose key, dimensions and checksums match is loaded
+ * (*used_cache = 1); otherwise the GGUF files are loaded and the cache is
+ * rewritten (*used_cache = 0).  Writing the cache is best effort: when it
+ * fails the call still returns SANA_OK with the weights loaded.  used_cache
+ * may be NULL. */
+int sana_dit_load_gguf_cached(sana_dit * ctx, const char * model_path, const char * caption_path,
+                              const char * denoiser_path, const char * cache_path, int * used_cache);
+
 /* Conditioning for the following forwards.  projected = 0: data is the raw
  * caption [B, L, caption_dim] and the caption projection
  * (project_caption_context, src/transformer_ops.cpp:64-76) runs on the GPU;

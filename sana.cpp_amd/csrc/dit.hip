@@ -14,7 +14,11 @@
 // No layout transposes remain: tokens_to_grid/grid_to_tokens/split_heads/
 // merge_heads of the reference are address arithmetic here, and the CFG
 // batch repeat is two batch rows reading the same latent.
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <cmath>
@@ -824,6 +828,123 @@ float * device_scratch(int dev) {
     }
     return scratch_addr[dev];
 }
+
+// ---------------------------------------------------------------------------
+// Packed weight image: every device weight buffer of a context in its device
+// layout (fp16 GEMM operands K-padded and fused, stacked cross K/V, tap-major
+// depthwise taps, fp32 vectors), so a later load is one mapped read and one
+// copy per buffer, with no conversion or packing.
+//   header | uploaded tensor names ('\n'-joined) | 3 flag bytes per block
+//   (has_ln1, has_ln2, has_qkv_bias) | buffer table | payloads (4 KiB aligned)
+// Each table entry holds the buffer's bytes, file offset and checksum.
+constexpr char kPackMagic[8] = {'S', 'A', 'N', 'A', 'P', 'K', '0', '1'};
+constexpr uint32_t kPackVersion = 1;
+constexpr uint64_t kPackAlign = 4096;
+
+struct PackHeader {
+    char magic[8];
+    uint32_t version, nbuf;
+    int64_t dims[10];       // layers, hidden, ffn, caption_dim, latent_channels, self_heads, cross_heads, Cp, Fp, Ccap_p
+    uint64_t key;           // caller's key of the source weights (0: none)
+    uint64_t names_bytes, flags_bytes, table_offset, file_bytes;
+};
+struct PackEntry {
+    uint64_t bytes, offset, checksum;
+};
+
+// The buffers in file order with the bytes each must hold; `optional` ones
+// (q|k|v bias, LayerNorm affine) may be absent (0 bytes).
+struct PackBuf {
+    DevMem * m;
+    uint64_t bytes;
+    bool optional;
+};
+constexpr size_t kPackTop = 21, kPackPerBlock = 17;  // entries before the blocks, entries per block
+// per-block entry indices of the flagged optional buffers
+constexpr size_t kPackQkvBias = 1, kPackLn1 = 13, kPackLn2 = 15;
+
+std::vector<PackBuf> pack_buffers(sana_dit * c) {
+    const uint64_t L = c->L_, C = c->C, E = c->E, Cp = c->Cp, Fp = c->Fp, Cl = c->Cl;
+    std::vector<PackBuf> v = {
+        {&c->w_k_all, L * C * Cp * 2, false}, {&c->b_k_all, L * C * 4, false},  {&c->w_v_all, L * C * Cp * 2, false},
+        {&c->b_v_all, L * C * 4, false},      {&c->sst_all, L * 6 * C * 4, false},
+        {&c->w_cap1, C * (uint64_t)c->Ccap_p * 2, false}, {&c->b_cap1, C * 4, false},
+        {&c->w_cap2, C * Cp * 2, false},      {&c->b_cap2, C * 4, false},       {&c->cap_norm, C * 4, false},
+        {&c->w_patch_t, Cl * C * 4, false},   {&c->b_patch, C * 4, false},      {&c->w_t1, C * 256 * 4, false},
+        {&c->b_t1, C * 4, false},             {&c->w_t2, C * C * 4, false},     {&c->b_t2, C * 4, false},
+        {&c->w_tp, 6 * C * C * 4, false},     {&c->b_tp, 6 * C * 4, false},     {&c->sst_final, 2 * C * 4, false},
+        {&c->w_proj, C * Cl * 4, false},      {&c->b_proj, Cl * 4, false},
+    };
+    if (v.size() != kPackTop) throw_err(SANA_ERR_STATE, "packed image layout");
+    for (auto & bp : c->blocks) {
+        BlockDev & w = *bp;
+        const PackBuf blk[] = {
+            {&w.w_qkv, 3 * C * Cp * 2, false}, {&w.b_qkv, 3 * C * 4, true}, {&w.w_out, C * Cp * 2, false},
+            {&w.b_out, C * 4, false},          {&w.w_cq, C * Cp * 2, false},  {&w.b_cq, C * 4, false},
+            {&w.w_co, C * Cp * 2, false},      {&w.b_co, C * 4, false},       {&w.w_inv, E * Cp * 2, false},
+            {&w.b_inv, E * 4, false},          {&w.w_dw, 9 * E * 4, false},   {&w.b_dw, E * 4, false},
+            {&w.w_pt, C * Fp * 2, false},      {&w.ln1_g, C * 4, true},       {&w.ln1_b, C * 4, true},
+            {&w.ln2_g, C * 4, true},           {&w.ln2_b, C * 4, true},
+        };
+        static_assert(sizeof(blk) / sizeof(blk[0]) == kPackPerBlock, "block entry count");
+        v.insert(v.end(), std::begin(blk), std::end(blk));
+    }
+    return v;
+}
+
+void pack_dims(const sana_dit * c, int64_t * d) {
+    const int64_t v[10] = {c->L_, c->C, c->E, c->Ccap, c->Cl, c->Hs, c->Hc, c->Cp, c->Fp, c->Ccap_p};
+    std::copy(v, v + 10, d);
+}
+
+// 64-bit FNV-1a over the 8-byte words of fixed 4 MiB chunks, the chunk values
+// folded in order (the same result on any number of threads).
+uint64_t pack_checksum(const unsigned char * p, uint64_t n) {
+    constexpr uint64_t kChunk = 4u << 20, kBasis = 14695981039346656037ULL, kPrime = 1099511628211ULL;
+    const uint64_t nch = (n + kChunk - 1) / kChunk;
+    std::vector<uint64_t> hs((size_t)nch);
+    host_parallel((size_t)nch, 1, [&](size_t c0, size_t c1) {
+        for (size_t ci = c0; ci < c1; ++ci) {
+            const uint64_t lo = ci * kChunk, hi = std::min(n, lo + kChunk);
+            uint64_t h = kBasis, i = lo;
+            for (; i + 8 <= hi; i += 8) {
+                uint64_t w;
+                std::memcpy(&w, p + i, 8);
+                h = (h ^ w) * kPrime;
+            }
+            for (; i < hi; ++i) h = (h ^ p[i]) * kPrime;
+            hs[ci] = h;
+        }
+    });
+    uint64_t h = kBasis ^ n;
+    for (uint64_t x : hs) h = (h ^ x) * kPrime;
+    return h;
+}
+
+// Read-only mapping of a whole file, unmapped on scope exit.
+struct FileMap {
+    const unsigned char * p = nullptr;
+    size_t n = 0;
+    explicit FileMap(const std::string & path) {
+        const int fd = open(path.c_str(), O_RDONLY);
+        if (fd < 0) throw_err(SANA_ERR_IO, "cannot open packed weights: " + path);
+        struct stat st;
+        if (fstat(fd, &st) != 0 || st.st_size <= 0) {
+            close(fd);
+            throw_err(SANA_ERR_FORMAT, "packed weights file is empty: " + path);
+        }
+        n = (size_t)st.st_size;
+        void * m = mmap(nullptr, n, PROT_READ, MAP_PRIVATE, fd, 0);
+        close(fd);
+        if (m == MAP_FAILED) throw_err(SANA_ERR_IO, "cannot map packed weights: " + path);
+        p = static_cast<const unsigned char *>(m);
+    }
+    ~FileMap() {
+        if (p) munmap(const_cast<unsigned char *>(p), n);
+    }
+    FileMap(const FileMap &) = delete;
+    FileMap & operator=(const FileMap &) = delete;
+};
 }  // namespace
 
 extern "C" {
@@ -1076,6 +1197,153 @@ int sana_dit_set_block_norm(sana_dit * c, int64_t blk, int which, const float * 
 int sana_dit_check_weights(sana_dit * c) {
     if (!c) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
     return guarded([&] { check_ready(c); });
+}
+
+int sana_dit_save_packed(sana_dit * c, const char * path, uint64_t key) {
+    if (!c || !path) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] {
+        check_ready(c);
+        const std::vector<PackBuf> bufs = pack_buffers(c);
+        PackHeader hd{};
+        std::memcpy(hd.magic, kPackMagic, 8);
+        hd.version = kPackVersion;
+        hd.nbuf = (uint32_t)bufs.size();
+        pack_dims(c, hd.dims);
+        hd.key = key;
+        std::string names;
+        for (const auto & kv : c->have) names += kv.first + "\n";
+        std::vector<uint8_t> flags;
+        for (auto & bp : c->blocks) {
+            flags.push_back(bp->has_ln1);
+            flags.push_back(bp->has_ln2);
+            flags.push_back(bp->has_qkv_bias);
+        }
+        hd.names_bytes = names.size();
+        hd.flags_bytes = flags.size();
+        hd.table_offset = sizeof(PackHeader) + names.size() + flags.size();
+        std::vector<PackEntry> tab(bufs.size());
+        uint64_t off = hd.table_offset + tab.size() * sizeof(PackEntry);
+        for (size_t i = 0; i < bufs.size(); ++i) {
+            const PackBuf & b = bufs[i];
+            const uint64_t have = b.m->p ? b.bytes : 0;
+            if (b.m->p && b.m->bytes < b.bytes)
+                throw_err(SANA_ERR_STATE, "device weight buffer smaller than its layout (buffer " + std::to_string(i) + ")");
+            if (!have && !b.optional)
+                throw_err(SANA_ERR_STATE, "device weight buffer missing (buffer " + std::to_string(i) + ")");
+            off = (off + kPackAlign - 1) / kPackAlign * kPackAlign;
+            tab[i].bytes = have;
+            tab[i].offset = off;
+            off += have;
+        }
+        hd.file_bytes = off;
+        // written to a temporary name and renamed, so a reader never maps a partial image
+        const std::string tmp = std::string(path) + ".tmp" + std::to_string((long long)getpid());
+        FILE * f = std::fopen(tmp.c_str(), "wb");
+        if (!f) throw_err(SANA_ERR_IO, "cannot write packed weights: " + tmp);
+        bool ok = true;
+        std::vector<unsigned char> host;
+        try {
+            hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+            for (size_t i = 0; i < bufs.size() && ok; ++i) {
+                if (!tab[i].bytes) continue;
+                host.resize(tab[i].bytes);
+                hip_check(hipMemcpy(host.data(), bufs[i].m->p, tab[i].bytes, hipMemcpyDeviceToHost), "download weights");
+                tab[i].checksum = pack_checksum(host.data(), tab[i].bytes);
+                ok = std::fseek(f, (long)tab[i].offset, SEEK_SET) == 0 &&
+                     std::fwrite(host.data(), 1, tab[i].bytes, f) == tab[i].bytes;
+            }
+            ok = ok && std::fseek(f, 0, SEEK_SET) == 0 && std::fwrite(&hd, sizeof(hd), 1, f) == 1 &&
+                 std::fwrite(names.data(), 1, names.size(), f) == names.size() &&
+                 std::fwrite(flags.data(), 1, flags.size(), f) == flags.size() &&
+                 std::fwrite(tab.data(), sizeof(PackEntry), tab.size(), f) == tab.size();
+            // the full length even when the image ends in absent (zero-byte) buffers
+            ok = ok && std::fflush(f) == 0 && ftruncate(fileno(f), (off_t)hd.file_bytes) == 0;
+        } catch (...) {
+            std::fclose(f);
+            std::remove(tmp.c_str());
+            throw;
+        }
+        ok = (std::fclose(f) == 0) && ok;
+        if (!ok || std::rename(tmp.c_str(), path) != 0) {
+            std::remove(tmp.c_str());
+            throw_err(SANA_ERR_IO, std::string("cannot write packed weights: ") + path);
+        }
+    });
+}
+
+int sana_dit_load_packed(sana_dit * c, const char * path, uint64_t key) {
+    if (!c || !path) return set_err(SANA_ERR_INVALID_ARGUMENT, "null argument");
+    return guarded([&] {
+        const FileMap fm(path);
+        const std::vector<PackBuf> bufs = pack_buffers(c);
+        auto bad = [&](const std::string & why) { throw_err(SANA_ERR_FORMAT, std::string(path) + ": " + why); };
+        if (fm.n < sizeof(PackHeader)) bad("truncated packed weights");
+        PackHeader hd;
+        std::memcpy(&hd, fm.p, sizeof(hd));
+        if (std::memcmp(hd.magic, kPackMagic, 8) != 0) bad("not a packed weight image");
+        if (hd.version != kPackVersion) bad("packed weight image version " + std::to_string(hd.version) + " is not supported");
+        int64_t dims[10];
+        pack_dims(c, dims);
+        if (std::memcmp(dims, hd.dims, sizeof(dims)) != 0) bad("packed weights are for other model dimensions");
+        if (hd.key != key) bad("packed weights were written from other source weights (key mismatch)");
+        if (hd.nbuf != bufs.size() || hd.file_bytes != fm.n || hd.flags_bytes != 3 * c->blocks.size() ||
+            hd.names_bytes > fm.n || hd.table_offset != sizeof(PackHeader) + hd.names_bytes + hd.flags_bytes ||
+            hd.table_offset + (uint64_t)hd.nbuf * sizeof(PackEntry) > fm.n)
+            bad("packed weight image is truncated or inconsistent");
+        std::vector<PackEntry> tab(hd.nbuf);
+        std::memcpy(tab.data(), fm.p + hd.table_offset, tab.size() * sizeof(PackEntry));
+        const uint8_t * flags = fm.p + sizeof(PackHeader) + hd.names_bytes;
+        for (size_t i = 0; i < bufs.size(); ++i) {
+            const PackEntry & e = tab[i];
+            const bool absent_ok = bufs[i].optional && e.bytes == 0;
+            if (!absent_ok && e.bytes != bufs[i].bytes)
+                bad("buffer " + std::to_string(i) + " holds " + std::to_string(e.bytes) + " bytes, the layout needs " +
+                    std::to_string(bufs[i].bytes));
+            if (e.offset % kPackAlign || e.offset > fm.n || e.bytes > fm.n - e.offset)
+                bad("buffer " + std::to_string(i) + " lies outside the file");
+        }
+        for (size_t b = 0; b < c->blocks.size(); ++b) {
+            // a flag set needs its buffers
+            const size_t base = kPackTop + b * kPackPerBlock;
+            const bool ln1 = flags[3 * b] != 0, ln2 = flags[3 * b + 1] != 0, qb = flags[3 * b + 2] != 0;
+            if ((ln1 && (!tab[base + kPackLn1].bytes || !tab[base + kPackLn1 + 1].bytes)) ||
+                (ln2 && (!tab[base + kPackLn2].bytes || !tab[base + kPackLn2 + 1].bytes)) ||
+                (qb && !tab[base + kPackQkvBias].bytes))
+                bad("block " + std::to_string(b) + " flags a buffer the image lacks");
+        }
+        // every checksum before any upload, so a bad image changes nothing
+        for (size_t i = 0; i < bufs.size(); ++i)
+            if (tab[i].bytes && pack_checksum(fm.p + tab[i].offset, tab[i].bytes) != tab[i].checksum)
+                bad("checksum mismatch in buffer " + std::to_string(i));
+        for (size_t i = 0; i < bufs.size(); ++i) {
+            if (!tab[i].bytes) continue;
+            DevMem & m = *bufs[i].m;
+            if (m.p && m.bytes < tab[i].bytes) {
+                hip_check(hipFree(m.p), "hipFree");
+                m.p = nullptr;
+                m.bytes = 0;
+            }
+            if (!m.p) m.ensure(tab[i].bytes, false);
+            copy_to_device(m.p, fm.p + tab[i].offset, tab[i].bytes, "upload packed weights");
+        }
+        for (size_t b = 0; b < c->blocks.size(); ++b) {
+            c->blocks[b]->has_ln1 = flags[3 * b] != 0;
+            c->blocks[b]->has_ln2 = flags[3 * b + 1] != 0;
+            c->blocks[b]->has_qkv_bias = flags[3 * b + 2] != 0;
+        }
+        const char * nm = reinterpret_cast<const char *>(fm.p + sizeof(PackHeader));
+        std::string cur;
+        for (uint64_t i = 0; i < hd.names_bytes; ++i) {
+            if (nm[i] == '\n') {
+                if (!cur.empty()) c->have[cur] = 1;
+                cur.clear();
+            } else {
+                cur += nm[i];
+            }
+        }
+        drop_graphs(c);
+        check_ready(c);
+    });
 }
 
 int sana_dit_set_context(sana_dit * c, const float * data, int64_t B, int64_t L, int64_t dim, int projected,

@@ -1,6 +1,9 @@
 // GGUF entry points of the C ABI: sana_dit_load_gguf (the three-file loader of
 // load_denoiser_weights, src/transformer.cpp:453-488) and the index
 // inspection helpers.
+#include <sys/stat.h>
+
+#include <cstdio>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -104,6 +107,30 @@ std::shared_ptr<sana::gguf::Index> cached_index(const std::string & path) {
     return g_cache;
 }
 
+// Key of a set of source files: FNV-1a over each path, size, modification
+// time and first MiB (the GGUF header and tensor directory).
+uint64_t source_key(const char * const * paths, int n) {
+    uint64_t h = 14695981039346656037ULL;
+    auto mix = [&](const void * p, size_t len) {
+        const unsigned char * b = static_cast<const unsigned char *>(p);
+        for (size_t i = 0; i < len; ++i) h = (h ^ b[i]) * 1099511628211ULL;
+    };
+    std::vector<unsigned char> head(1u << 20);
+    for (int i = 0; i < n; ++i) {
+        struct stat st;
+        if (stat(paths[i], &st) != 0) throw Err{SANA_ERR_IO, std::string("cannot stat ") + paths[i]};
+        mix(paths[i], std::strlen(paths[i]) + 1);
+        const int64_t meta[3] = {(int64_t)st.st_size, (int64_t)st.st_mtim.tv_sec, (int64_t)st.st_mtim.tv_nsec};
+        mix(meta, sizeof(meta));
+        FILE * f = std::fopen(paths[i], "rb");
+        if (!f) throw Err{SANA_ERR_IO, std::string("cannot open ") + paths[i]};
+        const size_t got = std::fread(head.data(), 1, head.size(), f);
+        std::fclose(f);
+        mix(head.data(), got);
+    }
+    return h;
+}
+
 template <class F>
 int guarded(F f) {
     try {
@@ -171,6 +198,27 @@ int sana_dit_load_gguf(sana_dit * ctx, const char * model_path, const char * cap
         }
         call(sana_dit_check_weights(ctx));
     });
+}
+
+int sana_dit_load_gguf_cached(sana_dit * ctx, const char * model_path, const char * caption_path,
+                              const char * denoiser_path, const char * cache_path, int * used_cache) {
+    if (used_cache) *used_cache = 0;
+    if (!ctx || !model_path || !caption_path || !denoiser_path || !cache_path) {
+        sana::set_last_error("null argument");
+        return SANA_ERR_INVALID_ARGUMENT;
+    }
+    uint64_t key = 0;
+    const char * const paths[3] = {model_path, caption_path, denoiser_path};
+    int rc = guarded([&] { key = source_key(paths, 3); });
+    if (rc != SANA_OK) return rc;
+    if (sana_dit_load_packed(ctx, cache_path, key) == SANA_OK) {
+        if (used_cache) *used_cache = 1;
+        return SANA_OK;
+    }
+    rc = sana_dit_load_gguf(ctx, model_path, caption_path, denoiser_path);
+    if (rc != SANA_OK) return rc;
+    (void)sana_dit_save_packed(ctx, cache_path, key);  // best effort
+    return SANA_OK;
 }
 
 int sana_gguf_num_tensors(const char * path, int64_t * n) {

@@ -66,6 +66,10 @@ PROTOTYPES = {
                                                      ctypes.c_int]),
     "sana_dit_check_weights": (ctypes.c_int, [_vp]),
     "sana_dit_load_gguf": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
+    "sana_dit_save_packed": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_uint64]),
+    "sana_dit_load_packed": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_uint64]),
+    "sana_dit_load_gguf_cached": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+                                                 ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)]),
     "sana_dit_set_context": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "sana_dit_get_context": (ctypes.c_int, [_vp, _vp]),
     "sana_dit_forward": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp]),
@@ -219,6 +223,19 @@ class Dit:
 
     def load_gguf(self, model, caption, denoiser):
         check(lib().sana_dit_load_gguf(self.h, model.encode(), caption.encode(), denoiser.encode()))
+
+    def save_packed(self, path, key=0):
+        check(lib().sana_dit_save_packed(self.h, path.encode(), key))
+
+    def load_packed(self, path, key=0):
+        check(lib().sana_dit_load_packed(self.h, path.encode(), key))
+
+    def load_gguf_cached(self, model, caption, denoiser, cache):
+        """Returns True when the packed cache was used."""
+        used = ctypes.c_int(0)
+        check(lib().sana_dit_load_gguf_cached(self.h, model.encode(), caption.encode(), denoiser.encode(),
+                                              cache.encode(), ctypes.byref(used)))
+        return bool(used.value)
 
     def set_context(self, data, projected, bias=None):
         data = _f32(data)
