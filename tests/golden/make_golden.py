@@ -4,7 +4,12 @@ Runs oracle/_ref/ref_harness (the reference's src/{tensor,common_ops,
 transformer_ops,transformer,scheduler,torch_rng}.cpp compiled from
 /root/reference by oracle/ref/Makefile) on the seeded synthetic model of
 oracle/model_spec.h and stores, per output tensor, its SHA-256 over the fp32
-bytes, its L2 norm, a strided subsample and (when small) the whole tensor.
+bytes, its L2 norm, a strided subsample and (when small) the whole tensor;
+a tensor too large to store whole also gets a spread subsample: the values
+at flat indices (k * SPREAD_STEP) mod size, k < SPREAD, which (SPREAD_STEP odd,
+prime and coprime with every size here) land on SPREAD distinct indices
+spread over every row and column rather than on one column as a stride
+that divides the row length does.
 Only data goes into the fixtures; nothing of the reference's source does.
 
 Cases (one .npz each):
@@ -70,6 +75,8 @@ CASES = {
 }
 FULL_LIMIT = 70000      # tensors up to this many values are stored whole
 SUBSAMPLE = 4096
+SPREAD = 65536
+SPREAD_STEP = 1000003
 
 
 def weights():
@@ -129,6 +136,11 @@ def main(names):
                 out[tn + "__sub"] = a.reshape(-1)[::stride].copy()
                 if a.size <= FULL_LIMIT:
                     out[tn] = a
+                else:
+                    idx = (np.arange(SPREAD, dtype=np.int64) * SPREAD_STEP) % a.size
+                    assert np.unique(idx).size == SPREAD
+                    out[tn + "__spread_step"] = np.array(SPREAD_STEP)
+                    out[tn + "__spread"] = a.reshape(-1)[idx].copy()
             for ln in res.stdout.splitlines():
                 if ln.endswith("_ms") or "_ms " in ln:
                     k, v = ln.split()[:2]

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from conftest import rel_l2
+from conftest import rel_l2, spread_subsample
 
 pytestmark = pytest.mark.gpu
 
@@ -102,7 +102,8 @@ def test_rejects_bad_input():
 
 def test_full_decoder_vs_reference():
     """Sana 1.0 DC-AE f32c32 decoder, latent 32x32 -> 1024x1024 RGB: the
-    fixture keeps a strided subsample of the reference's image and its L2 norm."""
+    fixture keeps a strided subsample of the reference's image, 65536 values
+    spread over every row and column, and its L2 norm."""
     path = os.path.join(GOLDEN, "vae_full.npz")
     if not os.path.exists(path):
         pytest.skip("vae_full golden not generated")
@@ -124,6 +125,11 @@ def test_full_decoder_vs_reference():
         assert np.isfinite(got).all()
         assert err < TOL
         assert norm_err < TOL
+        sp = spread_subsample(got, fx, "image")
+        if sp is not None:
+            serr = rel_l2(*sp)
+            print(f"full decoder: spread subsample ({sp[1].size} values) rel_l2 {serr:.3e}")
+            assert serr < TOL
     finally:
         dev.close()
 
