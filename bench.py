@@ -250,25 +250,27 @@ def cpu_baseline(quick=False):
                          "the 28-block forward of run_full_denoising_step_with_cfg at 1024 px, batch 2, t=999, "
                          "36x32/16x72 heads, seeded N(0,0.02) weights, 1 thread")
         fwd_ms, cap_ms = v["forward_ms"], v["caption_projection_ms"]
-    # config 3: the reference's loop projects the caption once and runs 20 CFG
-    # forwards (src/transformer.cpp:692-724); the solver update is negligible
-    res["config3_loop_20_steps_ms"] = round(20 * fwd_ms + cap_ms, 1)
-    res["config3_note"] = "extrapolated: 20 x the forward above + one caption projection"
-    # config 5: one block at 16384 tokens (B=1), x 2 batch rows x 28 blocks
-    c5 = _harness("time-block", DIMS["self_heads"], DIMS["cross_heads"], 1, 128, 1, timeout=900)
-    res["config5_block_16384_tokens_ms"] = round(c5["median_block_ms"], 1)
-    res["config5_forward_4096px_ms"] = round(c5["median_block_ms"] * 2 * DIMS["layers"], 1)
-    res["config5_note"] = ("extrapolated: one reference block_forward at B=1, 128x128 latent (16384 tokens), "
-                           "36x32/16x72 heads, L=300 (1 run), x 2 CFG batch rows x 28 blocks; the caption "
-                           "projection is left out (context resident, as the GPU forward_4096px line)")
-    c1 = _harness("time-block", 16, 16, 1, 16, CPU_REPS)
-    res["config1_block_ms"] = round(c1["median_block_ms"], 1)
-    c4 = _harness("time-micro", 64, CPU_REPS, timeout=900)
-    res["config4_linear_attention_ms"] = round(c4["median_linear_attention_ms"], 1)
-    res["config4_mixffn_ms"] = round(c4["median_mixffn_ms"], 1)
-    res["configs_note"] = ("config1: one block_forward, B=1, 16x16 latent (256 tokens), 16x72 self heads as "
-                           f"written, L=300, median of {CPU_REPS}; config4: linear_attention_4d on [2,16,4096,72] "
-                           f"and glumb_conv on [2,1152,64,64], median of {CPU_REPS}")
+    # the 20-step loop at 1024 px: the reference's loop projects the caption
+    # once and runs 20 CFG forwards (src/transformer.cpp:692-724); the solver
+    # update is negligible
+    res["loop_20_steps_1024px_ms"] = round(20 * fwd_ms + cap_ms, 1)
+    res["loop_20_steps_note"] = "extrapolated: 20 x the forward above + one caption projection"
+    # the 4096 px forward: one block at 16384 tokens (B=1), x 2 batch rows x 28 blocks
+    b16k = _harness("time-block", DIMS["self_heads"], DIMS["cross_heads"], 1, 128, 1, timeout=900)
+    res["block_16384_tokens_ms"] = round(b16k["median_block_ms"], 1)
+    res["forward_4096px_ms"] = round(b16k["median_block_ms"] * 2 * DIMS["layers"], 1)
+    res["forward_4096px_note"] = ("extrapolated: one reference block_forward at B=1, 128x128 latent (16384 tokens), "
+                                  "36x32/16x72 heads, L=300 (1 run), x 2 CFG batch rows x 28 blocks; the caption "
+                                  "projection is left out (context resident, as the GPU forward_4096px line)")
+    b256 = _harness("time-block", 16, 16, 1, 16, CPU_REPS)
+    res["block_256_tokens_ms"] = round(b256["median_block_ms"], 1)
+    micro = _harness("time-micro", 64, CPU_REPS, timeout=900)
+    res["linear_attention_4096_tokens_ms"] = round(micro["median_linear_attention_ms"], 1)
+    res["mixffn_4096_tokens_ms"] = round(micro["median_mixffn_ms"], 1)
+    res["block_and_micro_note"] = ("block_256_tokens: one block_forward, B=1, 16x16 latent (256 tokens), 16x72 self "
+                                   f"heads as written, L=300, median of {CPU_REPS}; linear_attention / mixffn "
+                                   "4096 tokens: linear_attention_4d on [2,16,4096,72] and glumb_conv on "
+                                   f"[2,1152,64,64], median of {CPU_REPS}")
     res["wall_s"] = round(time.time() - t0, 1)
     return res
 
