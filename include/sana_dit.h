@@ -138,7 +138,11 @@ int sana_dit_load_gguf_cached(sana_dit * ctx, const char * model_path, const cha
  * (project_caption_context, src/transformer_ops.cpp:64-76) runs on the GPU;
  * projected = 1: data is the context [B, L, hidden].  bias is the additive
  * key mask [B, 1, L] (or NULL).  The cross-attention keys/values of all
- * blocks are computed here once, since they depend only on the context. */
+ * blocks are computed here once, since they depend only on the context.
+ * Uploading a weight they were computed from (the caption projection,
+ * caption_norm, any block's attn2.to_k / attn2.to_v, or a packed image) drops
+ * the conditioning: calls that need it fail with SANA_ERR_STATE until it is
+ * set again.  Other weight uploads keep it. */
 int sana_dit_set_context(sana_dit * ctx, const float * data, int64_t B, int64_t L, int64_t dim, int projected,
                          const float * bias);
 /* Copy the projected context [B, L, hidden] (fp32 before the fp16 operand cast). */
@@ -146,7 +150,8 @@ int sana_dit_get_context(sana_dit * ctx, float * out);
 
 /* The forward of run_full_denoising_step_with_cfg (src/transformer.cpp:627-681):
  * latent [Bl, Cl, H, W] (repeated x2 for CFG), timestep t for every batch row,
- * the context set above (batch 2*Bl) -> noise_pred [2*Bl, Cl, H, W].  H == W. */
+ * the context set above (batch 2*Bl) -> noise_pred [2*Bl, Cl, H, W].  H * W
+ * must be a perfect square (infer_square_side, src/transformer.cpp:18-24). */
 int sana_dit_forward(sana_dit * ctx, const float * latent, int64_t Bl, int64_t H, int64_t W, float t,
                      float * noise_pred);
 /* Same with device pointers, asynchronous on `stream` (NULL = the context's stream). */

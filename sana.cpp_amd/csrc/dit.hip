@@ -165,6 +165,23 @@ void drop_graphs(sana_dit * c) {
     drop_loop_graphs(c);
 }
 
+// A weight upload: the captured graphs go, and so does the conditioning when
+// the weight is one it was computed from (caption projection, caption_norm,
+// cross-attention k / v): the next forward then needs sana_dit_set_context
+// again instead of running on stale cross K/V.
+void weights_changed(sana_dit * c, bool conditioning) {
+    drop_graphs(c);
+    if (conditioning) c->ctx_ready = false;
+}
+
+bool conditioning_weight(const std::string & name) {
+    return name.rfind("caption_projection.", 0) == 0 || name == "caption_norm.weight";
+}
+
+bool conditioning_block_weight(const std::string & suffix) {
+    return suffix.rfind("attn2.to_k.", 0) == 0 || suffix.rfind("attn2.to_v.", 0) == 0;
+}
+
 // Host fp32 -> device fp16 [rows, ld] with zero padding; src is [rows, cols]
 // (or [cols, rows] when transposed).  A value fp16 cannot hold is refused
 // (SANA_ERR_FORMAT naming `tensor`) before anything is copied.
@@ -1074,7 +1091,7 @@ int sana_dit_set_weight(sana_dit * c, const char * name, const float * data, con
             throw_err(SANA_ERR_INVALID_ARGUMENT, "unknown weight name: " + n);
         }
         c->have[n] = 1;
-        drop_graphs(c);
+        weights_changed(c, conditioning_weight(n));
     });
 }
 
@@ -1138,7 +1155,7 @@ int sana_dit_set_block_weight(sana_dit * c, int64_t blk, const char * suffix, co
             throw_err(SANA_ERR_INVALID_ARGUMENT, "unknown block weight suffix: " + s);
         }
         c->have["blk" + std::to_string(blk) + "." + s] = 1;
-        drop_graphs(c);
+        weights_changed(c, conditioning_block_weight(s));
     });
 }
 
@@ -1151,7 +1168,7 @@ int sana_dit_set_weight_f16(sana_dit * c, const char * name, const uint16_t * da
         expect_shape(name, shape, ndim, {o.rows, o.cols});
         upload_f16_bits(*o.dst, data, o.rows, o.cols, o.ld, n, o.row_off, o.total);
         c->have[n] = 1;
-        drop_graphs(c);
+        weights_changed(c, conditioning_weight(n));
     });
 }
 
@@ -1169,7 +1186,7 @@ int sana_dit_set_block_weight_f16(sana_dit * c, int64_t blk, const char * suffix
             expect_shape(suffix, shape, ndim, {o.rows, o.cols});
         upload_f16_bits(*o.dst, data, o.rows, o.cols, o.ld, block_tensor_name(blk, s), o.row_off, o.total);
         c->have["blk" + std::to_string(blk) + "." + s] = 1;
-        drop_graphs(c);
+        weights_changed(c, conditioning_block_weight(s));
     });
 }
 
@@ -1341,7 +1358,7 @@ int sana_dit_load_packed(sana_dit * c, const char * path, uint64_t key) {
                 cur += nm[i];
             }
         }
-        drop_graphs(c);
+        weights_changed(c, true);
         check_ready(c);
     });
 }

@@ -258,6 +258,38 @@ def test_small_forward_nonsquare_latent(small_model):
         d.forward(O.randn((1, 8, 4, 8), 23), 420.0)
 
 
+def test_conditioning_dropped_by_its_weights():
+    """Uploading a weight the conditioning was computed from (cross-attention
+    k / v, caption projection, caption_norm) drops it: the next forward fails
+    with SANA_ERR_STATE until sana_dit_set_context runs again; other weights
+    keep it."""
+    import sana_dit
+    m = O.Model(**SMALL)
+    d = sana_dit.Dit(layers=2, hidden=128, ffn=256, caption_dim=96, latent_channels=8, self_heads=4, cross_heads=2)
+    try:
+        man = sana_dit.manifest(2, 128, 256, 96, 8)
+        for name, shape in man.items():
+            d.set_weight(name, m.get(name, shape))
+        latent = O.randn((1, 8, 8, 8), 51)
+        caption = O.randn((2, 16, 96), 52)
+        d.set_context(caption, projected=False)
+        ref = d.forward(latent, 999.0)
+        for name in ("transformer_blocks.0.ff.conv_point.weight", "transformer_blocks.1.attn1.to_q.weight",
+                     "scale_shift_table"):
+            d.set_weight(name, m.get(name, man[name]))
+            assert np.array_equal(d.forward(latent, 999.0), ref), name
+        for name in ("transformer_blocks.1.attn2.to_k.weight", "transformer_blocks.0.attn2.to_v.bias",
+                     "caption_projection.linear_2.weight", "caption_norm.weight"):
+            d.set_weight(name, m.get(name, man[name]))
+            with pytest.raises(sana_dit.SanaError) as e:
+                d.forward(latent, 999.0)
+            assert e.value.code == sana_dit.SANA_ERR_STATE, name
+            d.set_context(caption, projected=False)
+            assert np.array_equal(d.forward(latent, 999.0), ref), name
+    finally:
+        d.close()
+
+
 def test_small_loop_batch2_vs_oracle(small_model):
     """The fused device loop on a latent batch of 2: CFG combines rows b and
     b + 2 of the noise prediction."""
