@@ -935,7 +935,7 @@ __global__ __launch_bounds__(256) void xattn_kernel(const f16 * __restrict__ q, 
 // head-major (blockIdx.x = head): consecutive workgroup ids go to different
 // XCDs, so each XCD's L2 holds the K/V of H/8 heads instead of all of them.
 //
-// The head's K [keys][KROW] and V^T [dims][VROW] are staged in LDS once and
+// The head's K [keys][dims] and V^T [dims][keys] (XaCfg layouts) are staged in LDS once and
 // shared by the 8 waves; wave w takes query group w & 3 (32 queries) and key
 // half w >> 2.  Scores are computed transposed, S^T = K . Q^T on
 // v_mfma_f32_32x32x16_f16, so each lane holds one query column and the
@@ -965,14 +965,45 @@ __global__ __launch_bounds__(256) void xattn_kernel(const f16 * __restrict__ q, 
 constexpr int kXaQ = 128;  // queries per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int LT, int KS>
+// Two LDS layouts of the staged head, both free of bank conflicts for the
+// 16-lane fragment reads (16 consecutive rows at one 16-byte chunk) and for
+// the staging writes:
+//  * padded (PACK false): K [LP][KS * 16 + 8] and V^T [DP][LP + 8] halves;
+//  * packed (PACK true):  K as 2 KS chunk planes of [LP][8] halves with row r
+//    of plane c in slot r ^ c (a staging write covers one row's chunks, which
+//    then land in distinct bank groups; a fragment read covers 16 rows of one
+//    plane, a permutation of 16 consecutive slots), and V^T [DP][LP] with
+//    chunk c of row r in slot c ^ (r & 15) when a row has a multiple of 16
+//    chunks, else c ^ ((r >> 1) & 7) (the row stride is then 8 chunks mod 16,
+//    so row parity picks the half of the 64 banks).
+// gfx950 allocates LDS per workgroup in 1280-byte granules (128 of them per
+// CU): a 64 x 64 GEMM workgroup's 49152 bytes take 39, leaving 89 = 113920
+// bytes.  The packed head of 300 keys x 72 dims is exactly that (the padded
+// one 120576), so the key-split path's workgroups share CUs with the other CFG
+// branch's 64 x 64 GEMM workgroups: 1024 px forward 5.234 -> 5.047 ms in one
+// process, while a 114080-byte variant (16-byte gaps between the K planes)
+// gained only 0.03 ms.  The online-softmax path keeps the padded layout: its
+// loop re-reads K and V^T for every query block, and the per-lane swizzle
+// there costs VALU work that path has no room for (40.7 -> 73.5 us per
+// 16384-token launch with it), and its 16384-row GEMM neighbours take 64-80 KB.
+template <int LT, int KS, bool PACK = false>
 struct XaCfg {
     static constexpr int LP = LT * 32;              // keys, padded to the score tile
-    static constexpr int KROW = KS * 16 + 8;        // halves per staged K row (72, 88, 104: conflict-free reads)
+    static constexpr int KROW = KS * 16 + 8;        // halves per padded K row (72, 88, 104: conflict-free reads)
+    static constexpr int KCH = KS * 2;              // 16-byte chunks per K row (< 16)
     static constexpr int DT = (KS * 16 + 31) / 32;  // 32-wide output dim tiles
     static constexpr int DP = DT * 32;              // staged V^T rows
-    static constexpr int VROW = LP + 8;             // halves per staged V^T row
-    static constexpr int K_BYTES = LP * KROW * 2;
+    static constexpr int VROW = PACK ? LP : LP + 8; // halves per staged V^T row
+    static constexpr bool V16 = (LP / 8) % 16 == 0;
+    static_assert(!PACK || (LP / 8) % 8 == 0, "V^T swizzle permutes aligned groups of 8 chunks");
+    // V^T slot swizzle of row r (depends on r's low five bits only)
+    static SANA_DEV int vx(int r) { return PACK ? (V16 ? (r & 15) : ((r >> 1) & 7)) : 0; }
+    // offsets in halves of chunk c of K row r and of V^T row r
+    // (packed: k_at(r0 + r, c) = k_at(r, c) + 8 r0 for r0 a multiple of 32)
+    static SANA_DEV int k_at(int r, int c) { return PACK ? (c * LP + (r ^ c)) * 8 : r * KROW + c * 8; }
+    static SANA_DEV int v_at(int r, int c) { return r * VROW + (c ^ vx(r)) * 8; }
+    static constexpr int K_BYTES = (PACK ? KCH * LP * 8 : LP * KROW) * 2;
+    static_assert(!PACK || (KCH <= 16 && LP % 16 == 0), "K row swizzle stays inside a 16-row group");
     static constexpr int V_BYTES = DP * VROW * 2;
     static constexpr int MERGE_BYTES = 4 * (DT * 16 + 2) * 64 * 4;
     static constexpr int STAGE_BYTES = K_BYTES + V_BYTES + LP * 4;
@@ -985,14 +1016,14 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
                                                         const f16 * __restrict__ vt, int64_t ldvt,
                                                         const float * __restrict__ bias, f16 * __restrict__ out,
                                                         int64_t ldo, int N, int L, int D, float scale, int qblocks) {
-    using X = XaCfg<LT, KS>;
+    using X = XaCfg<LT, KS, !FLASH>;
     static_assert(LT % 2 == 0, "key tiles split in two halves");
     static_assert(X::DP <= 128 && X::LP / 8 <= 64, "staging map");
     constexpr int LTH = LT / 2;
-    constexpr int LP = X::LP, KROW = X::KROW, VROW = X::VROW, DT = X::DT, DP = X::DP;
+    constexpr int LP = X::LP, DT = X::DT, DP = X::DP;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    f16 * Ks = reinterpret_cast<f16 *>(smem);                          // [LP][KROW]
-    f16 * Vs = reinterpret_cast<f16 *>(smem + X::K_BYTES);             // [DP][VROW], keys permuted
+    f16 * Ks = reinterpret_cast<f16 *>(smem);                          // K, X::k_at
+    f16 * Vs = reinterpret_cast<f16 *>(smem + X::K_BYTES);             // V^T, keys permuted, X::v_at
     float * bs = reinterpret_cast<float *>(smem + X::K_BYTES + X::V_BYTES);  // [LP] log2-scaled bias, -inf past L
     const int h = blockIdx.x, b = blockIdx.z, H = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -1065,7 +1096,7 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
     if (kc_live) {
 #pragma unroll
         for (int j = 0; j < LT; ++j)
-            *reinterpret_cast<f16x8 *>(Ks + (kr0 + 32 * j) * KROW + kc * 8) = kreg[j];
+            *reinterpret_cast<f16x8 *>(Ks + X::k_at(kr0 + 32 * j, kc)) = kreg[j];
     }
     if (vc_live) {
         // keys 8 vc .. 8 vc + 7: the first four go to positions 16 (vc >> 1) + 4 (vc & 1),
@@ -1082,8 +1113,14 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) w[e] &= km[e];
-            *reinterpret_cast<uint2 *>(Vs + d * VROW + pos) = make_uint2(w[0], w[1]);
-            *reinterpret_cast<uint2 *>(Vs + d * VROW + pos + 8) = make_uint2(w[2], w[3]);
+            if constexpr (!FLASH) {
+                // positions pos and pos + 8: offset pos & 7 of chunks pos >> 3 and (pos >> 3) + 1
+                *reinterpret_cast<uint2 *>(Vs + X::v_at(d, pos >> 3) + (pos & 7)) = make_uint2(w[0], w[1]);
+                *reinterpret_cast<uint2 *>(Vs + X::v_at(d, (pos >> 3) + 1) + (pos & 7)) = make_uint2(w[2], w[3]);
+            } else {
+                *reinterpret_cast<uint2 *>(Vs + d * X::VROW + pos) = make_uint2(w[0], w[1]);
+                *reinterpret_cast<uint2 *>(Vs + d * X::VROW + pos + 8) = make_uint2(w[2], w[3]);
+            }
         }
     }
     __syncthreads();
@@ -1121,7 +1158,7 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
 #pragma unroll
                     for (int t = 0; t < LTH; ++t) {
                         const f16x8 kf =
-                            *reinterpret_cast<const f16x8 *>(Ks + ((tb + t) * 32 + (lane & 31)) * KROW + d0);
+                            *reinterpret_cast<const f16x8 *>(Ks + ((tb + t) * 32 + (lane & 31)) * X::KROW + d0);
                         st[t] = mfma_32x32x16(kf, qf[ks], st[t]);
                     }
                 }
@@ -1184,7 +1221,7 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
 #pragma unroll
                         for (int dt = 0; dt < DT; ++dt) {
                             const f16x8 af =
-                                *reinterpret_cast<const f16x8 *>(Vs + (dt * 32 + (lane & 31)) * VROW + kpos);
+                                *reinterpret_cast<const f16x8 *>(Vs + (dt * 32 + (lane & 31)) * X::VROW + kpos);
                             o[dt] = mfma_32x32x16(af, pf[t][s2], o[dt]);
                         }
                     }
@@ -1226,10 +1263,11 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
         for (int i = 0; i < 16; ++i) st[t][i] = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-        const int d0 = ks * 16 + 8 * hh;
+        // chunk 2 ks + hh of row lane & 31; tile tb + t adds (tb + t) * 32 rows
+        const int kof = X::k_at(lane & 31, 2 * ks + hh);
 #pragma unroll
         for (int t = 0; t < LTH; ++t) {
-            const f16x8 kf = *reinterpret_cast<const f16x8 *>(Ks + ((tb + t) * 32 + (lane & 31)) * KROW + d0);
+            const f16x8 kf = *reinterpret_cast<const f16x8 *>(Ks + kof + (tb + t) * 32 * 8);
             st[t] = mfma_32x32x16(kf, qf[ks], st[t]);
         }
     }
@@ -1279,14 +1317,20 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
+    // this lane's V^T fragment offsets (row lane & 31 of the first dim tile);
+    // row dt * 32 + r swizzles as row r, so tile dt adds dt * 32 rows
+    int vof[LTH][2];
+#pragma unroll
+    for (int t = 0; t < LTH; ++t)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) vof[t][s2] = X::v_at(lane & 31, ((tb + t) * 32 + 16 * s2 + 8 * hh) >> 3);
 #pragma unroll
     for (int t = 0; t < LTH; ++t)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-            const int kpos = (tb + t) * 32 + 16 * s2 + 8 * hh;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                const f16x8 af = *reinterpret_cast<const f16x8 *>(Vs + (dt * 32 + (lane & 31)) * VROW + kpos);
+                const f16x8 af = *reinterpret_cast<const f16x8 *>(Vs + dt * 32 * X::VROW + vof[t][s2]);
                 o[dt] = mfma_32x32x16(af, pf[t][s2], o[dt]);
             }
         }
@@ -1350,7 +1394,7 @@ template <int LT, int KS, bool ONES, bool FLASH>
 hipError_t launch_xattn_lds2(const f16 * q, int64_t ldq, const f16 * k, int64_t ldk, const f16 * vt, int64_t ldvt,
                              const float * bias, f16 * out, int64_t ldo, int B, int N, int L, int H, int D,
                              float scale, hipStream_t s) {
-    using X = XaCfg<LT, KS>;
+    using X = XaCfg<LT, KS, !FLASH>;
     static const bool attr =
         hipFuncSetAttribute(reinterpret_cast<const void *>(&xattn_lds_kernel<LT, KS, ONES, FLASH>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, X::LDS_BYTES) == hipSuccess;
