@@ -22,9 +22,12 @@
 //     distinct 16-byte bank groups (row parity picks the half of the 256-byte
 //     window, (r >> 1) & 7 the group within it): no bank conflicts.  The
 //     slot c ^ (r & 7) conflicts two ways (rows r and r + 8 share a group).
-//   * Epilogue staged through LDS: the wave tiles are written to LDS in row
-//     order, then every thread moves 8 consecutive columns with 16-byte
-//     global accesses.
+//   * Epilogue staged through LDS: the MFMA computes the transposed tile, so
+//     each lane holds runs of 4 consecutive columns of one row and writes
+//     them to LDS as one 16-byte (fp32) or 8-byte (fp16) store; then every
+//     thread moves 8 consecutive columns with 16-byte global accesses.
+//     Outputs that are fp16 only are rounded in registers and staged as fp16
+//     (one pass for every tile shape).
 //
 // The workgroup -> tile map is XCD-aware: gfx950 deals workgroups round-robin
 // to 8 XCDs (each with its own L2), so workgroup id i goes to position
@@ -238,11 +241,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
             bf[buf][j] = *reinterpret_cast<const f16x8 *>(sb + R * 128 + ((ch ^ ((R >> 1) & 7)) << 4));
         }
     };
+    // The MFMA computes the transposed tile, D^T = W_frag * A_frag^T, so that
+    // lane l of wave tile (i, j) holds output row wm*WTM + i*32 + (l & 31) and,
+    // in acc[i][j][4g .. 4g+3], the four consecutive columns
+    // wn*WTN + j*32 + 8g + 4(l >> 5) + 0..3: the epilogue then writes 16-byte
+    // (fp32) or 8-byte (fp16) row runs to LDS instead of single elements.
     auto mfmas = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < G::TM; ++i)
 #pragma unroll
-            for (int j = 0; j < G::TN; ++j) acc[i][j] = mfma_32x32x16(af[buf][i], bf[buf][j], acc[i][j]);
+            for (int j = 0; j < G::TN; ++j) acc[i][j] = mfma_32x32x16(bf[buf][j], af[buf][i], acc[i][j]);
     };
 
     // Residual epilogue inputs (x rows and the gate), loaded before the main loop
@@ -251,11 +259,39 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
     // (8-column chunk, rows) map is the epilogue's.
     constexpr int ECPR = BN / 8, ERSTEP = G::NT / ECPR, ERPT = (G::EPI_ROWS + ERSTEP - 1) / ERSTEP;
     constexpr bool kPrefetch = MODE == kGemmResidual && CONV == 0 && G::EPI_ROWS == BM && ERPT <= 2;
-    float xpre[kPrefetch ? ERPT : 1][8], gpre[kPrefetch ? ERPT : 1][8];
+    float xpre[kPrefetch ? ERPT : 1][8], gpre[kPrefetch ? ERPT : 1][8], bpre[8];
+    // The fp16 epilogue's bias, one column per lane and wave sub-tile (column
+    // wn*WTN + j*32 + (lane & 31)); the epilogue hands each lane the values of
+    // its 4-column runs with lane shuffles.  Loaded here, its latency hides
+    // behind the main loop (loaded in the epilogue it cost 1-2 us per launch).
+    constexpr bool kH16 = MODE == kGemmQKV || (MODE == kGemmStore && ACT != kActGeglu);
+    float bcol[kH16 ? G::TN : 1];
+    if constexpr (kH16) {
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j) {
+            const int c = n0 + wn * G::WTN + j * 32 + (lane & 31);
+            bcol[j] = (p.bias && c < p.N) ? p.bias[c] : 0.0f;
+        }
+    }
     if constexpr (kPrefetch) {
         const int col = n0 + (tid % ECPR) * 8;
         const int nc = min(8, p.N - col);
         const bool act = nc > 0 && tid < ERSTEP * ECPR;
+        // bias of the thread's 8 columns
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bpre[e] = 0.0f;
+        if (act && p.bias) {
+            if (p.vec && nc == 8) {
+                const float4 b0 = *reinterpret_cast<const float4 *>(p.bias + col);
+                const float4 b1 = *reinterpret_cast<const float4 *>(p.bias + col + 4);
+                bpre[0] = b0.x; bpre[1] = b0.y; bpre[2] = b0.z; bpre[3] = b0.w;
+                bpre[4] = b1.x; bpre[5] = b1.y; bpre[6] = b1.z; bpre[7] = b1.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (e < nc) bpre[e] = p.bias[col + e];
+            }
+        }
 #pragma unroll
         for (int k = 0; k < ERPT; ++k) {
             const int row = m0 + tid / ECPR + k * ERSTEP;
@@ -376,6 +412,114 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
     }
 
     // ------------------------------------------------------------ epilogue
+    // fp16 output row of tile row `row`: plain, or inside the bordered grid of a conv output
+    auto orow16 = [&](int row) -> int64_t {
+        if constexpr (CONV != 0) {
+            if (p.out16_pad) {
+                const int hw = p.conv_h * p.conv_w;
+                const int img = row / hw, rem = row - img * hw;
+                const int y = rem / p.conv_w, x = rem - y * p.conv_w;
+                return ((int64_t)img * (p.conv_h + 2) + y + 1) * (p.conv_w + 2) + x + 1;
+            }
+        }
+        return row;
+    };
+    // fp16-only outputs (plain stores with no fp32 copy, and the q|k|v split):
+    // bias, activation and the fp16 rounding are applied to the accumulators in
+    // registers (the same operations, in the same order, as the fp32-staged
+    // path below), the rounded tile is staged in LDS once as fp16 (8-byte row
+    // runs, rows 16-byte aligned), and every thread then issues all of its
+    // 16-byte LDS reads before its 16-byte global stores.  Against the fp32
+    // staging this halves the LDS bytes, needs a single pass for every tile
+    // shape, and keeps several stores in flight per thread.
+    if constexpr (MODE == kGemmQKV || (MODE == kGemmStore && ACT != kActGeglu)) {
+        if (p.vec && !p.out32) {
+            constexpr int LDH = BN + 8;
+            static_assert(BM * LDH * 2 <= G::LDS_BYTES, "fp16 epilogue tile");
+            f16 * ht = reinterpret_cast<f16 *>(smem);
+            __syncthreads();  // every wave is done reading the operand ring
+#pragma unroll
+            for (int j = 0; j < G::TN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int c = wn * G::WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+                    const int col = n0 + c;
+                    float b4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) b4[e] = __shfl(bcol[j], 8 * g + 4 * (lane >> 5) + e, 64);
+                    // q and k sections are ReLU'd (a 4-column run never straddles
+                    // a section: qkv_c is a multiple of 8)
+                    const bool relu = MODE == kGemmQKV && col < 2 * p.qkv_c;
+#pragma unroll
+                    for (int i = 0; i < G::TM; ++i) {
+                        const int row = wm * G::WTM + i * 32 + (lane & 31);
+                        f16x4 h;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float v = acc[i][j][4 * g + e] + b4[e];
+                            if constexpr (ACT == kActSilu) v = silu_fast(v);
+                            if constexpr (ACT == kActGelu) v = gelu_tanh_f(v);
+                            if (relu) v = fmaxf(v, 0.0f);
+                            h[e] = (f16)v;
+                        }
+                        *reinterpret_cast<f16x4 *>(ht + row * LDH + c) = h;
+                    }
+                }
+            __syncthreads();
+            // row-major stores (the whole tile, or the q section of the split)
+            constexpr int HCPR = BN / 8, CHUNKS = BM * HCPR;
+            constexpr int PER = (CHUNKS + G::NT - 1) / G::NT;
+            f16x8 hv[PER];
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int idx = tid + k * G::NT;
+                if (CHUNKS % G::NT == 0 || idx < CHUNKS)
+                    hv[k] = *reinterpret_cast<const f16x8 *>(ht + (idx / HCPR) * LDH + (idx % HCPR) * 8);
+            }
+            f16 * o16 = reinterpret_cast<f16 *>(p.out16);
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int idx = tid + k * G::NT;
+                if (CHUNKS % G::NT != 0 && idx >= CHUNKS) continue;
+                const int row = m0 + idx / HCPR, col = n0 + (idx % HCPR) * 8;
+                if (row >= p.M || col >= p.N) continue;
+                if constexpr (MODE == kGemmQKV) {
+                    if (col >= p.qkv_c) continue;
+                }
+                f16 * dst = o16 + orow16(row) * p.ldo16 + col;
+                if (col + 8 <= p.N) {
+                    *reinterpret_cast<f16x8 *>(dst) = hv[k];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (col + e < p.N) dst[e] = hv[k][e];
+                }
+            }
+            if constexpr (MODE == kGemmQKV) {
+                // k and v sections: items (column, 8-row octet), 32 consecutive
+                // columns of one octet per 32 items; each item leaves as one
+                // 16-byte token run of relu(K)^T or V^T.  Rows of an octet share
+                // a batch (qkv_n % 8 == 0).
+                constexpr int OCT = BM / 8;
+                const int C3 = p.qkv_c;
+                for (int item = tid; item < BN * OCT; item += G::NT) {
+                    const int c32 = item % 32, rest = item / 32;
+                    const int oct = rest % OCT, cl = (rest / OCT) * 32 + c32;
+                    const int col = n0 + cl, row0 = m0 + oct * 8;
+                    if (col >= p.N || row0 >= p.M || col < C3) continue;
+                    const bool is_k = col < 2 * C3;
+                    const int ch = col - (is_k ? C3 : 2 * C3);
+                    f16x8 h;
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) h[jj] = ht[(oct * 8 + jj) * LDH + cl];
+                    const int b = row0 / p.qkv_n, t0 = row0 - b * p.qkv_n;
+                    f16 * dst = reinterpret_cast<f16 *>(is_k ? p.kt16 : p.vt16);
+                    *reinterpret_cast<f16x8 *>(dst + ((int64_t)b * C3 + ch) * p.qkv_n + t0) = h;
+                }
+            }
+            return;
+        }
+    }
     {
         float * ct = reinterpret_cast<float *>(smem);
         constexpr int LDC = BN + G::CPAD;
@@ -392,7 +536,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
         if constexpr (MODE == kGemmQKV) active = active && col < p.qkv_c;  // k / v columns: item loop
         const bool vec8 = p.vec && nc == 8;
         float bv[8];
-        if (!active) {
+        if constexpr (kPrefetch) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bv[e] = bpre[e];
+        } else if (!active) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) bv[e] = 0.0f;
         } else if (MODE == kGemmVT) {  // bias per row, added below
@@ -407,30 +554,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p_in) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) bv[e] = (p.bias && e < nc) ? p.bias[col + e] : 0.0f;
         }
-        // fp16 output row of tile row `row`: plain, or inside the bordered grid of a conv output
-        auto orow16 = [&](int row) -> int64_t {
-            if constexpr (CONV != 0) {
-                if (p.out16_pad) {
-                    const int hw = p.conv_h * p.conv_w;
-                    const int img = row / hw, rem = row - img * hw;
-                    const int y = rem / p.conv_w, x = rem - y * p.conv_w;
-                    return ((int64_t)img * (p.conv_h + 2) + y + 1) * (p.conv_w + 2) + x + 1;
-                }
-            }
-            return row;
-        };
         for (int pass = 0; pass < BM / ER; ++pass) {
             __syncthreads();  // the operand ring (pass 0) or the previous pass's rows are free
             if (ER == BM || wm == pass) {
+                // 16-byte row runs (rows are 16-byte aligned: LDC = BN + 4, BN a multiple of 8)
 #pragma unroll
                 for (int i = 0; i < G::TM; ++i)
 #pragma unroll
                     for (int j = 0; j < G::TN; ++j) {
-                        const int c = wn * G::WTN + j * 32 + (lane & 31);
+                        const int rr = (wm * G::WTM - pass * ER) + i * 32 + (lane & 31);
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int rr = (wm * G::WTM - pass * ER) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                            ct[rr * LDC + c] = acc[i][j][r];
+                        for (int g = 0; g < 4; ++g) {
+                            const int c = wn * G::WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+                            *reinterpret_cast<float4 *>(&ct[rr * LDC + c]) =
+                                make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
                         }
                     }
             }
