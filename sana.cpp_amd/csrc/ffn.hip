@@ -191,6 +191,140 @@ __global__ __launch_bounds__(64) void dwglu_pipe_kernel(const f16 * __restrict__
     }
 }
 
+// LDS-tiled variant for long sequences: a workgroup of 256 threads takes a
+// TH x 32 tile of output tokens and 32 data channels (with the matching 32 gate
+// channels).  The (TH + 2) x 34 input tokens of the tile and its one-token
+// halo are copied into LDS with global_load_lds_dwordx4 (two planes, data and
+// gate, of 64-byte token rows, in chunk order so each wave instruction fills
+// one contiguous KiB), so every input byte is requested once per tile and
+// 44 KB per workgroup are in flight at a time.  Thread (column x, channel
+// quad q) then slides a 3 x 3 window down its column of TH outputs, reading
+// one new input row (3 columns x 8 bytes of data and of gate) from LDS per
+// output; lanes 8 apart read consecutive tokens, so a wave's 8-byte reads
+// cover 256 contiguous bytes (no bank conflicts).  Halo positions outside the
+// grid are loaded from clamped addresses and zeroed in registers.  Taps are
+// summed in (ky, kx) order with zero padding, then the bias, as in
+// dwglu_row_kernel (same per-channel arithmetic, same results).
+#define SANA_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+constexpr int kDwTileW = 32;                          // output tokens per tile row
+constexpr int kDwTileC = 32;                          // data channels per tile
+constexpr int64_t kDwTileMinTokens = 1024;            // tokens per launch from which the tiled kernel is used
+template <int TH>
+struct DwTile {
+    static constexpr int ROWS = TH + 2, COLS = kDwTileW + 2, TOK = ROWS * COLS;
+    static constexpr int CHUNKS = 2 * TOK * (kDwTileC * 2 / 16);  // 16-byte chunks, both planes
+    static constexpr int INSTR = (CHUNKS + 63) / 64;              // wave DMA instructions
+    static constexpr int PLANE = TOK * kDwTileC * 2;              // bytes per plane
+    static constexpr int LDS = INSTR * 1024;                      // the last instruction's tail lanes land past the planes
+};
+
+template <int TH>
+__global__ __launch_bounds__(256) void dwglu_tile_kernel(const f16 * __restrict__ x, int64_t ldx,
+                                                         const float * __restrict__ wt,
+                                                         const float * __restrict__ bias, f16 * __restrict__ out,
+                                                         int64_t ldo, int Hh, int Ww, int F) {
+    using T = DwTile<TH>;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[T::LDS];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2).
+    // Tiles vary fastest, so with a multiple of 8 tiles the channel groups that
+    // share the 128-byte lines of a token (c0 and c0 + 32) run on one XCD; and
+    // XCD x takes a contiguous range of tiles in column-band-major order, so
+    // the tiles above and below one another, which share two halo rows, mostly
+    // run on the same XCD too.
+    const int c0 = blockIdx.y * kDwTileC;
+    const int nty = (Hh + TH - 1) / TH;
+    const int nt = (int)gridDim.x, per = nt / 8, id = (int)blockIdx.x;
+    const int o = id < per * 8 ? (id % 8) * per + id / 8 : id;
+    const int ty0 = (o % nty) * TH, tx0 = (o / nty) * kDwTileW;
+    const int b = blockIdx.z;
+    const f16 * xb = x + (int64_t)b * Hh * Ww * ldx + c0;
+    // 1. staging: chunk g = plane * (TOK * 4) + token * 4 + part -> LDS byte 16 g
+    for (int i = wid; i < T::INSTR; i += 4) {
+        const int g = min(i * 64 + lane, T::CHUNKS - 1);
+        const int plane = g / (T::TOK * 4), within = g - plane * (T::TOK * 4);
+        const int tok = within >> 2, part = within & 3;
+        const int r = tok / T::COLS, cc = tok - r * T::COLS;
+        const int yy = min(max(ty0 + r - 1, 0), Hh - 1), xx = min(max(tx0 + cc - 1, 0), Ww - 1);
+        const f16 * src = xb + ((int64_t)yy * Ww + xx) * ldx + plane * F + part * 8;
+        __builtin_amdgcn_global_load_lds(static_cast<const void *>(src), SANA_LDS(lds + i * 1024), 16, 0, 0);
+    }
+    // weights and bias of this thread's 4 channels (in flight with the staging)
+    const int q = tid & 7, xo = tid >> 3;  // channel quad, output column in the tile
+    const int c = c0 + 4 * q, E = 2 * F;
+    float wd[9][4], wg[9][4];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        const float4 a = *reinterpret_cast<const float4 *>(wt + (int64_t)k * E + c);
+        const float4 g4 = *reinterpret_cast<const float4 *>(wt + (int64_t)k * E + F + c);
+        wd[k][0] = a.x; wd[k][1] = a.y; wd[k][2] = a.z; wd[k][3] = a.w;
+        wg[k][0] = g4.x; wg[k][1] = g4.y; wg[k][2] = g4.z; wg[k][3] = g4.w;
+    }
+    const float4 bdv = *reinterpret_cast<const float4 *>(bias + c);
+    const float4 bgv = *reinterpret_cast<const float4 *>(bias + F + c);
+    const float bd[4] = {bdv.x, bdv.y, bdv.z, bdv.w}, bg[4] = {bgv.x, bgv.y, bgv.z, bgv.w};
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));  // vmcnt(0): this wave's DMA landed
+    __syncthreads();
+
+    // 2. the column's outputs; input column j of the window is tile column xo + j
+    const int ox = tx0 + xo;
+    bool colok[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int ix = ox + j - 1;
+        colok[j] = ix >= 0 && ix < Ww;
+    }
+    const f16 * dp = reinterpret_cast<const f16 *>(lds);
+    const f16 * gp = reinterpret_cast<const f16 *>(lds + T::PLANE);
+    f16x4 vd[3][3], vg[3][3];  // [window row][column]
+    auto load_row = [&](int slot, int r) {  // tile-local input row r (0 .. TH + 1)
+        const int iy = ty0 + r - 1;
+        const bool rok = iy >= 0 && iy < Hh;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int off = ((r * T::COLS + xo + j) * kDwTileC + 4 * q);
+            f16x4 d4 = *reinterpret_cast<const f16x4 *>(dp + off);
+            f16x4 g4 = *reinterpret_cast<const f16x4 *>(gp + off);
+            if (!(rok && colok[j])) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d4[e] = g4[e] = (f16)0.0f;
+            }
+            vd[slot][j] = d4;
+            vg[slot][j] = g4;
+        }
+    };
+    load_row(0, 0);
+    load_row(1, 1);
+#pragma unroll
+    for (int r = 0; r < TH; ++r) {
+        load_row((r + 2) % 3, r + 2);
+        const int oy = ty0 + r;
+        if (oy >= Hh || ox >= Ww) continue;
+        float ad[4], ag[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ad[e] = ag[e] = 0.0f;
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                const int slot = (r + ky) % 3;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ad[e] += (float)vd[slot][kx][e] * wd[ky * 3 + kx][e];
+                    ag[e] += (float)vg[slot][kx][e] * wg[ky * 3 + kx][e];
+                }
+            }
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float d = ad[e] + bd[e];
+            const float gt = ag[e] + bg[e];
+            o[e] = (f16)(d * silu_fast(gt));
+        }
+        *reinterpret_cast<f16x4 *>(out + ((int64_t)(b * Hh + oy) * Ww + ox) * ldo + c) = o;
+    }
+}
+
 // Scalar variant for channel counts that are not a multiple of 8.
 __global__ __launch_bounds__(256) void dwglu_scalar_kernel(const f16 * __restrict__ x, int64_t ldx,
                                                            const float * __restrict__ wt,
@@ -270,7 +404,26 @@ hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const flo
             // 30.1 / 29.7; F = 4096 at 1024 tokens pipe8 10.5 against pipe4
             // 11.7.  F = 2048 at 4096 tokens keeps pipe16 (17.0 against 19.6).
             const bool pow2 = (F & (F - 1)) == 0;
-            if (pow2 && tokens * F >= (int64_t)1 << 24)
+            if (tokens >= kDwTileMinTokens && F % kDwTileC == 0 && !pow2 && F / kDwTileC <= 65535) {
+                // LDS-tiled kernel, 4-row tiles up to 1024 tokens per launch and
+                // 8-row tiles above (alone on the GPU, 2880 channels, inputs cycled
+                // past the last-level cache, us; pipelined kernel in brackets):
+                //   tokens           TH = 4   6      8      10     16
+                //   1024 (32x32)     9.00     12.28  11.77  13.33  13.22   (9.86)
+                //   4096 (64x64)     26.30    27.76  25.65  30.39  29.69   (26.57)
+                //   16384 (128x128)  86.96    80.88  80.21  84.38  91.03   (89.43)
+                auto tile = [&](auto th_tag, const char * name) {
+                    constexpr int TH = decltype(th_tag)::value;
+                    const int64_t tiles = (int64_t)((Hh + TH - 1) / TH) * ((Ww + kDwTileW - 1) / kDwTileW);
+                    if (tiles > 2147483647) return hipErrorInvalidValue;
+                    note_kernel(name);
+                    hipLaunchKernelGGL((dwglu_tile_kernel<TH>), dim3((unsigned)tiles, F / kDwTileC, B), dim3(256), 0,
+                                       s, xx, ldx, wt, bias, oo, ldo, Hh, Ww, F);
+                    return hipSuccess;
+                };
+                e = tokens <= 1024 ? tile(std::integral_constant<int, 4>{}, "dwglu_tile_kernel<4>")
+                                   : tile(std::integral_constant<int, 8>{}, "dwglu_tile_kernel<8>");
+            } else if (pow2 && tokens * F >= (int64_t)1 << 24)
                 e = launch(std::integral_constant<int, 16>{}, "dwglu_row_kernel<16>", std::false_type{});
             else if (tokens <= 1024 && F >= 4096)
                 e = launch(std::integral_constant<int, 8>{}, "dwglu_pipe_kernel<8>", P{});

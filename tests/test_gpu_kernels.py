@@ -274,14 +274,19 @@ def test_cross_attention(L, B, N, Lk, H, D, masked):
 
 @pytest.mark.parametrize("B,S,F", [(2, 32, 2880), (2, 64, 2880), (1, 37, 40), (1, 16, 64), (1, 3, 5), (2, 1, 8),
                                    (1, 6, 16), (1, 7, 24), (2, 37, 40), (1, 115, 24), (1, 128, 16),
-                                   (1, 32, 4096), (1, 64, 4096), (1, 128, 2048)])
+                                   (1, 32, 4096), (1, 64, 4096), (1, 128, 2048),
+                                   (1, 128, 96), (1, 113, 160), (2, 112, 96), (1, 32, 96)])
 def test_dwconv_glu(L, B, S, F):
     # row segments of 4 tokens up to 1024 tokens, 8 below 12288, 16 above:
     # S = 6 and 7 (4), 37 (8) and 115 (16) leave a partial last segment, S = 1
     # and 3 a row shorter than a segment; F = 5 takes the scalar kernel; the
     # VAE's power-of-two channel counts take the 8-segment pipelined kernel
     # (1024 tokens, F = 4096) and the 8-channel row kernel (64x64 x 4096,
-    # 128x128 x 2048)
+    # 128x128 x 2048).  From 1024 tokens per launch, F a multiple of 32 and not
+    # a power of two, the LDS-tiled kernel: 4 x 32 token tiles at 1024 tokens
+    # (32 x 32 x 96), 8 x 32 above; 128 x 128 fills its tiles, 113 x 113 leaves
+    # partial tiles in both directions, and the batches of two (32 x 32, 64 x 64
+    # and 112 x 112 images) check the batch offset
     rng = np.random.default_rng(S + F)
     E = 2 * F
     x = f16(rng.standard_normal((B, S, S, E)))
