@@ -1025,7 +1025,16 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
     f16 * Ks = reinterpret_cast<f16 *>(smem);                          // K, X::k_at
     f16 * Vs = reinterpret_cast<f16 *>(smem + X::K_BYTES);             // V^T, keys permuted, X::v_at
     float * bs = reinterpret_cast<float *>(smem + X::K_BYTES + X::V_BYTES);  // [LP] log2-scaled bias, -inf past L
-    const int h = blockIdx.x, b = blockIdx.z, H = gridDim.x;
+    // (head, query block) from an XCD-aware order: workgroups are dealt
+    // round-robin to the 8 XCDs, so id goes to position (id % 8) * (n / 8) +
+    // id / 8 of the head-major order and each XCD runs a contiguous range of
+    // heads -- the query blocks of a head share its staged K / V in one L2, and
+    // neighbouring heads, whose query and output rows share 128-byte lines
+    // (head_dim 72 is not a multiple of 64), mostly share it too
+    const int H = gridDim.x, b = blockIdx.z;
+    const int nwg = H * (int)gridDim.y, per = nwg / 8, id = (int)blockIdx.x + H * (int)blockIdx.y;
+    const int pos = id < per * 8 ? (id % 8) * per + id / 8 : id;
+    const int h = pos / (int)gridDim.y, qy = pos - h * (int)gridDim.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = w & 3, kh = w >> 2;
     const int hh = lane >> 5;
@@ -1048,9 +1057,9 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
             __builtin_memcpy(&qf[ks], w, 16);
         }
     };
-    const int q0 = blockIdx.y * kXaQ + g * 32;  // key-split path: this wave's query group
+    const int q0 = qy * kXaQ + g * 32;  // key-split path: this wave's query group
     // this wave's first query block (online-softmax path: of the first 256-query block)
-    const int qw0 = FLASH ? (blockIdx.y * qblocks * 8 + w) * 32 : q0;
+    const int qw0 = FLASH ? (qy * qblocks * 8 + w) * 32 : q0;
     load_q(qw0);  // in flight during the K/V staging (rows clamped into range)
 
     // K staging: thread -> chunk kc = tid & 15 (8 dims), rows kr0 + 32 j.  Every
@@ -1132,7 +1141,7 @@ __global__ __launch_bounds__(512) void xattn_lds_kernel(const f16 * __restrict__
         // the waves never synchronise after the staging.
         const float scale2 = scale * kLog2e;
         for (int qb = 0; qb < qblocks; ++qb) {
-            const int qw = ((blockIdx.y * qblocks + qb) * 8 + w) * 32;
+            const int qw = ((qy * qblocks + qb) * 8 + w) * 32;
             if (qw >= N) break;
             // qf holds this block's queries: requested before the staging for
             // the first block, during the previous block's softmax otherwise
