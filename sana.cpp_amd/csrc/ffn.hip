@@ -191,13 +191,18 @@ __global__ __launch_bounds__(64) void dwglu_pipe_kernel(const f16 * __restrict__
     }
 }
 
-// LDS-tiled variant for long sequences: a workgroup of 256 threads takes a
-// TH x 32 tile of output tokens and 32 data channels (with the matching 32 gate
-// channels).  The (TH + 2) x 34 input tokens of the tile and its one-token
-// halo are copied into LDS with global_load_lds_dwordx4 (two planes, data and
-// gate, of 64-byte token rows, in chunk order so each wave instruction fills
-// one contiguous KiB), so every input byte is requested once per tile and
-// 44 KB per workgroup are in flight at a time.  Thread (column x, channel
+#define SANA_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+constexpr int kDwStripW = 32;                // output tokens per strip row
+constexpr int kDwStripC = 32;                // data channels per workgroup
+constexpr int64_t kDwStripMinTokens = 1024;  // tokens per launch from which the strip kernel is used
+
+// LDS-tiled variant for grids too small for tall strips (below): a workgroup
+// of 256 threads takes a TH x 32 tile of output tokens and 32 data channels
+// (with the matching 32 gate channels).  The (TH + 2) x 34 input tokens of the
+// tile and its one-token halo are copied into LDS with global_load_lds_dwordx4
+// (two planes, data and gate, of 64-byte token rows, in chunk order so each
+// wave instruction fills one contiguous KiB) in one go, 26 KB at TH = 4, and
+// one barrier later the tile is computed.  Thread (column x, channel
 // quad q) then slides a 3 x 3 window down its column of TH outputs, reading
 // one new input row (3 columns x 8 bytes of data and of gate) from LDS per
 // output; lanes 8 apart read consecutive tokens, so a wave's 8-byte reads
@@ -205,16 +210,12 @@ __global__ __launch_bounds__(64) void dwglu_pipe_kernel(const f16 * __restrict__
 // grid are loaded from clamped addresses and zeroed in registers.  Taps are
 // summed in (ky, kx) order with zero padding, then the bias, as in
 // dwglu_row_kernel (same per-channel arithmetic, same results).
-#define SANA_LDS(p) ((__attribute__((address_space(3))) void *)(p))
-constexpr int kDwTileW = 32;                          // output tokens per tile row
-constexpr int kDwTileC = 32;                          // data channels per tile
-constexpr int64_t kDwTileMinTokens = 1024;            // tokens per launch from which the tiled kernel is used
 template <int TH>
 struct DwTile {
-    static constexpr int ROWS = TH + 2, COLS = kDwTileW + 2, TOK = ROWS * COLS;
-    static constexpr int CHUNKS = 2 * TOK * (kDwTileC * 2 / 16);  // 16-byte chunks, both planes
+    static constexpr int ROWS = TH + 2, COLS = kDwStripW + 2, TOK = ROWS * COLS;
+    static constexpr int CHUNKS = 2 * TOK * (kDwStripC * 2 / 16);  // 16-byte chunks, both planes
     static constexpr int INSTR = (CHUNKS + 63) / 64;              // wave DMA instructions
-    static constexpr int PLANE = TOK * kDwTileC * 2;              // bytes per plane
+    static constexpr int PLANE = TOK * kDwStripC * 2;              // bytes per plane
     static constexpr int LDS = INSTR * 1024;                      // the last instruction's tail lanes land past the planes
 };
 
@@ -232,11 +233,11 @@ __global__ __launch_bounds__(256) void dwglu_tile_kernel(const f16 * __restrict_
     // XCD x takes a contiguous range of tiles in column-band-major order, so
     // the tiles above and below one another, which share two halo rows, mostly
     // run on the same XCD too.
-    const int c0 = blockIdx.y * kDwTileC;
+    const int c0 = blockIdx.y * kDwStripC;
     const int nty = (Hh + TH - 1) / TH;
     const int nt = (int)gridDim.x, per = nt / 8, id = (int)blockIdx.x;
     const int o = id < per * 8 ? (id % 8) * per + id / 8 : id;
-    const int ty0 = (o % nty) * TH, tx0 = (o / nty) * kDwTileW;
+    const int ty0 = (o % nty) * TH, tx0 = (o / nty) * kDwStripW;
     const int b = blockIdx.z;
     const f16 * xb = x + (int64_t)b * Hh * Ww * ldx + c0;
     // 1. staging: chunk g = plane * (TOK * 4) + token * 4 + part -> LDS byte 16 g
@@ -282,7 +283,7 @@ __global__ __launch_bounds__(256) void dwglu_tile_kernel(const f16 * __restrict_
         const bool rok = iy >= 0 && iy < Hh;
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
-            const int off = ((r * T::COLS + xo + j) * kDwTileC + 4 * q);
+            const int off = ((r * T::COLS + xo + j) * kDwStripC + 4 * q);
             f16x4 d4 = *reinterpret_cast<const f16x4 *>(dp + off);
             f16x4 g4 = *reinterpret_cast<const f16x4 *>(gp + off);
             if (!(rok && colok[j])) {
@@ -322,6 +323,197 @@ __global__ __launch_bounds__(256) void dwglu_tile_kernel(const f16 * __restrict_
             o[e] = (f16)(d * silu_fast(gt));
         }
         *reinterpret_cast<f16x4 *>(out + ((int64_t)(b * Hh + oy) * Ww + ox) * ldo + c) = o;
+    }
+}
+
+// LDS strip variant for long sequences: a workgroup of 256 threads walks a
+// strip of SH x 32 output tokens and 32 data (+ 32 gate) channels down the
+// grid, one output row per step.  Input rows (34 tokens with the halo
+// columns; data and gate planes of 64-byte token rows: 4352 bytes) stream
+// into a ring of kDwStripRing LDS slots by global_load_lds_dwordx4, P rows
+// ahead of the first row a step consumes, so the DMA of later rows is in
+// flight while a row's arithmetic runs and each input row is fetched once per
+// strip (tiles of TH rows fetch their two halo rows again: 10 rows for 8 at
+// TH = 8).  Each wave moves 68 of a row's 272 16-byte chunks (two
+// instructions, the second on 4 lanes), so every wave issues the same two DMA
+// instructions per row and its own vmcnt tracks a row's arrival.  Thread
+// (column x, channel quad q) keeps a 3 x 3 window of 4-channel vectors in
+// registers and reads one new input row (3 columns x 8 bytes of data and of
+// gate) from LDS per step; lanes 8 apart read consecutive tokens, so a wave's
+// 8-byte reads cover 256 contiguous bytes (no bank conflicts).  Halo
+// positions outside the grid are loaded from clamped addresses and zeroed in
+// registers.  Taps are summed in (ky, kx) order with zero padding, then the
+// bias, as in dwglu_row_kernel (same per-channel arithmetic, same results).
+constexpr int kDwStripRow = 2 * (kDwStripW + 2) * kDwStripC * 2;  // bytes per staged input row (both planes)
+constexpr int kDwStripChunks = kDwStripRow / 16;                // 272 chunks: 68 per wave
+constexpr int kDwStripRing = 8;                                 // LDS row slots
+
+// s_waitcnt vmcnt(2 k), k = input rows whose DMA may stay in flight (gfx9
+// encoding, the other counters unconstrained)
+template <int K>
+SANA_DEV void dw_wait_rows() {
+    static_assert(2 * K < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(((2 * K) & 15) | (7 << 4) | (15 << 8) | (((2 * K) >> 4) << 14));
+}
+template <int KMAX>
+SANA_DEV void dw_wait_rows_upto(int k) {
+    if constexpr (KMAX > 0) {
+        if (k >= KMAX) {
+            dw_wait_rows<KMAX>();
+            return;
+        }
+        dw_wait_rows_upto<KMAX - 1>(k);
+    } else {
+        dw_wait_rows<0>();
+    }
+}
+
+template <int SH, int P>
+__global__ __launch_bounds__(256) void dwglu_strip_kernel(const f16 * __restrict__ x, int64_t ldx,
+                                                          const float * __restrict__ wt,
+                                                          const float * __restrict__ bias, f16 * __restrict__ out,
+                                                          int64_t ldo, int Hh, int Ww, int F) {
+    // the prologue's rows 0 .. P - 1 take distinct slots; later, rows j + 2 ..
+    // j + P - 1 are resident or in flight when row j + P is requested into the
+    // slot of row j + P - kDwStripRing, which step j - 1 finished reading
+    static_assert(P >= 3 && P <= kDwStripRing, "prefetch distance against the ring");
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kDwStripRing * kDwStripRow + 3 * 1024];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2).
+    // Strips vary fastest, so with a multiple of 8 strips the channel groups
+    // that share the 128-byte lines of a token (c0 and c0 + 32) run on one XCD;
+    // and XCD x takes a contiguous range of strips in column-band-major order,
+    // so strips above and below one another, which share a halo row, mostly
+    // run on the same XCD too.
+    const int c0 = blockIdx.y * kDwStripC;
+    const int nsy = (Hh + SH - 1) / SH;
+    const int nt = (int)gridDim.x, per = nt / 8, id = (int)blockIdx.x;
+    const int o = id < per * 8 ? (id % 8) * per + id / 8 : id;
+    const int sy0 = (o % nsy) * SH, tx0 = (o / nsy) * kDwStripW;
+    const int b = blockIdx.z;
+    const int nout = min(SH, Hh - sy0), rows = nout + 2;  // output rows; input rows sy0 - 1 .. sy0 + nout
+    const f16 * xb = x + (int64_t)b * Hh * Ww * ldx + c0;
+    // this lane's chunks of an input row: g0 = 68 wid + lane, g1 = g0 + 64 (lanes < 4)
+    auto chunk_off = [&](int g) -> int64_t {
+        const int plane = g / (kDwStripChunks / 2), within = g - plane * (kDwStripChunks / 2);
+        const int tok = within >> 2, part = within & 3;
+        const int xx = min(max(tx0 + tok - 1, 0), Ww - 1);
+        return (int64_t)xx * ldx + plane * F + part * 8;
+    };
+    const int gw = (kDwStripChunks / 4) * wid;
+    const int64_t off0 = chunk_off(gw + lane), off1 = chunk_off(gw + 64 + (lane & 3));
+    auto issue_row = [&](int r) {  // strip-local input row r -> ring slot r % kDwStripRing
+        const int yy = min(max(sy0 + r - 1, 0), Hh - 1);
+        const f16 * rp = xb + (int64_t)yy * Ww * ldx;
+        unsigned char * slot = lds + (r % kDwStripRing) * kDwStripRow + gw * 16;
+        __builtin_amdgcn_global_load_lds(static_cast<const void *>(rp + off0), SANA_LDS(slot), 16, 0, 0);
+        if (lane < 4)
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(rp + off1), SANA_LDS(slot + 1024), 16, 0, 0);
+    };
+    // The workgroup's weights and biases (9 taps x 32 data + 32 gate channels,
+    // then the two bias rows: 160 16-byte chunks) go to LDS by the same DMA,
+    // ahead of the rows: every global access of the kernel is then a DMA or a
+    // store, so the only vmcnt waits are the row waits below (a weight kept in
+    // a VGPR from a global load would make the compiler wait for every
+    // outstanding DMA before its first use in each step).
+    float * wl = reinterpret_cast<float *>(lds + kDwStripRing * kDwStripRow);  // [10][2][32]: taps 0..8, bias
+    if (wid < 3) {
+        const int i = min(wid * 64 + lane, 159);
+        const int k = i >> 4, plane = (i >> 3) & 1, grp = i & 7;
+        const float * src = (k < 9 ? wt + (int64_t)k * (2 * F) : bias) + plane * F + c0 + 4 * grp;
+        __builtin_amdgcn_global_load_lds(static_cast<const void *>(src), SANA_LDS(lds + kDwStripRing * kDwStripRow + wid * 1024), 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < P; ++r)
+        if (r < rows) issue_row(r);
+    const int q = tid & 7, xo = tid >> 3;  // channel quad, output column in the strip
+    const int c = c0 + 4 * q;
+    const int ox = tx0 + xo;
+    bool colok[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int ix = ox + j - 1;
+        colok[j] = ix >= 0 && ix < Ww;
+    }
+    f16x4 vd[3][3], vg[3][3];  // [window row][column]
+    auto load_row = [&](int wslot, int r) {  // strip-local input row r from its ring slot
+        const int iy = sy0 + r - 1;
+        const bool rok = iy >= 0 && iy < Hh;
+        const f16 * dp = reinterpret_cast<const f16 *>(lds + (r % kDwStripRing) * kDwStripRow);
+        const f16 * gp = dp + kDwStripRow / 4;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int off = (xo + j) * kDwStripC + 4 * q;
+            f16x4 d4 = *reinterpret_cast<const f16x4 *>(dp + off);
+            f16x4 g4 = *reinterpret_cast<const f16x4 *>(gp + off);
+            if (!(rok && colok[j])) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d4[e] = g4[e] = (f16)0.0f;
+            }
+            vd[wslot][j] = d4;
+            vg[wslot][j] = g4;
+        }
+    };
+    // rows 0 and 1 have landed (every row requested after them may stay in flight)
+    __builtin_amdgcn_sched_barrier(0);
+    dw_wait_rows_upto<P - 2>(min(P, rows) - 2);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // (read as 16-byte f16x8 words, the type of the row reads: the row waits
+    // above already cover these DMAs, and with that type the compiler adds no
+    // wait of its own for every DMA in flight)
+    float wd[9][4], wg[9][4], bd[4], bg[4];
+    auto wload = [&](int row, float (&dst)[4]) {
+        const f16x8 v = *reinterpret_cast<const f16x8 *>(wl + row * 32 + 4 * q);
+        __builtin_memcpy(dst, &v, 16);
+    };
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        wload(k * 2 + 0, wd[k]);
+        wload(k * 2 + 1, wg[k]);
+    }
+    wload(18, bd);
+    wload(19, bg);
+    load_row(0, 0);
+    load_row(1, 1);
+#pragma unroll
+    for (int j = 0; j < SH; ++j) {
+        if (j >= nout) continue;  // uniform: the last strip of a grid whose height is not a multiple of SH
+        // row j + 2 has landed in every wave, and every LDS read issued before
+        // (the slot the next DMA takes included) has returned
+        __builtin_amdgcn_sched_barrier(0);
+        dw_wait_rows_upto<P - 3>(min(j + P - 1, rows - 1) - (j + 2));
+        __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + P < rows) issue_row(j + P);
+        load_row((j + 2) % 3, j + 2);
+        const int oy = sy0 + j;
+        if (ox < Ww) {
+            float ad[4], ag[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ad[e] = ag[e] = 0.0f;
+#pragma unroll
+            for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx) {
+                    const int slot = (j + ky) % 3;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        ad[e] += (float)vd[slot][kx][e] * wd[ky * 3 + kx][e];
+                        ag[e] += (float)vg[slot][kx][e] * wg[ky * 3 + kx][e];
+                    }
+                }
+            f16x4 ov;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float d = ad[e] + bd[e];
+                const float gt = ag[e] + bg[e];
+                ov[e] = (f16)(d * silu_fast(gt));
+            }
+            *reinterpret_cast<f16x4 *>(out + ((int64_t)(b * Hh + oy) * Ww + ox) * ldo + c) = ov;
+        }
     }
 }
 
@@ -404,25 +596,48 @@ hipError_t dwconv_glu(const half_t * x, int64_t ldx, const float * wt, const flo
             // 30.1 / 29.7; F = 4096 at 1024 tokens pipe8 10.5 against pipe4
             // 11.7.  F = 2048 at 4096 tokens keeps pipe16 (17.0 against 19.6).
             const bool pow2 = (F & (F - 1)) == 0;
-            if (tokens >= kDwTileMinTokens && F % kDwTileC == 0 && !pow2 && F / kDwTileC <= 65535) {
-                // LDS-tiled kernel, 4-row tiles up to 1024 tokens per launch and
-                // 8-row tiles above (alone on the GPU, 2880 channels, inputs cycled
-                // past the last-level cache, us; pipelined kernel in brackets):
-                //   tokens           TH = 4   6      8      10     16
-                //   1024 (32x32)     9.00     12.28  11.77  13.33  13.22   (9.86)
-                //   4096 (64x64)     26.30    27.76  25.65  30.39  29.69   (26.57)
-                //   16384 (128x128)  86.96    80.88  80.21  84.38  91.03   (89.43)
-                auto tile = [&](auto th_tag, const char * name) {
-                    constexpr int TH = decltype(th_tag)::value;
-                    const int64_t tiles = (int64_t)((Hh + TH - 1) / TH) * ((Ww + kDwTileW - 1) / kDwTileW);
-                    if (tiles > 2147483647) return hipErrorInvalidValue;
+            if (tokens >= kDwStripMinTokens && F % kDwStripC == 0 && !pow2 && F / kDwStripC <= 65535) {
+                // LDS strip kernel: the tallest strip (32, 16 or 8 rows) that
+                // still makes >= 720 workgroups, else 4 x 32 tiles staged whole
+                // (alone on the GPU, 2880 channels, inputs cycled past the
+                // last-level cache, us):
+                //   grid      SH,P = 32,5   32,4   16,4   16,5   8,4    4,4     tiles TH = 4 / 8
+                //   32x32            -      -      12.68  -      10.07  8.25    8.92 / 11.77
+                //   64x64            26.93  29.54  21.29  21.57  23.52  26.16   26.30 / 25.69
+                //   128x128          71.26  71.88  75.18  72.57  78.67  86.13   86.96 / 80.15
+                // (64-row strips spill the window registers; a prefetch of 3 rows
+                // is 5-7 % slower than 4-5.)  At 32 x 32, though, the 1024 px
+                // forward with the two CFG branches' launches side by side ran
+                // 4.935 ms with 4-row strips against 4.902 with 4-row tiles in one
+                // process (bit-identical), so grids that small keep the tiles.
+                auto strip = [&](auto sh_tag, auto p_tag, const char * name) {
+                    constexpr int SH = decltype(sh_tag)::value, PF = decltype(p_tag)::value;
+                    const int64_t strips = (int64_t)((Hh + SH - 1) / SH) * ((Ww + kDwStripW - 1) / kDwStripW);
+                    if (strips > 2147483647) return hipErrorInvalidValue;
                     note_kernel(name);
-                    hipLaunchKernelGGL((dwglu_tile_kernel<TH>), dim3((unsigned)tiles, F / kDwTileC, B), dim3(256), 0,
-                                       s, xx, ldx, wt, bias, oo, ldo, Hh, Ww, F);
+                    hipLaunchKernelGGL((dwglu_strip_kernel<SH, PF>), dim3((unsigned)strips, F / kDwStripC, B), dim3(256),
+                                       0, s, xx, ldx, wt, bias, oo, ldo, Hh, Ww, F);
                     return hipSuccess;
                 };
-                e = tokens <= 1024 ? tile(std::integral_constant<int, 4>{}, "dwglu_tile_kernel<4>")
-                                   : tile(std::integral_constant<int, 8>{}, "dwglu_tile_kernel<8>");
+                auto wgs = [&](int sh) {
+                    return (int64_t)((Hh + sh - 1) / sh) * ((Ww + kDwStripW - 1) / kDwStripW) * (F / kDwStripC) * B;
+                };
+                using I4 = std::integral_constant<int, 4>;
+                if (wgs(32) >= 720)
+                    e = strip(std::integral_constant<int, 32>{}, std::integral_constant<int, 5>{},
+                              "dwglu_strip_kernel<32, 5>");
+                else if (wgs(16) >= 720)
+                    e = strip(std::integral_constant<int, 16>{}, I4{}, "dwglu_strip_kernel<16, 4>");
+                else if (wgs(8) >= 720)
+                    e = strip(std::integral_constant<int, 8>{}, I4{}, "dwglu_strip_kernel<8, 4>");
+                else {
+                    const int64_t tiles = (int64_t)((Hh + 3) / 4) * ((Ww + kDwStripW - 1) / kDwStripW);
+                    if (tiles > 2147483647) return hipErrorInvalidValue;
+                    note_kernel("dwglu_tile_kernel<4>");
+                    hipLaunchKernelGGL((dwglu_tile_kernel<4>), dim3((unsigned)tiles, F / kDwStripC, B), dim3(256), 0, s,
+                                       xx, ldx, wt, bias, oo, ldo, Hh, Ww, F);
+                    e = hipSuccess;
+                }
             } else if (pow2 && tokens * F >= (int64_t)1 << 24)
                 e = launch(std::integral_constant<int, 16>{}, "dwglu_row_kernel<16>", std::false_type{});
             else if (tokens <= 1024 && F >= 4096)

@@ -283,23 +283,41 @@ def test_dwconv_glu(L, B, S, F):
     # VAE's power-of-two channel counts take the 8-segment pipelined kernel
     # (1024 tokens, F = 4096) and the 8-channel row kernel (64x64 x 4096,
     # 128x128 x 2048).  From 1024 tokens per launch, F a multiple of 32 and not
-    # a power of two, the LDS-tiled kernel: 4 x 32 token tiles at 1024 tokens
-    # (32 x 32 x 96), 8 x 32 above; 128 x 128 fills its tiles, 113 x 113 leaves
-    # partial tiles in both directions, and the batches of two (32 x 32, 64 x 64
-    # and 112 x 112 images) check the batch offset
-    rng = np.random.default_rng(S + F)
+    # a power of two, the LDS strip kernel, 32 columns wide and as tall (32, 16,
+    # 8 or 4 rows) as still makes 720 workgroups: 64 x 64 x 2880 in a batch of
+    # two takes 32-row strips, 32 x 32 x 2880 in a batch of two 8-row ones;
+    # smaller grids take 4 x 32 tiles staged whole (113 x 113 and 112 x 112
+    # leave partial tiles in both directions)
+    _dwconv_glu_case(L, B, S, S, F)
+
+
+@pytest.mark.parametrize("B,H,W,F", [(1, 64, 100, 2880), (1, 70, 64, 2880), (1, 40, 40, 2880), (1, 41, 33, 2880),
+                                     (1, 70, 40, 96), (1, 96, 20, 96), (1, 40, 70, 96)])
+def test_dwconv_glu_rect(L, B, H, W, F):
+    # rectangular grids through the strip kernel: 32-row strips with a last
+    # column strip of 4 live columns (64 x 100), 16-row strips ending in a strip
+    # of 6 rows (70 x 64), 8-row strips beside a strip of 8 live columns
+    # (40 x 40), and 8-row strips ending in a strip of 1 row (fewer rows than
+    # the DMA runs ahead) beside a strip of 1 live column (41 x 33: whole waves
+    # of the strip only load and never store); and through the 4-row tiles:
+    # partial tiles (70 x 40), a grid narrower than one tile (96 x 20), 40 x 70
+    _dwconv_glu_case(L, B, H, W, F)
+
+
+def _dwconv_glu_case(L, B, H, W, F):
+    rng = np.random.default_rng(H * 1000 + W + F)
     E = 2 * F
-    x = f16(rng.standard_normal((B, S, S, E)))
+    x = f16(rng.standard_normal((B, H, W, E)))
     w = (rng.standard_normal((E, 3, 3)) * 0.3).astype(np.float32)
     bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
     d = O.depthwise3x3(x, w, bias)
     ref = d[..., :F] * (d[..., F:] / (1 + np.exp(-d[..., F:])))
     wt = np.ascontiguousarray(w.reshape(E, 9).T)
     dx, dw, db = dev(x, torch.float16), dev(wt, torch.float32), dev(bias, torch.float32)
-    out = torch.empty((B * S * S, F), device="cuda", dtype=torch.float16)
-    L.check(L.lib().sana_hip_dwconv_glu(dx.data_ptr(), E, dw.data_ptr(), db.data_ptr(), out.data_ptr(), F, B, S, S, F,
+    out = torch.empty((B * H * W, F), device="cuda", dtype=torch.float16)
+    L.check(L.lib().sana_hip_dwconv_glu(dx.data_ptr(), E, dw.data_ptr(), db.data_ptr(), out.data_ptr(), F, B, H, W, F,
                                         stream()))
-    got = host(out).reshape(B, S, S, F)
+    got = host(out).reshape(B, H, W, F)
     assert rel_l2(got, ref) < 1e-3, rel_l2(got, ref)
 
 
