@@ -708,6 +708,118 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_apply32_kernel(const f16 * _
     }
 }
 
+// la_reduce_apply32_kernel: la_reduce_kernel and la_apply32_kernel in one
+// launch for head_dim 32.  Each workgroup first sums the nch chunk partials of
+// its (b, h) in chunk order, scales them by the same 2^k and splits them into
+// the same fp16 hi/lo pair as la_reduce_kernel (so the results are the same
+// bits), but into LDS; then its 8 waves apply the state to `span` tokens as
+// la_apply32_kernel does.  The partials (4.2 KB per chunk) come from L2 for
+// every workgroup of a head, so `span` is large (2048 tokens) to keep the
+// re-reads small next to the q and output bytes.
+__global__ __launch_bounds__(64 * kLfWaves) void la_reduce_apply32_kernel(const f16 * __restrict__ q, int64_t ldq,
+                                                                          const float * __restrict__ part,
+                                                                          const float * __restrict__ pmax, int nch,
+                                                                          f16 * __restrict__ out, int64_t ldo, int N,
+                                                                          int H, int span) {
+    constexpr int KP = 32, NP = 64, E = 33 * 32;
+    __shared__ __attribute__((aligned(16))) f16 sst[2][NP * KP];  // [hi|lo][r][d]
+    __shared__ __attribute__((aligned(16))) f16 ost[kLfWaves][32][32];
+    const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5;
+    const int wspan = span / kLfWaves;  // a multiple of 64
+    const int ta = min(N, blockIdx.x * span + w * wspan), tz = min(N, ta + wspan);
+    const f16 * qbase = q + (int64_t)b * N * ldq + (int64_t)h * 32 + 8 * hh;
+    auto load_q = [&](int t0, f16x8 (&qf)[2]) {
+        const int tq = min(t0 + (lane & 31), N - 1);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            qf[kk] = *reinterpret_cast<const f16x8 *>(qbase + (int64_t)tq * ldq + kk * 16);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[kk][e] = qf[kk][e] > (f16)0.0f ? qf[kk][e] : (f16)0.0f;
+        }
+    };
+    // the first step's queries do not depend on the state
+    f16x8 qa[2], qb[2];
+    if (ta < tz) {
+        load_q(ta, qa);
+        load_q(ta + 32, qb);
+    }
+    // 1. the state, as la_reduce_kernel computes it
+    const float * pmh = pmax + (int64_t)bh * nch;
+    const int kexp = la_state_exponent(la_bound(pmh, nch));
+    const float scale = ldexpf(1.0f, kexp), eps = ldexpf(1e-15f, kexp);
+    for (int e = tid; e < NP * KP; e += 64 * kLfWaves) {
+        const int r = e / KP, d = e - r * KP;
+        float s = 0.0f;
+        if (e < E) {  // rows 0 .. 32 (S, then ksum), d < 32
+            const float * p = part + (int64_t)bh * nch * E + r * 32 + d;
+            int c = 0;
+            for (; c + 8 <= nch; c += 8) {
+                float x[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) x[u] = p[(int64_t)(c + u) * E];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s += x[u];
+            }
+            for (; c < nch; ++c) s += p[(int64_t)c * E];
+        }
+        s *= scale;
+        const f16 hv = (f16)s;
+        sst[0][e] = hv;
+        sst[1][e] = (f16)(s - (float)hv);
+    }
+    __syncthreads();
+    // 2. apply (la_apply32_kernel's loop)
+    const int sb = (lane & 31) * KP + 8 * hh;
+    f16x8 sa[2][2][2];  // [tile][hi|lo][k-step]
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            sa[tile][0][kk] = *reinterpret_cast<const f16x8 *>(&sst[0][sb + tile * 32 * KP + kk * 16]);
+            sa[tile][1][kk] = *reinterpret_cast<const f16x8 *>(&sst[1][sb + tile * 32 * KP + kk * 16]);
+        }
+    auto apply_store = [&](int t0, const f32x16 & o, const f32x16 & dn) {
+        const float rden = 1.0f / (__shfl(dn[0], lane & 31, 64) + eps);
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            f16x4 v4;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v4[u] = (f16)(o[4 * i4 + u] * rden);
+            *reinterpret_cast<f16x4 *>(&ost[w][lane & 31][8 * la_ost_chunk(lane & 31, i4) + 4 * hh]) = v4;
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int tl = half * 16 + (lane >> 2), c8 = (lane & 3) * 8;
+            const f16x8 v8 = *reinterpret_cast<const f16x8 *>(&ost[w][tl][8 * la_ost_chunk(tl, lane & 3)]);
+            const int t = t0 + tl;
+            if (t < tz) *reinterpret_cast<f16x8 *>(out + ((int64_t)b * N + t) * ldo + (int64_t)h * 32 + c8) = v8;
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+    for (int t0 = ta; t0 < tz; t0 += 64) {
+        f32x16 oa, da, ob, db;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oa[i] = da[i] = ob[i] = db[i] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl) {
+                oa = mfma_32x32x16(sa[0][hl][kk], qa[kk], oa);
+                ob = mfma_32x32x16(sa[0][hl][kk], qb[kk], ob);
+                da = mfma_32x32x16(sa[1][hl][kk], qa[kk], da);
+                db = mfma_32x32x16(sa[1][hl][kk], qb[kk], db);
+            }
+        if (t0 + 64 < tz) {
+            load_q(t0 + 64, qa);
+            load_q(t0 + 96, qb);
+        }
+        apply_store(t0, oa, da);
+        if (t0 + 32 < tz) apply_store(t0 + 32, ob, db);
+    }
+}
+
 // la_applyT_kernel: the transposed apply of la_apply32_kernel for other head
 // dims (D % 8 == 0, D + 1 <= 96): O^T[r][t] = [S | ksum] . relu(q)^T with NT
 // 32-row tiles of the reduced hi/lo state as the A operand (rows 0..D-1 S,
@@ -1513,16 +1625,16 @@ hipError_t linear_attention_chunked(const half_t * q, int64_t ldq, const half_t 
     f16 * shi = reinterpret_cast<f16 *>(ws + ((size_t)B * H * E * nch + 3) / 4 * 4);
     f16 * slo = shi + (size_t)B * H * NP * KP;
     float * pmax = reinterpret_cast<float *>(slo + (size_t)B * H * NP * KP);
-    note_kernel("la_chunk_kernel + la_reduce_kernel + la_apply32_kernel");
+    (void)shi;
+    (void)slo;
+    note_kernel("la_chunk_kernel + la_reduce_apply32_kernel");
     hipLaunchKernelGGL(la_chunk_kernel, dim3((unsigned)nch, (unsigned)(B * H)), dim3(64 * kLfWaves), 0, s,
                        reinterpret_cast<const f16 *>(kt), reinterpret_cast<const f16 *>(vt), N, T, nch, part, pmax);
-    hipLaunchKernelGGL(la_reduce_kernel, dim3((NP * KP + 255) / 256, B * H), dim3(256), 0, s, part, pmax, nch, D, NP,
-                       KP, shi, slo);
-    // apply: 8 waves x 64 tokens per workgroup
-    constexpr int kSpan = 64 * kLfWaves;
-    hipLaunchKernelGGL(la_apply32_kernel, dim3((unsigned)((N + kSpan - 1) / kSpan), (unsigned)(B * H)),
-                       dim3(64 * kLfWaves), 0, s, reinterpret_cast<const f16 *>(q), ldq, shi, slo, pmax, nch,
-                       reinterpret_cast<f16 *>(out), ldo, N, H, kSpan);
+    // reduce + apply: 8 waves x kRaSpan / 8 tokens per workgroup
+    constexpr int kRaSpan = 2048;
+    hipLaunchKernelGGL(la_reduce_apply32_kernel, dim3((unsigned)((N + kRaSpan - 1) / kRaSpan), (unsigned)(B * H)),
+                       dim3(64 * kLfWaves), 0, s, reinterpret_cast<const f16 *>(q), ldq, part, pmax, nch,
+                       reinterpret_cast<f16 *>(out), ldo, N, H, kRaSpan);
     return hipGetLastError();
 }
 
