@@ -724,10 +724,16 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_reduce_apply32_kernel(const 
     constexpr int KP = 32, NP = 64, E = 33 * 32;
     __shared__ __attribute__((aligned(16))) f16 sst[2][NP * KP];  // [hi|lo][r][d]
     __shared__ __attribute__((aligned(16))) f16 ost[kLfWaves][32][32];
-    const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+    // XCD-aware order: workgroup ids are dealt round-robin to the 8 XCDs, so id
+    // goes to position (id % 8) * (n / 8) + id / 8 of the head-major order and
+    // the token blocks of one head, which read the same partials, share an L2
+    const int nb = (int)gridDim.x, nwg = nb * (int)gridDim.y, per = nwg / 8;
+    const int id = (int)blockIdx.x + nb * (int)blockIdx.y;
+    const int pos = id < per * 8 ? (id % 8) * per + id / 8 : id;
+    const int bh = pos / nb, blk = pos - bh * nb, b = bh / H, h = bh - b * H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5;
     const int wspan = span / kLfWaves;  // a multiple of 64
-    const int ta = min(N, blockIdx.x * span + w * wspan), tz = min(N, ta + wspan);
+    const int ta = min(N, blk * span + w * wspan), tz = min(N, ta + wspan);
     const f16 * qbase = q + (int64_t)b * N * ldq + (int64_t)h * 32 + 8 * hh;
     auto load_q = [&](int t0, f16x8 (&qf)[2]) {
         const int tq = min(t0 + (lane & 31), N - 1);
