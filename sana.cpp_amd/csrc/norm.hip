@@ -441,24 +441,36 @@ __global__ __launch_bounds__(64 * NW) void final_proj_kernel(const float * __res
             mods[1][c] = e[c] + T[C + c];
         }
     }
-    // 1. statistics (two-pass mean and variance, as final_norm_kernel)
-    for (int r = w; r < 32; r += NW) {
-        const float * xr = x + (int64_t)min(r0 + r, rows - 1) * C;
-        float v[kMaxPerLane];
+    // 1. statistics (two-pass mean and variance, as final_norm_kernel).  Wave w
+    // takes rows w, w + NW, ...: all of them are requested before the first
+    // reduction, so the row loads overlap instead of following one another.
+    constexpr int RW = (32 + NW - 1) / NW;  // rows per wave
+    constexpr int PL = kMaxPerLane;
+    float v[RW][PL];
+#pragma unroll
+    for (int k = 0; k < RW; ++k) {
+        const int r = w + k * NW;
+        const float * xr = x + (int64_t)min(r0 + min(r, 31), rows - 1) * C;
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            const int c = lane + 64 * i;
+            v[k][i] = (r < 32 && c < C) ? xr[c] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < RW; ++k) {
+        const int r = w + k * NW;
+        if (r >= 32) continue;
         float sum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
-            const int c = lane + 64 * i;
-            v[i] = c < C ? xr[c] : 0.0f;
-            sum += v[i];
-        }
+        for (int i = 0; i < PL; ++i) sum += v[k][i];
         const float mean = wave_sum(sum) / (float)C;
         float q = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
+        for (int i = 0; i < PL; ++i) {
             const int c = lane + 64 * i;
             if (c < C) {
-                const float d = v[i] - mean;
+                const float d = v[k][i] - mean;
                 q += d * d;
             }
         }
