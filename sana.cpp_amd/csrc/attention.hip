@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256) void la_apply_kernel(const f16 * __restrict__ 
 //      (8 consecutive tokens per lane: one 16-byte load).
 //   2. The 8 partial states are summed in LDS in wave order (bit-reproducible)
 //      and stored as an fp16 hi/lo pair, 2^k S = hi + lo, k from the sum of
-//      the 8 partials' maxima (the range rule of the three-kernel path).
+//      the 8 partials' maxima (the range rule of the chunked paths).
 //   3. Wave w applies it to its tokens transposed, O^T[r][t] = [S | ksum] .
 //      relu(q)^T, so each lane holds four consecutive head dims of one token
 //      (8-byte stores); the denominator is row 0 of the ksum tile.
@@ -544,14 +544,14 @@ __global__ __launch_bounds__(64 * kLfWaves) void la_fused_kernel(const f16 * __r
     }
 }
 
-// la_chunk_kernel: the chunk partial states of the three-kernel path for
-// head_dim 32, from the kGemmQKV layouts (relu(K)^T and V^T token-contiguous
-// per channel).  One workgroup of 8 waves per (token chunk, b, h): each wave
-// sums its share of the chunk as la_fused_kernel's step 1 does (MFMA operands
+// la_chunk_kernel: the chunk partial states of the chunked path for head_dim
+// 32, from the kGemmQKV layouts (relu(K)^T and V^T token-contiguous per
+// channel).  One workgroup of 8 waves per (token chunk, b, h): each wave sums
+// its share of the chunk as la_fused_kernel's step 1 does (MFMA operands
 // straight from global memory), the 8 partials are added in LDS in wave order
 // and the chunk's (D+1) x D partial is written in la_state_kernel's layout
-// (part[r * D + d] = S[r][d], ksum in row D) with its max |entry|, so
-// la_reduce_kernel and la_apply_kernel follow unchanged.
+// (part[r * D + d] = S[r][d], ksum in row D) with its max |entry|, which
+// la_reduce_apply32_kernel reduces and applies.
 __global__ __launch_bounds__(64 * kLfWaves) void la_chunk_kernel(const f16 * __restrict__ kt,
                                                                  const f16 * __restrict__ vt, int N, int T, int nch,
                                                                  float * __restrict__ part,

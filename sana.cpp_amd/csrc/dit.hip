@@ -279,8 +279,9 @@ void gemm_qkv_split(sana_dit * c, BlockDev & w, int64_t B, int64_t N, const half
 // Whether the self attention runs as kGemmQKV + one fused linear-attention kernel.
 // The fused linear attention rebuilds each head's state in every workgroup
 // that shares the head, which stops paying off on long sequences: at 16384
-// tokens per image the three-kernel path (chunk states, reduction, apply) made
-// the 4096 px forward 2 ms faster (57.9 against 59.9 ms), at 4096 tokens they tie.
+// tokens per image the chunked path (chunk states, then reduction and apply;
+// then three kernels) made the 4096 px forward 2 ms faster (57.9 against
+// 59.9 ms), at 4096 tokens they tie.
 constexpr int64_t kLaFusedMaxTokens = 8192;
 
 bool fused_linear_attention(const sana_dit * c, int64_t N) {
@@ -288,9 +289,9 @@ bool fused_linear_attention(const sana_dit * c, int64_t N) {
 }
 
 // Whether the q | k | v projection writes the kGemmQKV layouts: head_dim 32,
-// for the fused kernel up to kLaFusedMaxTokens and the chunked three-kernel
-// path from relu(K)^T / V^T beyond (at 16384 tokens per branch 55 us against
-// 80 us for the token-major three-kernel path).
+// for the fused kernel up to kLaFusedMaxTokens and the chunked path from
+// relu(K)^T / V^T beyond (at 16384 tokens per branch 55 us against 80 us for
+// the token-major three-kernel path, when both were three kernels).
 bool qkv_split_layout(const sana_dit * c, int64_t N) {
     return sana::linear_attention_fused_ok((int)N, (int)c->Ds) && c->C % 8 == 0;
 }
